@@ -1,0 +1,163 @@
+"""bench.py - decode attention + KV append over a 32K q8_0 cache, 8 layers, on one MI355X.
+
+One step = one decode token: for each of the 8 attention layers, bkv_decode_step appends the token's
+K/V (q8_0 quantise-on-write) and runs GQA attention (16 Q / 4 KV heads, d 256) over the whole cache.
+The cache is prefilled with seeded synthetic K/V (K ~ N(0,1) with 3 channels per (layer, kv head)
+scaled x8, V ~ N(0, 0.5) std, Q ~ N(0,1)) so that the timed steps attend over 32769..32768+K keys
+Inputs are resident in HBM before the timed region.
+
+    python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(n, gated=False):
+    """Compulsory HBM bytes of one layer's decode step over n keys (q8_0 K+V, d 256, 4 KV heads):
+    K/V read 2176 B/key, append write 2176 B, K/V fp32 input 8192 B, Q 16384 B, out 16384 B
+    (+ gate read and gated write 32768 B)."""
+    return 2176 * n + 43136 + (32768 if gated else 0)
+
+
+def gen_cache(cache, n, seed, layers):
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    chunk = 8192
+    for layer in range(layers):
+        ch = torch.stack([torch.randperm(256, generator=g, device="cuda")[:3] for _ in range(4)])
+        scale = torch.ones(4, 256, device="cuda")
+        scale.scatter_(1, ch, 8.0)
+        for s in range(0, n, chunk):
+            e = min(n, s + chunk)
+            k = torch.randn(e - s, 4, 256, generator=g, device="cuda") * scale
+            v = torch.randn(e - s, 4, 256, generator=g, device="cuda") * 0.5
+            cache.append(layer, s, k, v)
+    torch.cuda.synchronize()
+
+
+def cpu_baseline(ctx, seed=2):
+    """The CPU oracle (serial per head row, OpenMP over the 16 rows of a layer) on a bounded sample:
+    one layer's decode step at ctx+1 keys, scaled to 8 layers. Returns the baseline object."""
+    import numpy as np
+    import oracle
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    n = ctx + 1
+    host = oracle.HostCache(n_layers=1, cap=n, k_fmt=oracle.Q8_0, v_fmt=oracle.Q8_0)
+    k, v = oracle.synth_kv(n, 4, 256, seed, 0, outliers=3)
+    host.append(0, 0, k, v)
+    q = oracle.normal(16 * 256, seed, 5).reshape(16, 256)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        host.decode(0, n, q, nthreads=cores)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+            break
+    per_layer = (time.perf_counter() - t0) / reps
+    t1 = time.perf_counter()
+    host.decode_heads(0, n, q, 0, 1)          # one head row single-threaded, x16 rows
+    single = (time.perf_counter() - t1) * 16
+    return {"value": per_layer * 8 * 1e6, "unit": "us/token", "cores": cores, "kind": "port",
+            "sample": f"oracle decode of 1 layer (16 heads) at {n} q8_0 keys, {reps} reps, x8 layers",
+            "single_thread_us_per_token": single * 8 * 1e6,
+            "host_gbs": algorithmic_bytes(n) / per_layer / 1e9}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=48)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gate", action="store_true", help="also read the gate and write GOUT")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the KV path is sharded across GPUs by "
+              "KV head or sequence in design only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from bonsai_vk_amd import BKV_Q8_0, KvCache
+
+    L, K, W, ctx = args.layers, args.steps, args.warmup, args.ctx
+    cap = ctx + K + 1
+    cache = KvCache(n_layers=L, cap=cap, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=cap)
+    prefill = ctx - W                       # warmup appends positions ctx-W .. ctx-1
+    gen_cache(cache, prefill, seed=2, layers=L)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    nstep = W + K
+    knew = torch.randn(nstep, L, 1, 4, 256, generator=g, device="cuda")
+    vnew = torch.randn(nstep, L, 1, 4, 256, generator=g, device="cuda") * 0.5
+    q = torch.randn(nstep, L, 16, 256, generator=g, device="cuda")
+    gate = torch.randn(nstep, L, 16, 256, generator=g, device="cuda") if args.gate else None
+    out = torch.empty(L, 16, 256, device="cuda")
+    og = torch.empty(L, 16, 256, device="cuda") if args.gate else None
+
+    def step(i, ev=None):
+        pos = prefill + i
+        for layer in range(L):
+            if ev is not None:
+                ev[layer][0].record()
+            cache.decode_step(layer, pos, knew[i, layer], vnew[i, layer], q[i, layer],
+                              None if gate is None else gate[i, layer], out[layer],
+                              None if og is None else og[layer])
+            if ev is not None:
+                ev[layer][1].record()
+
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)]
+           for _ in range(K)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(K):
+        step(W + i, evs[i])
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_total = t_start.elapsed_time(t_end)
+    ms_step = ms_total / K
+    call_ms = [evs[i][l][0].elapsed_time(evs[i][l][1]) for i in range(K) for l in range(L)]
+    avg_call_s = sum(call_ms) / len(call_ms) / 1e3
+    ns = [ctx + 1 + i for i in range(K)]
+    bytes_step = sum(L * algorithmic_bytes(n, args.gate) for n in ns) / K
+    achieved = bytes_step / L / avg_call_s / 1e9
+
+    line = {
+        "metric": "us/token decode attn+KV append at 32K ctx (8 layers); achieved HBM GB/s % peak",
+        "value": round(ms_step * 1e3, 3), "unit": "us/token", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(ms_step, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 cache, fp32 accumulate",
+        "data": "synthetic (seeded torch.randn K/V/Q, 3 outlier K channels x8 per layer/head)",
+        "config": {"workload": "bkv_decode_step x 8 layers, q8_0 K+V, keys 32769..32768+steps "
+                               "(BASELINE config 3)", "ctx": ctx, "layers": L, "nh": 16, "nkv": 4,
+                   "hd": 256, "gate": bool(args.gate)},
+        "achieved_gbs_step": round(bytes_step / (ms_step / 1e3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "bkv_decode_step (one layer: qk+pv+merge launches)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_call_us": round(avg_call_s * 1e6, 3)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(ctx)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,39 @@
+"""Build libbkv.so (the gfx950 KV-cache path) in-tree with hipcc.
+
+    python -m bonsai_vk_amd.build        # or bonsai_vk_amd.build.build()
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libbkv.so")
+SOURCES = ["bkv_api.cpp", "bkv_decode.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    # packed fp32 ops stay off: the gfx950 pool has shown silent wrong results from some v_pk_*_f32 forms
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # correctly rounded fp32 divide/sqrt: the q8_0 scale d = amax/127 and id = 1/d must round exactly
+    "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-fast-math", "-ffp-contract=off",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def build(verbose=False):
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    cmd = [HIPCC] + FLAGS + ["-o", LIB + ".tmp"] + srcs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed building libbkv.so")
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,250 @@
+// bkv_api.cpp - the C ABI (include/bkv.h): descriptor validation, partition planning, workspace
+// layout and kernel dispatch. No allocation, no host synchronisation, no exception crosses out.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/bkv.h"
+#include "bkv_internal.h"
+
+namespace bkv {
+
+static thread_local char g_hip_err[256] = "";
+
+static int hip_fail(hipError_t e) {
+  if (e == hipSuccess) return BKV_OK;
+  std::snprintf(g_hip_err, sizeof g_hip_err, "%s: %s", hipGetErrorName(e), hipGetErrorString(e));
+  return BKV_EHIP;
+}
+
+static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+static inline int64_t next_pow2(int64_t x) {
+  int64_t p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Partition sizes: enough workgroups to cover the chip (1024 for QK, 512 for PV at nkv = 4) with at
+// least 16 keys each, never more than kMaxChunk keys (the LDS row).
+DecodePlan plan_decode(int nh, int nkv, int64_t n) {
+  DecodePlan p;
+  p.ch_qk = (int)std::min<int64_t>(kMaxChunk, std::max<int64_t>(16, next_pow2(cdiv(n * nkv, 1024))));
+  p.ch_pv = (int)std::min<int64_t>(kMaxChunk, std::max<int64_t>(16, next_pow2(cdiv(n * nkv, 512))));
+  p.nch_qk = (int)cdiv(n, p.ch_qk);
+  p.nch_pv = (int)cdiv(n, p.ch_pv);
+  p.ld = cdiv(n, 64) * 64;
+  // bounds that grow monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx
+  const int64_t nq_bound = std::max<int64_t>(256, cdiv(n, kMaxChunk));
+  const int64_t np_bound = std::max<int64_t>(128, cdiv(n, kMaxChunk));
+  p.off_score = 0;
+  p.off_stats = align256((size_t)nh * p.ld * sizeof(float));
+  p.off_part = p.off_stats + align256((size_t)nh * nq_bound * sizeof(float2));
+  p.total = p.off_part + align256((size_t)np_bound * nh * kHd * sizeof(float));
+  return p;
+}
+
+static bool aligned16(const void *p) { return p && ((uintptr_t)p & 15u) == 0; }
+
+static uint64_t slot_bytes(const bkv_cache_desc *d, int which) {
+  const int fmt = which < 2 ? d->k_fmt : d->v_fmt;
+  const uint64_t hd = (uint64_t)d->hd, nkv = (uint64_t)d->nkv;
+  switch (which) {
+    case 0: case 2: return fmt == BKV_F16 ? nkv * hd * 2 : nkv * hd;
+    default: return fmt == BKV_F16 ? 0 : nkv * (hd / 32) * 2;
+  }
+}
+
+static int check(const bkv_cache_desc *d) {
+  if (!d) return BKV_EINVAL;
+  if (d->n_layers < 1 || d->nkv < 1 || d->nh < 1 || d->hd < 1 || d->cap < 1) return BKV_EINVAL;
+  if ((d->k_fmt != BKV_F16 && d->k_fmt != BKV_Q8_0) || (d->v_fmt != BKV_F16 && d->v_fmt != BKV_Q8_0))
+    return BKV_EINVAL;
+  // KvGeom::check (runtime_vk/kv_guard.h:103-113)
+  if (d->hd % 4 || d->hd % 32 || (d->hd / 32) % 2) return BKV_ESHAPE;
+  if (d->nh % d->nkv) return BKV_ESHAPE;
+  if (!(std::isfinite(d->scale)) || d->scale <= 0.0f) return BKV_EINVAL;
+  if (d->page_tokens < 0) return BKV_EINVAL;
+  if (d->page_tokens > 0) {
+    if (d->cap % d->page_tokens || d->max_pages < 1 || !d->block_table) return BKV_EINVAL;
+  }
+  if (!d->k_data || !d->v_data) return BKV_EINVAL;
+  if (d->k_fmt == BKV_Q8_0 && !d->k_scales) return BKV_EINVAL;
+  if (d->v_fmt == BKV_Q8_0 && !d->v_scales) return BKV_EINVAL;
+  const void *ptrs[4] = {d->k_data, d->k_scales, d->v_data, d->v_scales};
+  for (int i = 0; i < 4; ++i) {
+    const uint64_t sb = slot_bytes(d, i);
+    if (!sb) continue;
+    if (!aligned16(ptrs[i])) return BKV_EALIGN;
+    if (d->n_layers > 1 && d->layer_stride_bytes[i] < sb * (uint64_t)d->cap) return BKV_EINVAL;
+    if (d->layer_stride_bytes[i] % 16) return BKV_EALIGN;
+  }
+  return BKV_OK;
+}
+
+// shapes the gfx950 kernels are specialised for: hd 256 and 4 query heads per KV head
+static int check_kernels(const bkv_cache_desc *d) {
+  if (d->hd != kHd || d->nh != kGqa * d->nkv) return BKV_EUNSUPPORTED;
+  return BKV_OK;
+}
+
+static int64_t max_positions(const bkv_cache_desc *d) {
+  return d->page_tokens > 0 ? (int64_t)d->max_pages * d->page_tokens : (int64_t)d->cap;
+}
+
+static LayerView view(const bkv_cache_desc *d, int layer) {
+  LayerView L;
+  auto at = [&](void *base, int i) -> const uint8_t * {
+    return base ? (const uint8_t *)base + (uint64_t)layer * d->layer_stride_bytes[i] : nullptr;
+  };
+  L.kd = at(d->k_data, 0);
+  L.ks = at(d->k_scales, 1);
+  L.vd = at(d->v_data, 2);
+  L.vs = at(d->v_scales, 3);
+  L.bt = d->page_tokens > 0 ? d->block_table + (int64_t)layer * d->max_pages : nullptr;
+  L.page = d->page_tokens > 0 ? d->page_tokens : 0;
+  return L;
+}
+
+static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
+                         const float *gate, float *out, float *out_gated, void *ws, size_t ws_bytes,
+                         hipStream_t st, const AppendArgs *fused) {
+  int rc = check(d);
+  if (rc) return rc;
+  if ((rc = check_kernels(d))) return rc;
+  if (layer < 0 || layer >= d->n_layers) return BKV_EINVAL;
+  if (nfill == 0 || (int64_t)nfill > max_positions(d)) return BKV_ECAP;
+  if (!aligned16(q) || !aligned16(out)) return q && out ? BKV_EALIGN : BKV_EINVAL;
+  if ((gate == nullptr) != (out_gated == nullptr)) return BKV_EINVAL;
+  if (!ws) return BKV_EWORKSPACE;
+  if (((uintptr_t)ws & 255u) != 0) return BKV_EALIGN;
+  const DecodePlan p = plan_decode(d->nh, d->nkv, nfill);
+  if (ws_bytes < p.total) return BKV_EWORKSPACE;
+  char *w = (char *)ws;
+  const LayerView L = view(d, layer);
+
+  QkArgs qa{};
+  qa.L = L; qa.nkv = d->nkv; qa.nfill = nfill; qa.chunk = p.ch_qk; qa.nch_qk = p.nch_qk;
+  qa.ld = p.ld; qa.scale = d->scale; qa.q = q;
+  qa.score = (float *)(w + p.off_score);
+  qa.stats = (float2 *)(w + p.off_stats);
+  if (fused) qa.ap = *fused;
+  PvArgs pa{};
+  pa.L = L; pa.nkv = d->nkv; pa.nh = d->nh; pa.nfill = nfill; pa.chunk = p.ch_pv;
+  pa.nch_pv = p.nch_pv; pa.nch_qk = p.nch_qk; pa.ld = p.ld; pa.scale = d->scale;
+  pa.score = qa.score; pa.stats = qa.stats; pa.part = (float *)(w + p.off_part);
+  RedArgs ra{};
+  ra.nh = d->nh; ra.nch_pv = p.nch_pv; ra.part = pa.part; ra.gate = gate; ra.out = out;
+  ra.out_gated = out_gated;
+  return hip_fail(launch_decode(qa, pa, ra, d->k_fmt, d->v_fmt, fused != nullptr, st));
+}
+
+}  // namespace bkv
+
+using namespace bkv;
+
+extern "C" {
+
+int bkv_geom_check(const bkv_cache_desc *d) { return check(d); }
+
+uint64_t bkv_slot_bytes(const bkv_cache_desc *d, int which) {
+  if (!d || which < 0 || which > 3) return 0;
+  return slot_bytes(d, which);
+}
+
+int64_t bkv_max_positions(const bkv_cache_desc *d) {
+  if (check(d)) return 0;
+  return max_positions(d);
+}
+
+int bkv_kv_append(const bkv_cache_desc *d, int layer, uint32_t pos, int n_tok, const float *k,
+                  const float *v, hipStream_t stream) {
+  int rc = check(d);
+  if (rc) return rc;
+  if ((rc = check_kernels(d))) return rc;
+  if (layer < 0 || layer >= d->n_layers || n_tok < 0) return BKV_EINVAL;
+  if (n_tok == 0) return BKV_OK;
+  if ((int64_t)pos + n_tok > max_positions(d)) return BKV_ECAP;
+  if (!k || !v) return BKV_EINVAL;
+  if (!aligned16(k) || !aligned16(v)) return BKV_EALIGN;
+  AppendArgs a{};
+  a.L = view(d, layer);
+  a.nkv = d->nkv;
+  a.pos = pos;
+  a.k = k;
+  a.v = v;
+  return hip_fail(launch_append(a, d->k_fmt, d->v_fmt, n_tok, stream));
+}
+
+int bkv_attn_decode(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
+                    const float *gate, float *out, float *out_gated, void *workspace,
+                    size_t ws_bytes, hipStream_t stream) {
+  return decode_common(d, layer, nfill, q, gate, out, out_gated, workspace, ws_bytes, stream,
+                       nullptr);
+}
+
+int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
+                    const float *v, const float *q, const float *gate, float *out,
+                    float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  int rc = check(d);
+  if (rc) return rc;
+  if (layer < 0 || layer >= d->n_layers) return BKV_EINVAL;
+  if ((int64_t)pos + 1 > max_positions(d)) return BKV_ECAP;
+  if (!k || !v) return BKV_EINVAL;
+  if (!aligned16(k) || !aligned16(v)) return BKV_EALIGN;
+  AppendArgs a{};
+  a.L = view(d, layer);
+  a.nkv = d->nkv;
+  a.pos = pos;
+  a.k = k;
+  a.v = v;
+  return decode_common(d, layer, pos + 1, q, gate, out, out_gated, workspace, ws_bytes, stream, &a);
+}
+
+int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                           const float *q, const float *gate, float *out, float *out_gated,
+                           void *workspace, size_t ws_bytes, hipStream_t stream) {
+  int rc = check(d);
+  if (rc) return rc;
+  if ((rc = check_kernels(d))) return rc;
+  if (n_q < 0 || n_q > BKV_PREFILL_MAX_Q) return BKV_EINVAL;
+  if (n_q == 0) return BKV_OK;
+  if ((int64_t)pos0 + n_q > max_positions(d)) return BKV_ECAP;
+  const size_t rs = (size_t)d->nh * d->hd;
+  for (int i = 0; i < n_q; ++i) {
+    rc = decode_common(d, layer, pos0 + (uint32_t)i + 1u, q + i * rs, gate ? gate + i * rs : nullptr,
+                       out + i * rs, out_gated ? out_gated + i * rs : nullptr, workspace, ws_bytes,
+                       stream, nullptr);
+    if (rc) return rc;
+  }
+  return BKV_OK;
+}
+
+size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
+  if (check(d) || max_ctx == 0) return 0;
+  if (op != BKV_OP_DECODE && op != BKV_OP_PREFILL) return 0;
+  return plan_decode(d->nh, d->nkv, max_ctx).total;
+}
+
+const char *bkv_strerror(int err) {
+  switch (err) {
+    case BKV_OK: return "ok";
+    case BKV_EINVAL: return "invalid argument";
+    case BKV_ESHAPE: return "cache geometry rule broken (hd%4, hd%32, hd/32 even, nh%nkv)";
+    case BKV_ECAP: return "position outside the cache (pos >= cap) or empty context";
+    case BKV_EALIGN: return "pointer or stride not aligned (16 B; workspace 256 B)";
+    case BKV_EWORKSPACE: return "workspace missing or smaller than bkv_workspace_bytes()";
+    case BKV_EHIP: return "HIP runtime error (see bkv_last_hip_error)";
+    case BKV_EUNSUPPORTED: return "shape not supported by the gfx950 kernels (hd 256, nh = 4*nkv)";
+    default: return "unknown error";
+  }
+}
+
+const char *bkv_last_hip_error(void) { return g_hip_err; }
+
+const char *bkv_version(void) { return "bkv 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// bkv_common.h - device helpers shared by the gfx950 KV-cache kernels: fp16 rounding, q8_0 block
+// arithmetic, wave64 DPP reductions and cache addressing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bkv.h"
+
+namespace bkv {
+
+constexpr int kHd = 256;        // head_dim the kernels are specialised for
+constexpr int kGqa = 4;         // query heads per KV head served from one K/V tile read
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ fp16
+// f32 -> binary16 bits, round to nearest even, with the reference packer's special cases
+// (runtime_vk/shaders/f16_rne.glslh:24-55): any NaN -> sign|0x7E00. v_cvt_f16_f32 rounds to nearest
+// even and keeps fp16 subnormals on gfx950, so only the NaN pattern needs the fix-up.
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+  const uint32_t hw = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  const uint32_t x = __float_as_uint(f);
+  const bool nan = (x & 0x7FFFFFFFu) > 0x7F800000u;
+  return nan ? (((x >> 16) & 0x8000u) | 0x7E00u) : hw;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// value of f32 rounded through fp16 (RNE), as fp32
+__device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)f; }
+
+// ------------------------------------------------------------------ q8_0 (attn_norm_rope2.comp:102-115)
+__device__ __forceinline__ float q8_scale(float amax) { return amax > 1e-35f ? amax / 127.0f : 0.0f; }
+__device__ __forceinline__ float q8_iscale(float amax) {
+  const float d = q8_scale(amax);
+  return d != 0.0f ? 1.0f / d : 0.0f;
+}
+template <bool RHAZ>
+__device__ __forceinline__ uint32_t q8_byte(float x, float id) {
+  const float t = x * id;
+  float r = RHAZ ? roundf(t) : __builtin_rintf(t);
+  r = (r != r) ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
+  return (uint32_t)((int)r) & 0xFFu;
+}
+
+// sign-extended byte k (0..3) of a word, as float
+__device__ __forceinline__ float sbyte(uint32_t w, int k) {
+  return (float)(int)(int8_t)(uint8_t)(w >> (8 * k));
+}
+
+// ------------------------------------------------------------------ DPP reductions inside a row of 16
+// quad_perm(1,0,3,2) = 0xB1, quad_perm(2,3,0,1) = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+// sum over the 16 lanes of a DPP row; every lane of the row receives the total
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+// full-wave reductions (all 64 lanes receive the result)
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// ------------------------------------------------------------------ addressing
+struct LayerView {
+  const uint8_t *kd, *ks, *vd, *vs;   // this layer's arrays (scales may be null)
+  const int32_t *bt;                  // this layer's block-table row, or null (contiguous)
+  int page;                           // tokens per page (paged) or 0
+};
+
+__device__ __forceinline__ int64_t slot_of(const LayerView &L, int64_t pos) {
+  if (L.page == 0) return pos;
+  const int64_t pg = pos / L.page;
+  return (int64_t)L.bt[pg] * L.page + (pos - pg * L.page);
+}
+
+// bytes of one head row of the data array, per format
+__host__ __device__ constexpr int row_bytes(int fmt) { return fmt == BKV_F16 ? kHd * 2 : kHd; }
+// bytes of one head row of the scale array (q8_0 only)
+constexpr int kScaleRowBytes = kHd / 32 * 2;   // 8 fp16 = 16 B
+
+}  // namespace bkv

@@ -1,0 +1,137 @@
+/* bkv.h - C ABI of the MI355X (gfx950) KV-cache path: quantise-on-write KV append, the gather over
+ * cached keys/values, and GQA softmax attention (decode and chunked prefill).
+ *
+ * Every entry point takes plain pointers and sizes. Device pointers are caller-owned memory
+ * (hipMalloc or any allocator); the library never allocates on these paths. Calls are
+ * stream-ordered: they enqueue work on `stream` and return without a host synchronisation. Calls on
+ * one cache are thread-compatible, not thread-safe. No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (hiyoing/bonsai-vk, paths relative to its root):
+ *  - bkv_kv_append        <- the K/V branch of shaders/attn_norm_rope2.comp:167-217, dispatched from
+ *                            runtime_vk/bonsai_forward.h:609-612 (attn_block). K/V arrive post-RoPE.
+ *  - bkv_attn_decode      <- the QK-softmax row kernel + PV(+gate) kernel pair dispatched at
+ *                            runtime_vk/bonsai_forward.h:622-633 (attn_qk_softmax*.comp,
+ *                            attn_pv{,_q8v,_q8v_gqa}.comp); CPU twin runtime_vk/attn_vk.h:156-212.
+ *  - bkv_attn_prefill_chunk <- the prefill loop of one decode step per prompt token
+ *                            (runtime_vk/bonsai_forward.h:2752-2759); same result per query row.
+ *  - bkv_decode_step      <- the append + QK + PV sequence of one attention layer at one position
+ *                            (runtime_vk/bonsai_forward.h:603-633), fused into fewer launches.
+ *  - bkv_geom_check       <- KvGeom::check / compute (runtime_vk/kv_guard.h:94-150).
+ */
+#ifndef BKV_H
+#define BKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers (same definition as hip_runtime_api.h). */
+typedef struct ihipStream_t *hipStream_t;
+
+/* ------------------------------------------------------------------ formats and errors */
+enum bkv_fmt {
+  BKV_F16  = 0,   /* [slot][nkv][hd/2] u32, element 2w in the low half of word w (RNE packed)  */
+  BKV_Q8_0 = 1    /* data [slot][nkv][hd/4] u32 (element e = byte e%4 of word e/4, int8) plus   */
+                  /* scales [slot][nkv][hd/64] u32 (fp16 scale of block 2i low, 2i+1 high)      */
+};
+
+enum bkv_err {
+  BKV_OK          = 0,
+  BKV_EINVAL      = -1,  /* a NULL pointer or a field out of range                             */
+  BKV_ESHAPE      = -2,  /* geometry rule broken: hd%32, (hd/32) odd, nh%nkv, hd>256 ...         */
+  BKV_ECAP        = -3,  /* position >= cap (the KvGuard REFUSE case), or nfill == 0            */
+  BKV_EALIGN      = -4,  /* a device pointer not 16-byte aligned                                */
+  BKV_EWORKSPACE  = -5,  /* workspace NULL or smaller than bkv_workspace_bytes()                */
+  BKV_EHIP        = -6,  /* the HIP runtime reported an error on launch                         */
+  BKV_EUNSUPPORTED = -7  /* a valid request this build does not implement                       */
+};
+
+/* bkv_workspace_bytes() op codes */
+enum bkv_op { BKV_OP_DECODE = 0, BKV_OP_PREFILL = 1 };
+
+/* ------------------------------------------------------------------ the cache descriptor
+ * One descriptor covers the attention layers of one model. Per layer there are four arrays (K data,
+ * K scales, V data, V scales); scales are NULL for an fp16 tensor. Layer l's array starts at
+ * base + l * layer_stride_bytes[i]. Slot s of an array holds one position of all nkv heads, in the
+ * per-format layout of enum bkv_fmt - the reference arena layout (runtime_vk/kv_guard.h:118-130,
+ * runtime_vk/bonsai_forward.h:1940-1973) when page_tokens == 0.
+ *
+ * Contiguous (page_tokens == 0): position p lives in slot p, 0 <= p < cap.
+ * Paged (page_tokens > 0): the pool has cap slots (cap % page_tokens == 0); position p lives in slot
+ *   block_table[layer * max_pages + p / page_tokens] * page_tokens + p % page_tokens,
+ *   and positions run up to max_pages * page_tokens. block_table is device memory.              */
+typedef struct bkv_cache_desc {
+  int32_t n_layers, nh, nkv, hd;   /* 8, 16, 4, 256 for the reference model                      */
+  int32_t cap;                     /* slots per layer (contiguous) or pool slots (paged)          */
+  int32_t k_fmt, v_fmt;            /* enum bkv_fmt                                                */
+  int32_t page_tokens;             /* 0 = contiguous                                              */
+  int32_t max_pages;               /* block-table row length (paged only)                         */
+  float   scale;                   /* softmax scale applied to the raw dot, 1/sqrt(hd) = 0.0625   */
+  void *k_data, *k_scales, *v_data, *v_scales;
+  uint64_t layer_stride_bytes[4];  /* k_data, k_scales, v_data, v_scales                          */
+  const int32_t *block_table;      /* [n_layers][max_pages] physical page ids, NULL if contiguous */
+} bkv_cache_desc;
+
+/* Validate a descriptor (no device access). Returns BKV_OK or the first rule broken. */
+int bkv_geom_check(const bkv_cache_desc *d);
+
+/* Bytes per slot per layer of each array, as KvGeom::compute derives them (kv_guard.h:118-130). */
+uint64_t bkv_slot_bytes(const bkv_cache_desc *d, int which /* 0 k_data 1 k_scales 2 v_data 3 v_scales */);
+
+/* Largest position count a call can attend over: cap, or max_pages * page_tokens when paged. */
+int64_t bkv_max_positions(const bkv_cache_desc *d);
+
+/* ------------------------------------------------------------------ the path
+ * kv_append: write n_tok consecutive positions pos, pos+1, ... of `layer`.
+ *   k, v: device fp32 [n_tok][nkv][hd] (post-RoPE K, raw V). fp16 tensors are RNE packed; q8_0
+ *   tensors are quantised on write (per 32-block: d = amax/127 if amax > 1e-35 else 0,
+ *   id = 1/d, q = clamp(rne(x*id), -127, 127), scale stored as RNE fp16 of d).                  */
+int bkv_kv_append(const bkv_cache_desc *d, int layer, uint32_t pos, int n_tok,
+                  const float *k, const float *v, hipStream_t stream);
+
+/* attn_decode: one query token attending over positions [0, nfill) of `layer`.
+ *   q: device fp32 [nh][hd], rounded RNE to fp16 before the dot (the reference's Q16 operand).
+ *   out: device fp32 [nh][hd] attention result (the reference's PGATE).
+ *   gate/out_gated: optional (both NULL or both set): out_gated = out * 1/(1+exp(-gate)).
+ *   Semantics per head row: score = q16 . k, v = score*scale, p = exp(v - max)/sum, p rounded to
+ *   fp16, out = sum_j p16_j * V_j (q8_0 V reconstructed as f16(scale)*int8).                   */
+int bkv_attn_decode(const bkv_cache_desc *d, int layer, uint32_t nfill,
+                    const float *q, const float *gate, float *out, float *out_gated,
+                    void *workspace, size_t ws_bytes, hipStream_t stream);
+
+/* decode_step: kv_append of one token at `pos` followed by attn_decode with nfill = pos+1, with the
+ * append fused into the attention launch.                                                      */
+int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos,
+                    const float *k, const float *v, const float *q, const float *gate,
+                    float *out, float *out_gated, void *workspace, size_t ws_bytes,
+                    hipStream_t stream);
+
+/* attn_prefill_chunk: n_q query tokens at positions pos0 .. pos0+n_q-1 (already appended), each
+ * attending causally over [0, pos0+i]. q: [n_q][nh][hd] fp32, out/out_gated/gate: [n_q][nh][hd].
+ * Row i equals attn_decode(nfill = pos0+i+1) on the same cache (to the stated tolerance).       */
+int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                           const float *q, const float *gate, float *out, float *out_gated,
+                           void *workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Workspace needed by op (enum bkv_op) for contexts up to max_ctx positions (prefill: max_ctx is
+ * pos0 + n_q, the chunk is bounded by BKV_PREFILL_MAX_Q). Returns 0 on a bad descriptor.      */
+size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx);
+
+/* Human-readable text of an enum bkv_err value (static storage). */
+const char *bkv_strerror(int err);
+
+/* Text of the last HIP error seen by this thread (empty if none). */
+const char *bkv_last_hip_error(void);
+
+/* Library version string. */
+const char *bkv_version(void);
+
+#define BKV_PREFILL_MAX_Q 4096
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BKV_H */

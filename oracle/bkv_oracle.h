@@ -1,0 +1,106 @@
+/* bkv_oracle.h - CPU oracle of the KV-cache path. TEST INFRASTRUCTURE ONLY: it is the checker the
+ * parity tests, smoke() and bench.py's cpu_baseline leg compare the HIP path against, and is never
+ * linked into or called by the product library.
+ *
+ * It restates, in plain C and in the reference's exact operation order, the arithmetic of
+ * hiyoing/bonsai-vk's KV path (paths relative to the reference root):
+ *   fp16 pack/unpack ........ runtime_vk/f16_rne_host.h:27-53 (f32_to_f16_bits),
+ *                             runtime_vk/ptq_decode.h:47-77 (f16_to_f32)
+ *   q8_0 quantise-on-write .. runtime_vk/shaders/attn_norm_rope2.comp:102-115 (q8_scale/q8_iscale/
+ *                             q8_byte), :184-217 (block absmax, data and scale words)
+ *   fp16 K/V append ......... runtime_vk/shaders/attn_norm_rope2.comp:167-181
+ *   score/softmax/P16/PV .... runtime_vk/attn_vk.h:156-212 and :261-311 (attn_forward<true>)
+ *   fp64 ideal leg .......... runtime_vk/attn_vk.h:320-387 (attn_forward_ideal)
+ *   q8_0 reconstruction ..... runtime_vk/bonsai_forward.h:1404-1488 (kv_dump)
+ *   arena layout ............ runtime_vk/kv_guard.h:94-150, runtime_vk/bonsai_forward.h:1940-1973
+ *
+ * Parity pins (what checks each function; see tests/test_oracle_*.py):
+ *   bko_f16_to_f32 ... exhaustive over 2^16 patterns against numpy float16 (IEEE binary16).
+ *   bko_f32_to_f16 ... every f32 exponent class, ties and carries against numpy's RNE cast, and the
+ *                      reference's own packer compiled from its sources (oracle/_ref, when built).
+ *   bko_q8_block ..... invariants (|q|<=127, max|q|==127 per live block, d_half = f16(amax/127),
+ *                      dead blocks), brute force over tiny blocks, and the reference's dumped q8_0 V
+ *                      (runs/kv_q8_0_v4.tsv) re-derived from the fp16 V of the same run.
+ *   bko_attn_decode .. the reference's attn_score_row/attn_softmax_row/attn_pv_row/attn_gate_row
+ *                      compiled from runtime_vk/attn_vk.h (bit-exact, fp16 cache), plus closed forms:
+ *                      one key -> p = 1, identical keys -> uniform p, GQA-identical scores.
+ *   bko_attn_decode_ideal ... numpy float64 recomputation in tests.
+ */
+#ifndef BKV_ORACLE_H
+#define BKV_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/bkv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 */
+uint16_t bko_f32_to_f16(float f);
+float bko_f16_to_f32(uint16_t h);
+void bko_f32_to_f16_array(const float *x, uint16_t *h, size_t n);
+void bko_f16_to_f32_array(const uint16_t *h, float *x, size_t n);
+
+/* one q8_0 block of 32 values -> 32 bytes (int8 as uint8) + fp16 scale bits.
+ * rhaz = 0: ties round half to even (the contract); rhaz = 1: half away from zero (ggml roundf). */
+void bko_q8_block(const float *x, int rhaz, uint8_t *q, uint16_t *scale_bits);
+
+/* number of exact .5 ties (x*id == k + 0.5) met while quantising one block (tie census) */
+int bko_q8_block_ties(const float *x);
+
+/* physical slot of logical position pos (desc pointers are HOST pointers here) */
+int64_t bko_slot(const bkv_cache_desc *d, int layer, int64_t pos);
+
+/* append n_tok tokens: k, v host fp32 [n_tok][nkv][hd] */
+void bko_kv_append(const bkv_cache_desc *d, int layer, uint32_t pos, int n_tok,
+                   const float *k, const float *v, int rhaz);
+
+/* reconstruct one cached row (K if which == 0, V if which == 1) as fp32 [hd] */
+void bko_load_row(const bkv_cache_desc *d, int which, int layer, int64_t pos, int head, float *out);
+
+/* serial mirror of one decode step over positions [0, nfill).
+ * q [nh][hd] fp32; gate may be NULL (then out_gated is not written).
+ * dbg_score / dbg_prob (fp32 [nh][nfill]) and dbg_p16 (u16 [nh][nfill]) may be NULL.
+ * nthreads > 1 runs the independent head rows on OpenMP threads (same numbers). */
+void bko_attn_decode(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
+                     const float *gate, float *out, float *out_gated, float *dbg_score,
+                     float *dbg_prob, uint16_t *dbg_p16, int nthreads);
+
+/* the same over a subset of head rows [h0, h1) (for bounded CPU-baseline samples) */
+void bko_attn_decode_heads(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
+                           const float *gate, float *out, float *out_gated, int h0, int h1);
+
+/* fp64 ideal leg on the cached (already fp16/q8_0) K/V: round_bits bit0 = round Q to fp16,
+ * bit1 = round P to fp16. out [nh][hd] double. */
+void bko_attn_decode_ideal(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
+                           int round_bits, double *out);
+
+/* chunked prefill: row i = decode over [0, pos0+i] with q + i*nh*hd */
+void bko_attn_prefill(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q, const float *q,
+                      const float *gate, float *out, float *out_gated, int nthreads);
+
+/* seeded synthetic data: splitmix64 -> Box-Muller (double) -> float * sigma.
+ * Element i of stream (seed, stream_id) is a pure function of (seed, stream_id, i). */
+uint64_t bko_splitmix64(uint64_t x);
+void bko_fill_normal(float *x, size_t n, uint64_t seed, uint64_t stream_id, float sigma);
+
+/* K outlier channels: n_out distinct channels in [0, hd) for (seed, layer, kv head) */
+void bko_outlier_channels(uint64_t seed, int layer, int head, int hd, int n_out, int *ch);
+
+/* apply the outlier scaling in place to x [n_tok][nkv][hd] for one layer */
+void bko_apply_outliers(float *x, int n_tok, int nkv, int hd, uint64_t seed, int layer,
+                        int n_out, float factor);
+
+/* wall-clock seconds (monotonic) */
+double bko_now(void);
+
+/* OpenMP thread count the library would use (omp_get_max_threads) */
+int bko_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
