@@ -28,22 +28,31 @@ static inline int64_t next_pow2(int64_t x) {
 }
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Partition sizes: enough workgroups to cover the chip (1024 for QK, 512 for PV at nkv = 4) with at
-// least 16 keys each, never more than kMaxChunk keys (the LDS row).
-DecodePlan plan_decode(int nh, int nkv, int64_t n) {
+// Partition sizes. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16 keys). Probability
+// chunks: 256 keys. PV: enough workgroups to cover the chip (512 at nkv = 4) with 16..512 keys each.
+// Every array is sized by a bound that grows monotonically with n, so a workspace sized for max_ctx
+// fits every n <= max_ctx.
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
   DecodePlan p;
-  p.ch_qk = (int)std::min<int64_t>(kMaxChunk, std::max<int64_t>(16, next_pow2(cdiv(n * nkv, 1024))));
-  p.ch_pv = (int)std::min<int64_t>(kMaxChunk, std::max<int64_t>(16, next_pow2(cdiv(n * nkv, 512))));
-  p.nch_qk = (int)cdiv(n, p.ch_qk);
-  p.nch_pv = (int)cdiv(n, p.ch_pv);
-  p.ld = cdiv(n, 64) * 64;
-  // bounds that grow monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx
-  const int64_t nq_bound = std::max<int64_t>(256, cdiv(n, kMaxChunk));
-  const int64_t np_bound = std::max<int64_t>(128, cdiv(n, kMaxChunk));
-  p.off_score = 0;
-  p.off_stats = align256((size_t)nh * p.ld * sizeof(float));
-  p.off_part = p.off_stats + align256((size_t)nh * nq_bound * sizeof(float2));
-  p.total = p.off_part + align256((size_t)np_bound * nh * kHd * sizeof(float));
+  p.qk_chunk = qk_keys_per_wg(kfmt);
+  p.nch_qk = (int)cdiv(n, p.qk_chunk);
+  p.nch_e = (int)cdiv(n, kE2Chunk);
+  p.pv_chunk = (int)std::min<int64_t>(kPvMaxChunk, std::max<int64_t>(16, next_pow2(cdiv(n * nkv, 512))));
+  p.nch_pv = (int)cdiv(n, p.pv_chunk);
+  p.ld = cdiv(n, kE2Chunk) * kE2Chunk;
+  const int64_t nq_bound = cdiv(n, 128);
+  const int64_t np_bound = std::max<int64_t>(128, cdiv(n, kPvMaxChunk));
+  size_t o = 0;
+  p.off_score = o;  o += align256((size_t)nh * p.ld * sizeof(float));
+  p.off_e = o;      o += align256((size_t)nh * p.ld * sizeof(float));
+  p.off_stats = o;  o += align256((size_t)nh * nq_bound * sizeof(float2));
+  p.off_rec = o;    o += align256((size_t)nh * p.nch_e * sizeof(ChunkRec));
+  p.off_spec = o;   o += align256((size_t)nh * p.nch_e * kMaxSpecial * sizeof(Special));
+  p.off_cnt = o;    o += align256((size_t)nh * sizeof(unsigned));
+  p.off_sum = o;    o += align256((size_t)nh * sizeof(float));
+  p.off_status = o; o += align256((size_t)nh * sizeof(unsigned));
+  p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
+  p.total = o;
   return p;
 }
 
@@ -121,25 +130,35 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if ((gate == nullptr) != (out_gated == nullptr)) return BKV_EINVAL;
   if (!ws) return BKV_EWORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return BKV_EALIGN;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, nfill);
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, nfill);
   if (ws_bytes < p.total) return BKV_EWORKSPACE;
   char *w = (char *)ws;
   const LayerView L = view(d, layer);
 
   QkArgs qa{};
-  qa.L = L; qa.nkv = d->nkv; qa.nfill = nfill; qa.chunk = p.ch_qk; qa.nch_qk = p.nch_qk;
-  qa.ld = p.ld; qa.scale = d->scale; qa.q = q;
+  qa.L = L; qa.nkv = d->nkv; qa.nfill = nfill; qa.nch = p.nch_qk; qa.ld = p.ld; qa.scale = d->scale;
+  qa.q = q;
   qa.score = (float *)(w + p.off_score);
   qa.stats = (float2 *)(w + p.off_stats);
+  qa.counters = (unsigned *)(w + p.off_cnt);
   if (fused) qa.ap = *fused;
+  EArgs ea{};
+  ea.nh = d->nh; ea.nfill = nfill; ea.nch_qk = p.nch_qk; ea.qk_chunk = p.qk_chunk; ea.nch = p.nch_e;
+  ea.ld = p.ld; ea.scale = d->scale; ea.score = qa.score; ea.stats = qa.stats;
+  ea.e = (float *)(w + p.off_e);
+  ea.rec = (ChunkRec *)(w + p.off_rec);
+  ea.spec = (Special *)(w + p.off_spec);
+  ea.counters = qa.counters;
+  ea.sum = (float *)(w + p.off_sum);
+  ea.status = (unsigned *)(w + p.off_status);
   PvArgs pa{};
-  pa.L = L; pa.nkv = d->nkv; pa.nh = d->nh; pa.nfill = nfill; pa.chunk = p.ch_pv;
-  pa.nch_pv = p.nch_pv; pa.nch_qk = p.nch_qk; pa.ld = p.ld; pa.scale = d->scale;
-  pa.score = qa.score; pa.stats = qa.stats; pa.part = (float *)(w + p.off_part);
+  pa.L = L; pa.nkv = d->nkv; pa.nh = d->nh; pa.nfill = nfill; pa.chunk = p.pv_chunk;
+  pa.nch = p.nch_pv; pa.ld = p.ld; pa.e = ea.e; pa.sum = ea.sum;
+  pa.part = (float *)(w + p.off_part);
   RedArgs ra{};
-  ra.nh = d->nh; ra.nch_pv = p.nch_pv; ra.part = pa.part; ra.gate = gate; ra.out = out;
+  ra.nh = d->nh; ra.nch = p.nch_pv; ra.part = pa.part; ra.gate = gate; ra.out = out;
   ra.out_gated = out_gated;
-  return hip_fail(launch_decode(qa, pa, ra, d->k_fmt, d->v_fmt, fused != nullptr, st));
+  return hip_fail(launch_decode(qa, ea, pa, ra, d->k_fmt, d->v_fmt, fused != nullptr, st));
 }
 
 }  // namespace bkv
@@ -226,7 +245,7 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
   if (check(d) || max_ctx == 0) return 0;
   if (op != BKV_OP_DECODE && op != BKV_OP_PREFILL) return 0;
-  return plan_decode(d->nh, d->nkv, max_ctx).total;
+  return plan_decode(d->nh, d->nkv, d->k_fmt, max_ctx).total;
 }
 
 const char *bkv_strerror(int err) {

@@ -105,3 +105,96 @@ __host__ __device__ constexpr int row_bytes(int fmt) { return fmt == BKV_F16 ? k
 constexpr int kScaleRowBytes = kHd / 32 * 2;   // 8 fp16 = 16 B
 
 }  // namespace bkv
+
+namespace bkv {
+
+// fp16 rounding of a wave-uniform value, written in integer arithmetic so that it stays on the
+// scalar unit. Half-normal range: round to nearest even at f32 mantissa bit 13. Everything else
+// (half subnormals, overflow, Inf/NaN) takes the general conversion.
+__device__ __forceinline__ float round_f16_uniform(float x) {
+  const uint32_t u = __float_as_uint(x), a = u & 0x7FFFFFFFu;
+  if (a >= 0x38800000u && a < 0x477FF000u)
+    return __uint_as_float(((a + 0xFFFu + ((a >> 13) & 1u)) & 0xFFFFE000u) | (u & 0x80000000u));
+  return f16_to_f32(f32_to_f16_rne(x));
+}
+
+// exp of a float argument, correctly rounded to float (through the f64 exp)
+__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+
+// ------------------------------------------------------------------ workgroup scans (NT threads)
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const T t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_incl_max_scan(T v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const T t = __shfl_up(v, o);
+    if (lane >= o) v = v > t ? v : t;
+  }
+  return v;
+}
+// exclusive prefix sum over the workgroup; *total receives the sum. sh: NT/64 scratch slots.
+template <int NT, typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T *sh, T *total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const T inc = wave_incl_scan(v, lane);
+  if (lane == 63) sh[w] = inc;
+  __syncthreads();
+  T base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) {
+    if (i < w) base += sh[i];
+    tot += sh[i];
+  }
+  __syncthreads();
+  *total = tot;
+  return base + inc - v;
+}
+// exclusive running max over the workgroup (identity `lo`)
+template <int NT, typename T>
+__device__ __forceinline__ T block_excl_max_scan(T v, T lo, T *sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const T inc = wave_incl_max_scan(v, lane);
+  T ex = __shfl_up(inc, 1);
+  if (lane == 0) ex = lo;
+  if (lane == 63) sh[w] = inc;
+  __syncthreads();
+  T base = lo;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i)
+    if (i < w) base = base > sh[i] ? base : sh[i];
+  __syncthreads();
+  return base > ex ? base : ex;
+}
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float *sh) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) r = fmaxf(r, sh[i]);
+  __syncthreads();
+  return r;
+}
+template <int NT>
+__device__ __forceinline__ double block_sum_f64(double v, double *sh) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) r += sh[i];
+  __syncthreads();
+  return r;
+}
+
+}  // namespace bkv

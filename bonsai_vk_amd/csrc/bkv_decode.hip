@@ -1,16 +1,14 @@
-// bkv_decode.hip - gfx950 kernels of the decode path: q8_0/fp16 append (quantise on write),
-// split-K QK + partition statistics, global-softmax PV over LDS-staged probabilities, and the
-// partition merge with the optional sigmoid gate.
+// bkv_decode.hip - gfx950 kernels of the decode path: q8_0/fp16 append (quantise on write), QK in
+// the reference's accumulation order, the exact serial softmax sum, PV over fp16 probabilities and
+// the partition merge with the optional sigmoid gate.
 //
-// Per layer and decode token the work is three launches:
-//   qk  grid (nch_qk, nkv): one workgroup per (key partition, KV head). Each K row is read once with
-//       128-bit loads (16 lanes per q8_0 row, 32 per fp16 row), dequantised in registers and dotted
-//       with the 4 query heads of the group. Scores go to the workspace, and each partition's
-//       (max, sum exp) pair to the statistics array. The fused variant also appends the new token.
-//   pv  grid (nch_pv, nkv): merges the statistics into the global max and sum of each head, forms
-//       p = exp(s*scale - max)/sum rounded to fp16 exactly as the reference does before its PV
-//       matmul, and accumulates p*V for the 4 heads from one V tile read.
-//   red grid (nh): sums the partition partials and applies the gate.
+// Per layer and decode token the work is four launches:
+//   qk    grid (nch_qk, nkv): K tile in LDS, one accumulation chain per (key, head); scores and
+//         per-partition (max, sum exp). The fused variant appends the new token first.
+//   e     grid (nch_e, nh): e_j = exp(s_j*scale - max) and its exact placement on the serial sum;
+//         the last workgroup of each head walks the chunk records to the exact fp32 sum.
+//   pv    grid (nch_pv, nkv): p16 = f16(e/sum), p16*V for the 4 heads of a group per V tile read.
+//   merge grid (nh, 4): sums the PV partials, applies the gate.
 #include "bkv_common.h"
 #include "bkv_internal.h"
 
@@ -84,117 +82,340 @@ __global__ __launch_bounds__(64) void append_kernel(AppendArgs a) {
   append_token<KF, VF, RHAZ>(a, (int64_t)a.pos + t, t, g, threadIdx.x);
 }
 
-// ------------------------------------------------------------------ QK + partition statistics
+// ------------------------------------------------------------------ QK in the reference's order
+// One thread per key, the K tile staged in LDS with 128-bit coalesced loads. Each score is a single
+// accumulation chain in ascending d, exactly attn_score_row (runtime_vk/attn_vk.h:156-170): fp16 K:
+// acc = acc + q16_d*k_d with exact products; q8_0 K: per 32-block inner = sum of q16_d*int8_d (exact
+// products), then acc = acc + f16(scale)*inner.
+// The 1024 q16 operands of the group live in 64 VGPRs: register (h, j) holds q16[h][16j + lane%16]
+// in every 16-lane DPP row, and each FMA takes its operand through a row_newbcast broadcast of lane
+// d%16, so the shared operand costs no LDS or scalar traffic.
+template <int N>
+__device__ __forceinline__ void fmac_bc(float &acc, float q, float k) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(q), "v"(k), "n"(N));
+}
+// acc = acc + q[base+i]*x[i] for i = 0..I-1, in ascending i
+template <int I>
+struct Dot16 {
+  static __device__ __forceinline__ void run(float &acc, float qr, const float (&x)[16]) {
+    Dot16<I - 1>::run(acc, qr, x);
+    fmac_bc<I - 1>(acc, qr, x[I - 1]);
+  }
+};
+template <>
+struct Dot16<0> {
+  static __device__ __forceinline__ void run(float &, float, const float (&)[16]) {}
+};
+
 template <int KF>
+struct QkTile {
+  static constexpr int DPR = KF == BKV_Q8_0 ? 16 : 32;      // data uint4 per K row
+  static constexpr int UPR = DPR + 1;                       // + scales / pad (bank spread)
+  static constexpr int NT = KF == BKV_Q8_0 ? 256 : 128;     // threads = keys per workgroup
+  static constexpr int KEYS = NT;
+};
+
+template <int KF, int VF, bool FUSE, bool RHAZ>
+__global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
+  using T = QkTile<KF>;
+  constexpr int NT = T::NT;
+  __shared__ uint4 tile[T::KEYS * T::UPR];
+  __shared__ float red[NT / 64 + 1];
+  const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int64_t j0 = (int64_t)c * T::KEYS;
+  const int n = (int)min((int64_t)T::KEYS, (int64_t)a.nfill - j0);
+  const LayerView &L = a.L;
+
+  if (c == 0 && g == 0 && tid < a.nkv * kGqa) a.counters[tid] = 0u;
+  if (FUSE) {
+    if (tid < 64 && (int64_t)a.ap.pos >= j0 && (int64_t)a.ap.pos < j0 + n)
+      append_token<KF, VF, RHAZ>(a.ap, a.ap.pos, 0, g, tid);
+    __syncthreads();
+  }
+  constexpr int RB = row_bytes(KF);
+  for (int i = tid; i < n * T::DPR; i += NT) {
+    const int r = i / T::DPR, col = i % T::DPR;
+    const int64_t slot = slot_of(L, j0 + r);
+    tile[r * T::UPR + col] = *reinterpret_cast<const uint4 *>(L.kd + (slot * a.nkv + g) * RB + col * 16);
+  }
+  if (KF == BKV_Q8_0) {
+    for (int r = tid; r < n; r += NT) {
+      const int64_t slot = slot_of(L, j0 + r);
+      tile[r * T::UPR + 16] = *reinterpret_cast<const uint4 *>(L.ks + (slot * a.nkv + g) * kScaleRowBytes);
+    }
+  }
+  // the group's query rows, rounded to fp16 (the reference's Q16 operand), DPP-row replicated
+  float qv[kGqa][kHd / 16];
+  {
+    const float *qg = a.q + (size_t)g * kGqa * kHd + (tid & 15);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qg[h * kHd + 16 * j]);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qv[h][j]));
+  }
+  __syncthreads();
+  asm volatile("s_nop 4");      // DPP source registers written above: VALU-write -> DPP-read gap
+
+  const uint4 *row = tile + tid * T::UPR;
+  float acc[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) acc[h] = 0.0f;
+  if (KF == BKV_Q8_0) {
+    const uint4 scl = row[16];
+#pragma unroll
+    for (int b = 0; b < kHd / 32; ++b) {
+      const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
+      float x0[16], x1[16];
+      const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        x0[i] = sbyte(u0[i >> 2], i & 3);
+        x1[i] = sbyte(u1[i >> 2], i & 3);
+      }
+      const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
+      const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        float inner = 0.0f;
+        Dot16<16>::run(inner, qv[h][2 * b], x0);
+        Dot16<16>::run(inner, qv[h][2 * b + 1], x1);
+        acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kHd / 16; ++j) {
+      const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+      const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) Dot16<16>::run(acc[h], qv[h][j], x);   // exact products
+    }
+  }
+
+  // scores, and per head the partition's (max, sum exp) used to place each key on the running sum
+  const bool valid = tid < n;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float m = -INFINITY;
+    if (valid) {
+      a.score[(size_t)(g * kGqa + h) * a.ld + j0 + tid] = acc[h];
+      m = acc[h] * a.scale;
+    }
+    m = block_max<NT>(m, red);
+    float l = valid ? __expf(acc[h] * a.scale - m) : 0.0f;
+    l = wave_sum(l);
+    if ((tid & 63) == 0) red[tid >> 6] = l;
+    __syncthreads();
+    if (tid == 0) {
+      float t = 0.0f;
+      for (int i = 0; i < NT / 64; ++i) t += red[i];
+      a.stats[(size_t)(g * kGqa + h) * a.nch + c] = make_float2(m, t);
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ probabilities' numerators and the exact serial sum
+// e_j = exp(s_j*scale - max) (attn_vk.h:182-186), then the reference's serial fp32 sum
+// sum = sum + e_j over ascending j, reproduced exactly. The running sum is non-decreasing, so inside
+// one binade [2^B, 2^(B+1)) every step adds e_j rounded to a multiple of the binade's ulp 2^(B-23):
+// an integer. Each chunk places its keys on the running sum with an approximate fp64 prefix (built
+// from the QK partition statistics, no cross-workgroup wait), turns every step that is safely inside
+// a binade into an exact integer increment, and records the rest - binade crossings, steps within a
+// relative 2^-12 of a binade edge, exact ties, tiny sums - as specials. The last workgroup of each
+// head walks the chunk records in order, adding increments exactly and specials in fp32, and checks
+// every binade assumption; if one fails it recomputes the serial loop itself.
+constexpr double kMargin = 1.0 / 4096.0;
+
+__device__ __forceinline__ void classify(double abefore, double aafter, float e, bool &special,
+                                         int &bin, long long &inc) {
+  special = true;
+  bin = kNoBinade;
+  inc = 0;
+  if (!(aafter >= 0x1p-17) || aafter >= 0x1p22) return;
+  const int B = ilogb(aafter);
+  const double lo = ldexp(1.0, B);
+  if (aafter > 2.0 * lo * (1.0 - kMargin) || abefore < lo * (1.0 + kMargin)) return;
+  const double t = ldexp((double)e, 23 - B);
+  const double fl = floor(t);
+  if (t - fl == 0.5) return;
+  special = false;
+  bin = B;
+  inc = (long long)rint(t) << (B + 17);
+}
+
+__device__ __forceinline__ bool to_units(float s, int B, long long &u) {
+  if (!(s >= ldexpf(1.0f, B) && s < ldexpf(1.0f, B + 1))) return false;
+  u = (long long)ldexp((double)s, 40);
+  return true;
+}
+__device__ __forceinline__ bool from_units(long long u, int B, float &s) {
+  const double d = ldexp((double)u, -40);
+  const float f = (float)d;
+  if ((double)f != d || (long long)ldexp((double)f, 40) != u) return false;
+  if (!(f >= ldexpf(1.0f, B) && f < ldexpf(1.0f, B + 1))) return false;
+  s = f;
+  return true;
+}
+
+__global__ __launch_bounds__(256) void e_kernel(EArgs a) {
+  constexpr int NT = 256;
+  __shared__ double shd[NT / 64];
+  __shared__ long long shl[NT / 64];
+  __shared__ int shi[NT / 64];
+  __shared__ float shf[NT / 64 + 1];
+  __shared__ int s_bin[NT];
+  __shared__ unsigned s_last;
+  __shared__ ChunkRec s_rec[NT];
+  const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int64_t j0 = (int64_t)c * kE2Chunk;
+  const int n = (int)min((int64_t)kE2Chunk, (int64_t)a.nfill - j0);
+  const float2 *st = a.stats + (size_t)h * a.nch_qk;
+
+  float m = -INFINITY;
+  for (int i = tid; i < a.nch_qk; i += NT) m = fmaxf(m, st[i].x);
+  m = block_max<NT>(m, shf);
+  const int cq = (int)(j0 / a.qk_chunk);
+  double p = 0.0;
+  for (int i = tid; i < cq; i += NT) p += (double)st[i].y * exp((double)st[i].x - (double)m);
+  p = block_sum_f64<NT>(p, shd);
+
+  const bool valid = tid < n;
+  float e = 0.0f;
+  if (valid) {
+    const float v = a.score[(size_t)h * a.ld + j0 + tid] * a.scale;
+    e = exp_cr(v - m);
+    a.e[(size_t)h * a.ld + j0 + tid] = e;
+  }
+  double tot_d;
+  const double ex = block_excl_scan<NT, double>((double)e, shd, &tot_d);
+  bool sp = false;
+  int bin = kNoBinade;
+  long long inc = 0;
+  if (valid) classify(p + ex, p + ex + (double)e, e, sp, bin, inc);
+  s_bin[tid] = bin;
+  long long tot_l;
+  const long long ipre = block_excl_scan<NT, long long>(inc, shl, &tot_l);
+  int nsp;
+  const int idx = block_excl_scan<NT, int>((valid && sp) ? 1 : 0, shi, &nsp);
+  const int last_ns = block_excl_max_scan<NT, int>((valid && !sp) ? tid : -1, -1, shi);
+  const int last_sp = block_excl_max_scan<NT, int>((valid && sp) ? tid : -1, -1, shi);
+  __syncthreads();
+  Special *spec = a.spec + ((size_t)h * a.nch + c) * kMaxSpecial;
+  if (valid && sp && idx < kMaxSpecial) {
+    Special s;
+    s.ipre = ipre;
+    s.e = e;
+    const int bprev = last_ns >= 0 ? s_bin[last_ns] : kNoBinade;
+    s.meta = tid | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16) | ((last_ns > last_sp) ? (1 << 24) : 0);
+    spec[idx] = s;
+  }
+  // the chunk record: thread NT-1 sees the whole chunk through its inclusive view
+  if (tid == NT - 1) {
+    const bool me_ns = valid && !sp, me_sp = valid && sp;
+    const int lns = me_ns ? tid : last_ns, lsp = me_sp ? tid : last_sp;
+    ChunkRec r;
+    r.tot = tot_l;
+    r.nsp = nsp;
+    r.blast = (lns > lsp && lns >= 0) ? s_bin[lns] : kNoBinade;
+    a.rec[(size_t)h * a.nch + c] = r;
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&a.counters[h], 1u) == (unsigned)(a.nch - 1) ? 1u : 0u;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // ---- the walk (last workgroup of head h)
+  float s = 0.0f;
+  long long seg = 0;
+  int segb = kNoBinade;
+  bool seg_has = false, ok = true;
+  for (int cb = 0; cb < a.nch && ok; cb += NT) {
+    const int nb = min(NT, a.nch - cb);
+    if (tid < nb) s_rec[tid] = a.rec[(size_t)h * a.nch + cb + tid];
+    __syncthreads();
+    if (tid == 0) {
+      for (int cc = 0; cc < nb && ok; ++cc) {
+        const ChunkRec r = s_rec[cc];
+        if (r.nsp > kMaxSpecial) { ok = false; break; }
+        const Special *sp2 = a.spec + ((size_t)h * a.nch + cb + cc) * kMaxSpecial;
+        long long prev = 0;
+        for (int j = 0; j < r.nsp; ++j) {
+          const Special x = sp2[j];
+          seg += x.ipre - prev;
+          prev = x.ipre;
+          if (x.meta & (1 << 24)) {
+            segb = ((x.meta >> 16) & 0xFF) - 128;
+            seg_has = true;
+          }
+          if (seg_has) {
+            long long u;
+            if (!to_units(s, segb, u) || !from_units(u + seg, segb, s)) { ok = false; break; }
+          } else if (seg != 0) { ok = false; break; }
+          seg = 0;
+          seg_has = false;
+          s = __fadd_rn(s, x.e);
+        }
+        seg += r.tot - prev;
+        if (r.blast != kNoBinade) {
+          segb = r.blast;
+          seg_has = true;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0) s_last = ok ? 1u : 0u;
+    __syncthreads();
+    ok = s_last != 0;
+  }
+  if (tid == 0 && ok && seg_has) {
+    long long u;
+    if (!to_units(s, segb, u) || !from_units(u + seg, segb, s)) ok = false;
+  }
+  if (tid == 0) s_last = ok ? 1u : 0u;
+  __syncthreads();
+  if (!s_last) {
+    // fallback: the serial loop itself, 256 terms staged in LDS at a time
+    float *stage = reinterpret_cast<float *>(s_rec);
+    float ss = 0.0f;
+    for (int64_t b0 = 0; b0 < a.nfill; b0 += NT) {
+      const int nb = (int)min((int64_t)NT, (int64_t)a.nfill - b0);
+      if (tid < nb) stage[tid] = a.e[(size_t)h * a.ld + b0 + tid];
+      __syncthreads();
+      if (tid == 0)
+        for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, stage[i]);
+      __syncthreads();
+    }
+    s = ss;
+  }
+  if (tid == 0) {
+    a.sum[h] = s;
+    a.status[h] = s_last ? 0u : 1u;
+  }
+}
+
+// ------------------------------------------------------------------ PV over the fp16 probabilities
+template <int VF>
 struct KRow {
-  static constexpr int LPR = KF == BKV_Q8_0 ? 16 : 32;   // lanes per head row
+  static constexpr int LPR = VF == BKV_Q8_0 ? 16 : 32;   // lanes per head row
   static constexpr int EPL = kHd / LPR;                  // elements per lane (16 or 8)
   static constexpr int KPW = kWave / LPR;                // rows per wave per step (4 or 2)
 };
 
-// partial dot of one lane's EPL elements of a K row with the 4 query heads
-template <int KF>
-__device__ __forceinline__ void k_partial(const uint4 w, float ksc, const float (&q)[kGqa][KRow<KF>::EPL],
-                                          float (&part)[kGqa]) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) part[h] = 0.0f;
-  if (KF == BKV_Q8_0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float x = sbyte(ww[i >> 2], i & 3);
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h) part[h] = fmaf(q[h][i], x, part[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) part[h] *= ksc;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float x = f16_to_f32((ww[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h) part[h] = fmaf(q[h][i], x, part[h]);
-    }
-  }
-}
-
-template <int KF, int VF, bool FUSE, bool RHAZ>
-__global__ __launch_bounds__(256) void qk_kernel(QkArgs a) {
-  using R = KRow<KF>;
-  __shared__ float s_sc[kGqa][kMaxChunk];
-  const int c = blockIdx.x, g = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % R::LPR, kk = lane / R::LPR;
-  const int64_t j0 = (int64_t)c * a.chunk;
-  const int64_t j1 = min(j0 + (int64_t)a.chunk, (int64_t)a.nfill);
-  const int n = (int)(j1 - j0);
-
-  if (FUSE) {
-    if (wave == 0 && (int64_t)a.ap.pos >= j0 && (int64_t)a.ap.pos < j1)
-      append_token<KF, VF, RHAZ>(a.ap, a.ap.pos, 0, g, lane);
-    __syncthreads();
-  }
-
-  // the lane's slice of the 4 query rows, rounded to fp16 (the reference's Q16 operand)
-  float q[kGqa][R::EPL];
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)(g * kGqa + h) * kHd + sub * R::EPL);
-#pragma unroll
-    for (int i = 0; i < R::EPL / 4; ++i) {
-      const float4 t = qp[i];
-      q[h][4 * i] = round_f16(t.x); q[h][4 * i + 1] = round_f16(t.y);
-      q[h][4 * i + 2] = round_f16(t.z); q[h][4 * i + 3] = round_f16(t.w);
-    }
-  }
-
-  const LayerView &L = a.L;
-  constexpr int RB = row_bytes(KF);
-  for (int jb = wave * R::KPW; jb < n; jb += 4 * R::KPW) {
-    const int jl = jb + kk;
-    const bool valid = jl < n;
-    const int64_t slot = slot_of(L, j0 + (valid ? jl : 0));
-    const uint4 w = *reinterpret_cast<const uint4 *>(L.kd + (slot * a.nkv + g) * RB + sub * 16);
-    float ksc = 1.0f;
-    if (KF == BKV_Q8_0) {
-      const uint32_t sw = *reinterpret_cast<const uint32_t *>(L.ks + (slot * a.nkv + g) * kScaleRowBytes +
-                                                              (sub >> 2) * 4);
-      ksc = f16_to_f32(((sub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-    }
-    float part[kGqa];
-    k_partial<KF>(w, ksc, q, part);
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) {
-      float v = row16_sum(part[h]);
-      if (R::LPR == 32) v += __shfl_xor(v, 16);
-      part[h] = v;
-    }
-    if (valid && sub < kGqa) {
-      const float v = sub == 0 ? part[0] : sub == 1 ? part[1] : sub == 2 ? part[2] : part[3];
-      s_sc[sub][jl] = v;
-    }
-  }
-  __syncthreads();
-
-  // wave h: scores of head h to the workspace, and the partition's (max, sum exp)
-  {
-    const int h = wave;
-    float *dst = a.score + (size_t)(g * kGqa + h) * a.ld + j0;
-    float m = -INFINITY;
-    for (int t = lane; t < n; t += kWave) {
-      const float s = s_sc[h][t];
-      dst[t] = s;
-      m = fmaxf(m, s * a.scale);
-    }
-    m = wave_max(m);
-    float l = 0.0f;
-    for (int t = lane; t < n; t += kWave) l += expf(s_sc[h][t] * a.scale - m);
-    l = wave_sum(l);
-    if (lane == 0) a.stats[(size_t)(g * kGqa + h) * a.nch_qk + c] = make_float2(m, l);
-  }
-}
-
-// ------------------------------------------------------------------ PV over globally normalised P16
+// p16_j = f16_rne(e_j / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296); out = sum_j p16_j*V_j.
+// 16 lanes per q8_0 V row (32 per fp16 row) with 128-bit loads; the 4 heads of the group share each
+// V tile read. Accumulation order is free here (within the tolerance).
 template <int VF>
 __device__ __forceinline__ void v_accum(const uint4 w, float vsc, const float (&p)[kGqa],
                                         float (&acc)[kGqa][KRow<VF>::EPL]) {
@@ -222,38 +443,22 @@ __device__ __forceinline__ void v_accum(const uint4 w, float vsc, const float (&
 template <int VF>
 __global__ __launch_bounds__(256) void pv_kernel(PvArgs a) {
   using R = KRow<VF>;
-  __shared__ float s_p[kGqa][kMaxChunk];
+  __shared__ float s_p[kGqa][kPvMaxChunk];
   __shared__ float s_red[4][kGqa][kHd];
-  __shared__ float s_ms[kGqa][2];
   const int c = blockIdx.x, g = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane % R::LPR, kk = lane / R::LPR;
   const int64_t j0 = (int64_t)c * a.chunk;
-  const int64_t j1 = min(j0 + (int64_t)a.chunk, (int64_t)a.nfill);
-  const int n = (int)(j1 - j0);
+  const int n = (int)min((int64_t)a.chunk, (int64_t)a.nfill - j0);
 
-  // global max and sum of head (g*4 + wave) from the QK partition statistics
-  {
-    const float2 *st = a.stats + (size_t)(g * kGqa + wave) * a.nch_qk;
-    float m = -INFINITY;
-    for (int i = lane; i < a.nch_qk; i += kWave) m = fmaxf(m, st[i].x);
-    m = wave_max(m);
-    float l = 0.0f;
-    for (int i = lane; i < a.nch_qk; i += kWave) {
-      const float2 v = st[i];
-      l += v.y * expf(v.x - m);
-    }
-    l = wave_sum(l);
-    if (lane == 0) { s_ms[wave][0] = m; s_ms[wave][1] = l; }
-  }
-  __syncthreads();
-  // p16 of every key of the partition (attn_vk.h:175-189 then the fp16 operand cast, :295-296)
+  float inv[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) inv[h] = a.sum[g * kGqa + h];
   for (int t = tid; t < n; t += 256) {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) {
-      const float s = a.score[(size_t)(g * kGqa + h) * a.ld + j0 + t];
-      const float e = expf(s * a.scale - s_ms[h][0]);
-      s_p[h][t] = round_f16(e / s_ms[h][1]);
+      const float e = a.e[(size_t)(g * kGqa + h) * a.ld + j0 + t];
+      s_p[h][t] = round_f16(e / inv[h]);
     }
   }
   __syncthreads();
@@ -282,7 +487,6 @@ __global__ __launch_bounds__(256) void pv_kernel(PvArgs a) {
     for (int h = 0; h < kGqa; ++h) p[h] = valid ? s_p[h][jl] : 0.0f;
     v_accum<VF>(w, vsc, p, acc);
   }
-  // reduce the row groups of the wave (lanes sub, sub+LPR, ...)
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
@@ -307,13 +511,21 @@ __global__ __launch_bounds__(256) void pv_kernel(PvArgs a) {
 }
 
 // ------------------------------------------------------------------ partition merge + gate
-__global__ __launch_bounds__(256) void reduce_kernel(RedArgs a) {
-  const int h = blockIdx.x, d = threadIdx.x;
+// gated = out * (1/(1 + exp(-gate))) (attn_vk.h:210-212)
+__global__ __launch_bounds__(256) void merge_kernel(RedArgs a) {
+  __shared__ float s[4][64];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int d = blockIdx.y * 64 + (tid & 63), grp = tid >> 6;
   float acc = 0.0f;
-  for (int c = 0; c < a.nch_pv; ++c) acc += a.part[((size_t)c * a.nh + h) * kHd + d];
-  const size_t o = (size_t)h * kHd + d;
-  a.out[o] = acc;
-  if (a.gate) a.out_gated[o] = acc * (1.0f / (1.0f + expf(-a.gate[o])));
+  for (int c = grp; c < a.nch; c += 4) acc += a.part[((size_t)c * a.nh + h) * kHd + d];
+  s[grp][tid & 63] = acc;
+  __syncthreads();
+  if (tid < 64) {
+    const float v = (s[0][tid] + s[1][tid]) + (s[2][tid] + s[3][tid]);
+    const size_t o = (size_t)h * kHd + d;
+    a.out[o] = v;
+    if (a.gate) a.out_gated[o] = v * (1.0f / (1.0f + exp_cr(-a.gate[o])));
+  }
 }
 
 // ------------------------------------------------------------------ launchers
@@ -331,16 +543,20 @@ hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStre
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const QkArgs &qa, const PvArgs &pa, const RedArgs &ra, int kf, int vf,
-                         bool fuse, hipStream_t st) {
+int qk_keys_per_wg(int kf) { return kf == BKV_Q8_0 ? QkTile<1>::KEYS : QkTile<0>::KEYS; }
+
+hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, const RedArgs &ra,
+                         int kf, int vf, bool fuse, hipStream_t st) {
   BKV_FMT_SWITCH(kf, vf, {
+    constexpr int NT = QkTile<KF_>::NT;
     if (fuse)
-      hipLaunchKernelGGL((qk_kernel<KF_, VF_, true, false>), dim3(qa.nch_qk, qa.nkv), dim3(256), 0, st, qa);
+      hipLaunchKernelGGL((qk_kernel<KF_, VF_, true, false>), dim3(qa.nch, qa.nkv), dim3(NT), 0, st, qa);
     else
-      hipLaunchKernelGGL((qk_kernel<KF_, VF_, false, false>), dim3(qa.nch_qk, qa.nkv), dim3(256), 0, st, qa);
-    hipLaunchKernelGGL((pv_kernel<VF_>), dim3(pa.nch_pv, pa.nkv), dim3(256), 0, st, pa);
+      hipLaunchKernelGGL((qk_kernel<KF_, VF_, false, false>), dim3(qa.nch, qa.nkv), dim3(NT), 0, st, qa);
+    hipLaunchKernelGGL(e_kernel, dim3(ea.nch, ea.nh), dim3(256), 0, st, ea);
+    hipLaunchKernelGGL((pv_kernel<VF_>), dim3(pa.nch, pa.nkv), dim3(256), 0, st, pa);
   });
-  hipLaunchKernelGGL(reduce_kernel, dim3(ra.nh), dim3(256), 0, st, ra);
+  hipLaunchKernelGGL(merge_kernel, dim3(ra.nh, 4), dim3(256), 0, st, ra);
   return hipGetLastError();
 }
 

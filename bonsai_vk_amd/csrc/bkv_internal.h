@@ -1,20 +1,35 @@
-// bkv_internal.h - kernel argument blocks and launchers shared by the API layer and the kernels.
+// bkv_internal.h - kernel argument blocks, workspace plan and launchers shared by the API layer and
+// the kernels.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/bkv.h"
-
-namespace bkv {
-
-constexpr int kMaxChunk = 512;   // keys per decode partition held in LDS
-
-}  // namespace bkv
-
 #include "bkv_common.h"
 
 namespace bkv {
+
+// ------------------------------------------------------------------ decode geometry
+constexpr int kE2Chunk = 256;      // keys per workgroup of the probability kernel
+constexpr int kMaxSpecial = 32;    // exactly-added steps recorded per probability chunk
+constexpr int kPvMaxChunk = 512;   // keys per PV partition held in LDS
+
+// one probability chunk's contribution to the exact serial softmax sum
+struct ChunkRec {
+  long long tot;      // sum of the non-special increments, units of 2^-40
+  int nsp;            // specials recorded (> kMaxSpecial: overflow)
+  int blast;          // binade of the last non-special step after the last special, or kNoBinade
+};
+// one step the walker adds in fp32 exactly as the serial loop does
+struct Special {
+  long long ipre;     // increments of the chunk's non-special steps before it, units of 2^-40
+  float e;            // the term added
+  int meta;           // bits 0..15: position in chunk; bits 16..23: binade+128 of the last
+                      // non-special step before it in the chunk (0 = none); bit 24: a
+                      // non-special step lies between it and the previous special of the chunk
+};
+constexpr int kNoBinade = -1000;
 
 struct AppendArgs {
   LayerView L;
@@ -27,45 +42,63 @@ struct QkArgs {
   LayerView L;
   int nkv;
   uint32_t nfill;
-  int chunk, nch_qk;
-  int64_t ld;                    // score row stride (floats)
+  int nch;                       // QK partitions
+  int64_t ld;                    // row stride of score / e (floats)
   float scale;
-  const float *q;                // [nh][hd]
+  const float *q;                // [nh][hd] fp32
   float *score;                  // [nh][ld]
-  float2 *stats;                 // [nh][nch_qk]
+  float2 *stats;                 // [nh][nch] (partition max of s*scale, sum exp(s*scale - max))
+  unsigned *counters;            // [nh] arrivals of the probability kernel (zeroed here)
   AppendArgs ap;                 // fused append of position ap.pos (decode_step)
+};
+
+struct EArgs {
+  int nh;
+  uint32_t nfill;
+  int nch_qk, qk_chunk, nch;     // QK partitions (stats), probability chunks
+  int64_t ld;
+  float scale;
+  const float *score;
+  const float2 *stats;
+  float *e;                      // [nh][ld] exp(s*scale - max), correctly rounded
+  ChunkRec *rec;                 // [nh][nch]
+  Special *spec;                 // [nh][nch][kMaxSpecial]
+  unsigned *counters;            // [nh]
+  float *sum;                    // [nh] the exact serial sum
+  unsigned *status;              // [nh] 1 when the walker fell back to the serial loop
 };
 
 struct PvArgs {
   LayerView L;
   int nkv, nh;
   uint32_t nfill;
-  int chunk, nch_pv, nch_qk;
+  int chunk, nch;
   int64_t ld;
-  float scale;
-  const float *score;
-  const float2 *stats;
-  float *part;                   // [nch_pv][nh][hd]
+  const float *e;
+  const float *sum;
+  float *part;                   // [nch][nh][hd]
 };
 
 struct RedArgs {
-  int nh, nch_pv;
+  int nh, nch;
   const float *part;
   const float *gate;
   float *out, *out_gated;
 };
 
-// decode partition plan for nfill keys
+// decode partition plan and workspace layout for nfill keys
 struct DecodePlan {
-  int ch_qk, nch_qk, ch_pv, nch_pv;
+  int qk_chunk, nch_qk, nch_e, pv_chunk, nch_pv;
   int64_t ld;
-  size_t off_score, off_stats, off_part, total;
+  size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_part,
+      total;
 };
 
-DecodePlan plan_decode(int nh, int nkv, int64_t nfill);
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t nfill);
+int qk_keys_per_wg(int kfmt);
 
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);
-hipError_t launch_decode(const QkArgs &qa, const PvArgs &pa, const RedArgs &ra, int kf, int vf,
-                         bool fuse, hipStream_t st);
+hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, const RedArgs &ra,
+                         int kf, int vf, bool fuse, hipStream_t st);
 
 }  // namespace bkv

@@ -66,6 +66,7 @@ def lib():
             "bko_outlier_channels": (None, [ctypes.c_uint64, i32, i32, i32, i32, P]),
             "bko_apply_outliers": (None, [P, i32, i32, i32, ctypes.c_uint64, i32, i32, ctypes.c_float]),
             "bko_now": (ctypes.c_double, []),
+            "bko_set_exp_mode": (None, [i32]),
             "bko_max_threads": (i32, []),
         }
         for n, (r, a) in sig.items():
@@ -92,6 +93,19 @@ def ref():
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class exp_mode:
+    """context manager: 0 = correctly rounded exp (default), 1 = libm expf (the reference mirror's)"""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        lib().bko_set_exp_mode(self.mode)
+
+    def __exit__(self, *a):
+        lib().bko_set_exp_mode(0)
 
 
 # ------------------------------------------------------------------ fp16 / q8_0

@@ -11,6 +11,15 @@
 #include <omp.h>
 #endif
 
+/* exp used by the softmax and the gate. Mode 0 (default): the correctly rounded exp of the float
+ * argument, formed as (float)exp((double)x) - the value both this oracle and the gfx950 kernels
+ * compute. Mode 1: the C library's expf, as the reference's CPU mirror calls std::exp(float)
+ * (runtime_vk/attn_vk.h:184,211); used to check the oracle against that mirror bit for bit. The two
+ * differ only where the library's expf is not correctly rounded. */
+static int g_exp_mode = 0;
+void bko_set_exp_mode(int mode) { g_exp_mode = mode; }
+static inline float oexp(float x) { return g_exp_mode ? expf(x) : (float)exp((double)x); }
+
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
@@ -229,11 +238,24 @@ static void decode_row(const bkv_cache_desc *d, int layer, uint32_t nfill, const
         acc = acc + q16[2 * w + 1] * khi;
       }
     } else {
+      /* q8_0 K (no reference counterpart: the reference never compresses K). The block scale is
+       * factored out of each 32-element block: inner = sum over the block, ascending, of
+       * q16_d * int8_d (every product exact in fp32), then acc = acc + f16(scale) * inner. */
       const uint32_t *row = arr(d, 0, layer) + (slot * d->nkv + g) * (hd / 4);
       const uint32_t *srow = arr(d, 1, layer) + (slot * d->nkv + g) * (hd / 64);
-      for (int e = 0; e < hd; ++e) acc = acc + q16[e] * q8_elem(row, srow, e);
-    }
-    s[j] = acc;
+      for (int b = 0; b < hd / 32; ++b) {
+        const uint32_t sw = srow[b >> 1];
+        const float sc = bko_f16_to_f32((uint16_t)((b & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+        float inner = 0.0f;
+        for (int e = 32 * b; e < 32 * b + 32; ++e) {
+          const uint32_t w = row[e >> 2];
+          const int by = (int)((w >> ((e & 3) * 8)) & 0xFFu);
+          inner = inner + q16[e] * (float)(by >= 128 ? by - 256 : by);
+        }
+        const float t = sc * inner;
+        acc = acc + t;
+      }
+    }    s[j] = acc;
   }
   {
     float mx = -INFINITY, sum = 0.0f;
@@ -243,7 +265,7 @@ static void decode_row(const bkv_cache_desc *d, int layer, uint32_t nfill, const
     }
     for (uint32_t j = 0; j < nfill; ++j) {
       const float v = s[j] * d->scale;
-      pr[j] = expf(v - mx);
+      pr[j] = oexp(v - mx);
       sum = sum + pr[j];
     }
     for (uint32_t j = 0; j < nfill; ++j) {
@@ -261,7 +283,7 @@ static void decode_row(const bkv_cache_desc *d, int layer, uint32_t nfill, const
     for (int dd = 0; dd < hd; ++dd) orow[dd] = orow[dd] + pr[j] * krow[dd];
   }
   if (grow && gout)
-    for (int dd = 0; dd < hd; ++dd) gout[dd] = orow[dd] * (1.0f / (1.0f + expf(-grow[dd])));
+    for (int dd = 0; dd < hd; ++dd) gout[dd] = orow[dd] * (1.0f / (1.0f + oexp(-grow[dd])));
 }
 
 static void decode_range(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,

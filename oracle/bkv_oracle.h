@@ -82,6 +82,9 @@ void bko_attn_decode_ideal(const bkv_cache_desc *d, int layer, uint32_t nfill, c
 void bko_attn_prefill(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q, const float *q,
                       const float *gate, float *out, float *out_gated, int nthreads);
 
+/* exp mode: 0 = correctly rounded (float)exp((double)x) (default), 1 = libm expf */
+void bko_set_exp_mode(int mode);
+
 /* seeded synthetic data: splitmix64 -> Box-Muller (double) -> float * sigma.
  * Element i of stream (seed, stream_id) is a pure function of (seed, stream_id, i). */
 uint64_t bko_splitmix64(uint64_t x);

@@ -31,7 +31,8 @@ def test_config1_matches_reference_mirror_bitwise():
     nfill = 256
     c, _, _ = make_cache(nfill, F16, F16, seed=0)
     q, g = q_gate(0)
-    out, og, sc, pr, p16 = c.decode(0, nfill, q, g, debug=True)
+    with oracle.exp_mode(1):                      # the mirror calls std::exp(float)
+        out, og, sc, pr, p16 = c.decode(0, nfill, q, g, debug=True)
     q16 = oracle.f32_to_f16(q).view(np.uint32).reshape(16, 128)
     kc = np.ascontiguousarray(c.k_data[0]).view(np.uint32)
     vc = np.ascontiguousarray(c.v_data[0]).view(np.uint32)
@@ -154,3 +155,34 @@ def test_threads_do_not_change_numbers():
     a, ag = c.decode(0, 500, q, g, nthreads=1)
     b, bg = c.decode(0, 500, q, g, nthreads=4)
     assert oracle.bit_diff(a, b) == 0 and oracle.bit_diff(ag, bg) == 0
+
+
+def test_exp_modes_differ_only_where_libm_is_not_correctly_rounded():
+    c, _, _ = make_cache(2048, Q8_0, Q8_0, seed=13, outliers=3)
+    q, g = q_gate(13)
+    a, ag, _, pa, _ = c.decode(0, 2048, q, g, debug=True)
+    with oracle.exp_mode(1):
+        b, bg, _, pb, _ = c.decode(0, 2048, q, g, debug=True)
+    # almost every probability is bit-identical, and the outputs agree far inside the tolerance
+    assert (pa != pb).mean() < 0.01
+    assert oracle.rel_err(a, b) < 1e-4 and oracle.rel_err(ag, bg) < 1e-4
+
+
+def test_q8_k_dot_is_block_factored():
+    """q8_0 K: score = sum over blocks of f16(scale) * (ascending exact sum of q16*int8)."""
+    n = 8
+    c, _, _ = make_cache(n, Q8_0, F16, seed=14, outliers=3)
+    q, _ = q_gate(14)
+    _, _, sc, _, _ = c.decode(0, n, q, debug=True)
+    q16 = oracle.f16_to_f32(oracle.f32_to_f16(q))
+    i8 = c.k_data[0].view(np.int8).reshape(n, 4, 8, 32).astype(np.float32)
+    s = c.k_scales[0].view(np.float16).reshape(n, 4, 8).astype(np.float32)
+    for h in range(16):
+        for j in range(n):
+            acc = np.float32(0)
+            for b in range(8):
+                inner = np.float32(0)
+                for e in range(32):
+                    inner = np.float32(inner + np.float32(q16[h, 32 * b + e] * i8[j, h // 4, b, e]))
+                acc = np.float32(acc + np.float32(s[j, h // 4, b] * inner))
+            assert acc == sc[h, j]
