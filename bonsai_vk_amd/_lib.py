@@ -19,7 +19,7 @@ ERRORS = {
 EXPORTS = [
     "bkv_geom_check", "bkv_slot_bytes", "bkv_max_positions", "bkv_kv_append", "bkv_attn_decode",
     "bkv_decode_step", "bkv_attn_prefill_chunk", "bkv_workspace_bytes", "bkv_strerror",
-    "bkv_last_hip_error", "bkv_version",
+    "bkv_last_hip_error", "bkv_version", "bkv_debug_layout",
 ]
 
 
@@ -71,6 +71,7 @@ def lib():
         "bkv_strerror": (ctypes.c_char_p, [i32]),
         "bkv_last_hip_error": (ctypes.c_char_p, []),
         "bkv_version": (ctypes.c_char_p, []),
+        "bkv_debug_layout": (i32, [D, u32, ctypes.POINTER(ctypes.c_uint64)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

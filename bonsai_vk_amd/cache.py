@@ -197,6 +197,22 @@ class KvCache:
         return self._pws
 
     # ---------------------------------------------------------------- inspection
+    def debug_intermediates(self, nfill):
+        """After a decode over nfill keys (stream-synchronised): scores [nh][nfill], e [nh][nfill],
+        exact softmax sums [nh] and walker status [nh], read from the workspace."""
+        out = (ctypes.c_uint64 * 6)()
+        check(lib().bkv_debug_layout(ctypes.byref(self.desc), nfill, out), "bkv_debug_layout")
+        ld, o_s, o_e, o_sum, o_st = (int(x) for x in out[:5])
+        ws = self.workspace
+        f = lambda off, n: ws[off:off + 4 * n].view(torch.float32)
+        nh = self.nh
+        score = f(o_s, nh * ld).view(nh, ld)[:, :nfill].cpu()
+        e = f(o_e, nh * ld).view(nh, ld)[:, :nfill].cpu()
+        ssum = f(o_sum, nh).cpu()
+        status = ws[o_st:o_st + 4 * nh].view(torch.int32).cpu()
+        return score, e, ssum, status
+
+    
     def host_arrays(self):
         """The four sub-arenas as CPU uint8 tensors [n_layers][cap][row bytes] (None if absent)."""
         return [None if a is None else a.cpu() for a in

@@ -48,7 +48,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
   p.off_stats = o;  o += align256((size_t)nh * nq_bound * sizeof(float2));
   p.off_rec = o;    o += align256((size_t)nh * p.nch_e * sizeof(ChunkRec));
   p.off_spec = o;   o += align256((size_t)nh * p.nch_e * kMaxSpecial * sizeof(Special));
-  p.off_cnt = o;    o += align256((size_t)nh * sizeof(unsigned));
+  p.off_cnt = o;    o += align256((size_t)nh * kCounterStride * sizeof(unsigned));
   p.off_sum = o;    o += align256((size_t)nh * sizeof(float));
   p.off_status = o; o += align256((size_t)nh * sizeof(unsigned));
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
@@ -260,6 +260,20 @@ const char *bkv_strerror(int err) {
     case BKV_EUNSUPPORTED: return "shape not supported by the gfx950 kernels (hd 256, nh = 4*nkv)";
     default: return "unknown error";
   }
+}
+
+int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
+  const int rc = check(d);
+  if (rc) return rc;
+  if (!out || nfill == 0) return BKV_EINVAL;
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, nfill);
+  out[0] = (uint64_t)p.ld;
+  out[1] = p.off_score;
+  out[2] = p.off_e;
+  out[3] = p.off_sum;
+  out[4] = p.off_status;
+  out[5] = p.total;
+  return BKV_OK;
 }
 
 const char *bkv_last_hip_error(void) { return g_hip_err; }

@@ -128,7 +128,7 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
   const int n = (int)min((int64_t)T::KEYS, (int64_t)a.nfill - j0);
   const LayerView &L = a.L;
 
-  if (c == 0 && g == 0 && tid < a.nkv * kGqa) a.counters[tid] = 0u;
+  if (c == 0 && g == 0 && tid < a.nkv * kGqa) a.counters[tid * kCounterStride] = 0u;
   if (FUSE) {
     if (tid < 64 && (int64_t)a.ap.pos >= j0 && (int64_t)a.ap.pos < j0 + n)
       append_token<KF, VF, RHAZ>(a.ap, a.ap.pos, 0, g, tid);
@@ -231,10 +231,12 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
 // an integer. Each chunk places its keys on the running sum with an approximate fp64 prefix (built
 // from the QK partition statistics, no cross-workgroup wait), turns every step that is safely inside
 // a binade into an exact integer increment, and records the rest - binade crossings, steps within a
-// relative 2^-12 of a binade edge, exact ties, tiny sums - as specials. The last workgroup of each
+// relative 2^-14 of a binade edge (the fp64
+// prefix stays within ~1.2e-5 of the serial sum at 64K keys), exact ties, tiny sums - as specials. The last workgroup of each
 // head walks the chunk records in order, adding increments exactly and specials in fp32, and checks
 // every binade assumption; if one fails it recomputes the serial loop itself.
-constexpr double kMargin = 1.0 / 4096.0;
+constexpr double kMargin = 1.0 / 16384.0;
+constexpr int kWalkBatch = 32;
 
 __device__ __forceinline__ void classify(double abefore, double aafter, float e, bool &special,
                                          int &bin, long long &inc) {
@@ -267,15 +269,58 @@ __device__ __forceinline__ bool from_units(long long u, int B, float &s) {
   return true;
 }
 
+// Cross-workgroup hand-off inside the probability kernel without L2-wide fences: everything the
+// walker reads (chunk records, specials, e) is written with agent-scope relaxed atomic stores, which
+// write through the XCD's L2, and read with agent-scope atomic loads, which bypass it; each producer
+// waits for its stores to complete (s_waitcnt) before it counts itself in.
+template <typename T>
+__device__ __forceinline__ void st_agent(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T *p) {
+  return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_rec(ChunkRec *p, const ChunkRec &r) {
+  st_agent(&p->tot, r.tot);
+  st_agent(&p->nsp, r.nsp);
+  st_agent(&p->blast, r.blast);
+}
+__device__ __forceinline__ ChunkRec ld_rec(const ChunkRec *p) {
+  ChunkRec r;
+  r.tot = ld_agent(&p->tot);
+  r.nsp = ld_agent(&p->nsp);
+  r.blast = ld_agent(&p->blast);
+  return r;
+}
+__device__ __forceinline__ void st_spec(Special *p, const Special &x) {
+  st_agent(&p->ipre, x.ipre);
+  st_agent(&p->e, x.e);
+  st_agent(&p->meta, x.meta);
+}
+__device__ __forceinline__ Special ld_spec(const Special *p) {
+  Special x;
+  x.ipre = ld_agent(&p->ipre);
+  x.e = ld_agent(&p->e);
+  x.meta = ld_agent(&p->meta);
+  return x;
+}
+
 __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
-  constexpr int NT = 256;
+  constexpr int NT = 256, EPT = kE2Chunk / NT;       // 4 keys per thread
   __shared__ double shd[NT / 64];
   __shared__ long long shl[NT / 64];
   __shared__ int shi[NT / 64];
   __shared__ float shf[NT / 64 + 1];
-  __shared__ int s_bin[NT];
+  __shared__ int s_bin[kE2Chunk];
   __shared__ unsigned s_last;
-  __shared__ ChunkRec s_rec[NT];
+  // walker staging (structure of arrays)
+  __shared__ long long w_ibase[kWalkBatch];
+  __shared__ int w_blast[kWalkBatch], w_cnt[kWalkBatch], w_off[kWalkBatch + 1];
+  __shared__ long long w_i[kWalkBatch * kMaxSpecial];
+  __shared__ long long w_k[kWalkBatch * kMaxSpecial];
+  __shared__ float w_e[kWalkBatch * kMaxSpecial];
+  __shared__ int w_b[kWalkBatch * kMaxSpecial];
   const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int64_t j0 = (int64_t)c * kE2Chunk;
   const int n = (int)min((int64_t)kE2Chunk, (int64_t)a.nfill - j0);
@@ -289,109 +334,154 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
   for (int i = tid; i < cq; i += NT) p += (double)st[i].y * exp((double)st[i].x - (double)m);
   p = block_sum_f64<NT>(p, shd);
 
-  const bool valid = tid < n;
-  float e = 0.0f;
-  if (valid) {
-    const float v = a.score[(size_t)h * a.ld + j0 + tid] * a.scale;
-    e = exp_cr(v - m);
-    a.e[(size_t)h * a.ld + j0 + tid] = e;
+  // e for this thread's EPT consecutive keys
+  float e[EPT];
+  double loc = 0.0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int t = EPT * tid + i;
+    e[i] = 0.0f;
+    if (t < n) {
+      const float v = a.score[(size_t)h * a.ld + j0 + t] * a.scale;
+      e[i] = exp_cr(v - m);
+      st_agent(&a.e[(size_t)h * a.ld + j0 + t], e[i]);
+    }
+    loc += (double)e[i];
   }
   double tot_d;
-  const double ex = block_excl_scan<NT, double>((double)e, shd, &tot_d);
-  bool sp = false;
-  int bin = kNoBinade;
-  long long inc = 0;
-  if (valid) classify(p + ex, p + ex + (double)e, e, sp, bin, inc);
-  s_bin[tid] = bin;
-  long long tot_l;
-  const long long ipre = block_excl_scan<NT, long long>(inc, shl, &tot_l);
-  int nsp;
-  const int idx = block_excl_scan<NT, int>((valid && sp) ? 1 : 0, shi, &nsp);
-  const int last_ns = block_excl_max_scan<NT, int>((valid && !sp) ? tid : -1, -1, shi);
-  const int last_sp = block_excl_max_scan<NT, int>((valid && sp) ? tid : -1, -1, shi);
-  __syncthreads();
-  Special *spec = a.spec + ((size_t)h * a.nch + c) * kMaxSpecial;
-  if (valid && sp && idx < kMaxSpecial) {
-    Special s;
-    s.ipre = ipre;
-    s.e = e;
-    const int bprev = last_ns >= 0 ? s_bin[last_ns] : kNoBinade;
-    s.meta = tid | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16) | ((last_ns > last_sp) ? (1 << 24) : 0);
-    spec[idx] = s;
+  double ab = p + block_excl_scan<NT, double>(loc, shd, &tot_d);
+  bool sp[EPT];
+  long long inc = 0, incs[EPT];
+  int nsp_t = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int t = EPT * tid + i;
+    int bin = kNoBinade;
+    long long d = 0;
+    sp[i] = false;
+    if (t < n) classify(ab, ab + (double)e[i], e[i], sp[i], bin, d);
+    ab += (double)e[i];
+    s_bin[t] = (t < n && !sp[i]) ? bin : kNoBinade;
+    incs[i] = d;
+    inc += d;
+    nsp_t += sp[i] ? 1 : 0;
   }
-  // the chunk record: thread NT-1 sees the whole chunk through its inclusive view
-  if (tid == NT - 1) {
-    const bool me_ns = valid && !sp, me_sp = valid && sp;
-    const int lns = me_ns ? tid : last_ns, lsp = me_sp ? tid : last_sp;
+  long long tot_l;
+  long long ipre = block_excl_scan<NT, long long>(inc, shl, &tot_l);
+  int nsp;
+  int idx = block_excl_scan<NT, int>(nsp_t, shi, &nsp);
+  __syncthreads();                       // s_bin complete
+  Special *spec = a.spec + ((size_t)h * a.nch + c) * kMaxSpecial;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int t = EPT * tid + i;
+    if (t < n && sp[i]) {
+      if (idx < kMaxSpecial) {
+        Special x;
+        x.ipre = ipre;
+        x.e = e[i];
+        // binade of the step just before this one: in this chunk (non-special or kNoBinade),
+        // or 255 = "the previous chunk's last step" for the chunk's first key
+        const int bprev = t > 0 ? s_bin[t - 1] : 127;
+        x.meta = t | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+        st_spec(&spec[idx], x);
+      }
+      ++idx;
+    }
+    ipre += incs[i];
+  }
+  if (tid == 0) {
     ChunkRec r;
     r.tot = tot_l;
     r.nsp = nsp;
-    r.blast = (lns > lsp && lns >= 0) ? s_bin[lns] : kNoBinade;
-    a.rec[(size_t)h * a.nch + c] = r;
+    r.blast = s_bin[n - 1];
+    st_rec(&a.rec[(size_t)h * a.nch + c], r);
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);      // this thread's write-through stores have completed
   __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&a.counters[h], 1u) == (unsigned)(a.nch - 1) ? 1u : 0u;
+  if (tid == 0) s_last = atomicAdd(&a.counters[h * kCounterStride], 1u) == (unsigned)(a.nch - 1) ? 1u : 0u;
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
 
-  // ---- the walk (last workgroup of head h)
+  // ---- the walk (last workgroup of head h). Every field of a special is resolved in parallel -
+  // its global key index, the global increment prefix before it, the binade of the step before
+  // it - so thread 0's serial chain only carries the running sum. Segments between specials hold
+  // only non-special steps: their sum is exact integer arithmetic in units of 2^-40.
   float s = 0.0f;
-  long long seg = 0;
-  int segb = kNoBinade;
-  bool seg_has = false, ok = true;
-  for (int cb = 0; cb < a.nch && ok; cb += NT) {
-    const int nb = min(NT, a.nch - cb);
-    if (tid < nb) s_rec[tid] = a.rec[(size_t)h * a.nch + cb + tid];
+  long long i_prev = 0, k_prev = -1, ibase_run = 0;
+  int blast_prev = kNoBinade;      // blast of the chunk before the current batch
+  bool ok = true;
+  for (int cb = 0; cb < a.nch && ok; cb += kWalkBatch) {
+    const int nb = min(kWalkBatch, a.nch - cb);
+    long long tot = 0;
+    int cnt = 0;
+    if (tid < nb) {
+      const ChunkRec r = ld_rec(&a.rec[(size_t)h * a.nch + cb + tid]);
+      tot = r.tot;
+      cnt = r.nsp;
+      w_blast[tid] = r.blast;
+    }
+    long long tsum;
+    const long long ib = ibase_run + block_excl_scan<NT, long long>(tid < nb ? tot : 0, shl, &tsum);
+    int csum;
+    const int off = block_excl_scan<NT, int>(tid < nb ? min(cnt, kMaxSpecial) : 0, shi, &csum);
+    if (tid < nb) {
+      w_ibase[tid] = ib;
+      w_cnt[tid] = cnt;
+      w_off[tid] = off;
+    }
+    if (tid == 0) w_off[nb] = csum;
     __syncthreads();
-    if (tid == 0) {
-      for (int cc = 0; cc < nb && ok; ++cc) {
-        const ChunkRec r = s_rec[cc];
-        if (r.nsp > kMaxSpecial) { ok = false; break; }
-        const Special *sp2 = a.spec + ((size_t)h * a.nch + cb + cc) * kMaxSpecial;
-        long long prev = 0;
-        for (int j = 0; j < r.nsp; ++j) {
-          const Special x = sp2[j];
-          seg += x.ipre - prev;
-          prev = x.ipre;
-          if (x.meta & (1 << 24)) {
-            segb = ((x.meta >> 16) & 0xFF) - 128;
-            seg_has = true;
-          }
-          if (seg_has) {
-            long long u;
-            if (!to_units(s, segb, u) || !from_units(u + seg, segb, s)) { ok = false; break; }
-          } else if (seg != 0) { ok = false; break; }
-          seg = 0;
-          seg_has = false;
-          s = __fadd_rn(s, x.e);
-        }
-        seg += r.tot - prev;
-        if (r.blast != kNoBinade) {
-          segb = r.blast;
-          seg_has = true;
-        }
+    for (int i = tid; i < nb * kMaxSpecial; i += NT) {
+      const int cc = i / kMaxSpecial, j = i % kMaxSpecial;
+      if (j < min(w_cnt[cc], kMaxSpecial)) {
+        const Special x = ld_spec(&a.spec[((size_t)h * a.nch + cb + cc) * kMaxSpecial + j]);
+        const int o = w_off[cc] + j, pos = x.meta & 0xFFFF, bf = (x.meta >> 16) & 0xFF;
+        int bprev;
+        if (bf == 255) bprev = cc > 0 ? w_blast[cc - 1] : blast_prev;
+        else bprev = bf == 0 ? kNoBinade : bf - 128;
+        w_i[o] = w_ibase[cc] + x.ipre;
+        w_k[o] = (long long)(cb + cc) * kE2Chunk + pos;
+        w_e[o] = x.e;
+        w_b[o] = bprev;
       }
     }
     __syncthreads();
-    if (tid == 0) s_last = ok ? 1u : 0u;
+    if (tid == 0) {
+      for (int cc = 0; cc < nb && ok; ++cc) {
+        if (w_cnt[cc] > kMaxSpecial) { ok = false; break; }   // handled by the serial fallback
+      }
+      for (int o = 0; o < csum && ok; ++o) {
+        const long long kk = w_k[o], ii = w_i[o];
+        if (kk - k_prev > 1) {                   // a segment of non-special steps precedes it
+          long long u;
+          if (!to_units(s, w_b[o], u) || !from_units(u + (ii - i_prev), w_b[o], s)) { ok = false; break; }
+        } else if (ii != i_prev) { ok = false; break; }
+        s = __fadd_rn(s, w_e[o]);
+        k_prev = kk;
+        i_prev = ii;
+      }
+      s_last = ok ? 1u : 0u;
+    }
     __syncthreads();
     ok = s_last != 0;
+    ibase_run += tsum;
+    blast_prev = w_blast[nb - 1];
+    __syncthreads();
   }
-  if (tid == 0 && ok && seg_has) {
+  if (tid == 0 && ok && (int64_t)a.nfill - 1 - k_prev > 0) {   // the trailing segment
     long long u;
-    if (!to_units(s, segb, u) || !from_units(u + seg, segb, s)) ok = false;
+    if (!to_units(s, blast_prev, u) || !from_units(u + (ibase_run - i_prev), blast_prev, s)) ok = false;
   }
   if (tid == 0) s_last = ok ? 1u : 0u;
   __syncthreads();
   if (!s_last) {
-    // fallback: the serial loop itself, 256 terms staged in LDS at a time
-    float *stage = reinterpret_cast<float *>(s_rec);
+    // fallback: the serial loop itself, NT terms staged in LDS at a time
+    float *stage = w_e;
     float ss = 0.0f;
     for (int64_t b0 = 0; b0 < a.nfill; b0 += NT) {
       const int nb = (int)min((int64_t)NT, (int64_t)a.nfill - b0);
-      if (tid < nb) stage[tid] = a.e[(size_t)h * a.ld + b0 + tid];
+      if (tid < nb) stage[tid] = ld_agent(&a.e[(size_t)h * a.ld + b0 + tid]);
       __syncthreads();
       if (tid == 0)
         for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, stage[i]);
@@ -470,22 +560,29 @@ __global__ __launch_bounds__(256) void pv_kernel(PvArgs a) {
     for (int i = 0; i < R::EPL; ++i) acc[h][i] = 0.0f;
 
   const LayerView &L = a.L;
-  constexpr int RB = row_bytes(VF);
-  for (int jb = wave * R::KPW; jb < n; jb += 4 * R::KPW) {
-    const int jl = jb + kk;
-    const bool valid = jl < n;
-    const int64_t slot = slot_of(L, j0 + (valid ? jl : 0));
-    const uint4 w = *reinterpret_cast<const uint4 *>(L.vd + (slot * a.nkv + g) * RB + sub * 16);
-    float vsc = 1.0f;
-    if (VF == BKV_Q8_0) {
-      const uint32_t sw = *reinterpret_cast<const uint32_t *>(L.vs + (slot * a.nkv + g) * kScaleRowBytes +
-                                                              (sub >> 2) * 4);
-      vsc = f16_to_f32(((sub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-    }
-    float p[kGqa];
+  constexpr int RB = row_bytes(VF), U = 4, STEP = 4 * R::KPW;   // keys per workgroup step
+  for (int jb = wave * R::KPW; jb < n; jb += STEP * U) {
+    uint4 w[U];
+    uint32_t sw[U];
+    int jl[U];
 #pragma unroll
-    for (int h = 0; h < kGqa; ++h) p[h] = valid ? s_p[h][jl] : 0.0f;
-    v_accum<VF>(w, vsc, p, acc);
+    for (int u = 0; u < U; ++u) {                 // all U row loads in flight before any FMA
+      jl[u] = jb + u * STEP + kk;
+      const int64_t slot = slot_of(L, j0 + (jl[u] < n ? jl[u] : 0));
+      w[u] = *reinterpret_cast<const uint4 *>(L.vd + (slot * a.nkv + g) * RB + sub * 16);
+      if (VF == BKV_Q8_0)
+        sw[u] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * a.nkv + g) * kScaleRowBytes + (sub >> 2) * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = jl[u] < n;
+      float vsc = 1.0f;
+      if (VF == BKV_Q8_0) vsc = f16_to_f32(((sub >> 1) & 1) ? (sw[u] >> 16) : (sw[u] & 0xFFFFu));
+      float p[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) p[h] = valid ? s_p[h][jl[u]] : 0.0f;
+      v_accum<VF>(w[u], vsc, p, acc);
+    }
   }
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)

@@ -11,23 +11,24 @@
 namespace bkv {
 
 // ------------------------------------------------------------------ decode geometry
-constexpr int kE2Chunk = 256;      // keys per workgroup of the probability kernel
-constexpr int kMaxSpecial = 32;    // exactly-added steps recorded per probability chunk
+constexpr int kE2Chunk = 1024;     // keys per workgroup of the probability kernel
+constexpr int kMaxSpecial = 64;    // exactly-added steps recorded per probability chunk
 constexpr int kPvMaxChunk = 512;   // keys per PV partition held in LDS
+constexpr int kCounterStride = 64; // u32 words between per-head arrival counters (own 256 B line)
 
 // one probability chunk's contribution to the exact serial softmax sum
 struct ChunkRec {
   long long tot;      // sum of the non-special increments, units of 2^-40
   int nsp;            // specials recorded (> kMaxSpecial: overflow)
-  int blast;          // binade of the last non-special step after the last special, or kNoBinade
+  int blast;          // binade of the chunk's last step, kNoBinade if that step is special
 };
 // one step the walker adds in fp32 exactly as the serial loop does
 struct Special {
   long long ipre;     // increments of the chunk's non-special steps before it, units of 2^-40
   float e;            // the term added
-  int meta;           // bits 0..15: position in chunk; bits 16..23: binade+128 of the last
-                      // non-special step before it in the chunk (0 = none); bit 24: a
-                      // non-special step lies between it and the previous special of the chunk
+  int meta;           // bits 0..15: position in chunk; bits 16..23: binade+128 of the step
+                      // just before it (0 = that step is special, 255 = it is the previous
+                      // chunk's last step)
 };
 constexpr int kNoBinade = -1000;
 

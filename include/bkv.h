@@ -120,6 +120,14 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
  * pos0 + n_q, the chunk is bounded by BKV_PREFILL_MAX_Q). Returns 0 on a bad descriptor.      */
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx);
 
+/* Diagnostics (no counterpart in the reference; for parity tests and profiling): where a decode of
+ * nfill keys keeps its intermediates inside the workspace. out[0] = row stride ld (floats),
+ * out[1] = offset of the scores [nh][ld] fp32, out[2] = offset of e_j = exp(s_j*scale - max)
+ * [nh][ld] fp32, out[3] = offset of the exact serial softmax sums [nh] fp32, out[4] = offset of the
+ * walker status [nh] u32 (1 = the exact walk fell back to the serial loop), out[5] = workspace
+ * bytes needed. Returns BKV_OK or an error for a bad descriptor. */
+int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]);
+
 /* Human-readable text of an enum bkv_err value (static storage). */
 const char *bkv_strerror(int err);
 

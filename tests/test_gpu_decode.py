@@ -107,3 +107,43 @@ def test_deterministic_repeat():
     o2, _ = dev.decode(0, n, qt)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("kf,vf,n,seed", [(BKV_Q8_0, BKV_Q8_0, 4097, 1), (BKV_F16, BKV_F16, 3000, 7),
+                                          (BKV_Q8_0, BKV_Q8_0, 40000, 2)])
+def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed):
+    """The intermediates the reference's bitwise gate (BONSAI_QCHECK stages A/B) compares: every score,
+    every e_j = exp(s_j*scale - max) and the serial fp32 softmax sum match the oracle bit for bit, and
+    so do the fp16 probabilities formed from them."""
+    say(f"bit-exact intermediates kf={kf} n={n}")
+    dev, host = pair(1, n, kf, vf)
+    fill(dev, host, 0, n, seed=seed)
+    q, _ = qg(seed, 0)
+    want, _, sc, pr, p16 = host.decode(0, n, q, debug=True, nthreads=8)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    score, e, ssum, status = dev.debug_intermediates(n)
+    assert oracle.bit_diff(score.numpy(), sc) == 0
+    assert int(status.sum()) == 0, "the exact walk fell back to the serial loop"
+    p_gpu = (e.numpy() / ssum.numpy()[:, None]).astype(np.float32)
+    assert oracle.bit_diff(p_gpu, pr) == 0
+    assert np.array_equal(oracle.f32_to_f16(p_gpu), p16)
+    assert report("out", out.cpu().numpy(), want) <= TOL
+
+
+def test_identical_keys_uniform_attention():
+    """All scores equal: every e_j = 1 and the serial sum is exactly n; p = 1/n in fp16."""
+    n = 5000
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    k1, _ = oracle.synth_kv(1, 4, 256, 9, 0)
+    _, v = oracle.synth_kv(n, 4, 256, 9, 1)
+    k = np.repeat(k1, n, axis=0)
+    host.append(0, 0, k, v)
+    dev.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    q, _ = qg(9, 0)
+    want, _ = host.decode(0, n, q)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    _, e, ssum, status = dev.debug_intermediates(n)
+    assert torch.all(e == 1.0) and torch.all(ssum == float(n)) and int(status.sum()) == 0
+    assert report("uniform", out.cpu().numpy(), want) <= TOL
