@@ -51,6 +51,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
   p.off_cnt = o;    o += align256((size_t)nh * kCounterStride * sizeof(unsigned));
   p.off_sum = o;    o += align256((size_t)nh * sizeof(float));
   p.off_status = o; o += align256((size_t)nh * sizeof(unsigned));
+  p.off_dbg = o;    o += align256((size_t)nh * 8 * sizeof(unsigned long long));
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
   p.total = o;
   return p;
@@ -151,6 +152,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   ea.counters = qa.counters;
   ea.sum = (float *)(w + p.off_sum);
   ea.status = (unsigned *)(w + p.off_status);
+  ea.dbg = (unsigned long long *)(w + p.off_dbg);
   PvArgs pa{};
   pa.L = L; pa.nkv = d->nkv; pa.nh = d->nh; pa.nfill = nfill; pa.chunk = p.pv_chunk;
   pa.nch = p.nch_pv; pa.ld = p.ld; pa.e = ea.e; pa.sum = ea.sum;

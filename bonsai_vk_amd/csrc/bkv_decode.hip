@@ -92,6 +92,10 @@ __global__ __launch_bounds__(64) void append_kernel(AppendArgs a) {
 // d%16, so the shared operand costs no LDS or scalar traffic.
 template <int N>
 __device__ __forceinline__ void fmac_bc(float &acc, float q, float k) {
+#ifdef BKV_EXPERIMENT_NODPP
+  acc = fmaf(q, k, acc);
+  return;
+#endif
   asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
       : "+v"(acc)
       : "v"(q), "v"(k), "n"(N));
@@ -255,17 +259,18 @@ __device__ __forceinline__ void classify(double abefore, double aafter, float e,
   inc = (long long)rint(t) << (B + 17);
 }
 
-__device__ __forceinline__ bool to_units(float s, int B, long long &u) {
-  if (!(s >= ldexpf(1.0f, B) && s < ldexpf(1.0f, B + 1))) return false;
-  u = (long long)ldexp((double)s, 40);
-  return true;
-}
-__device__ __forceinline__ bool from_units(long long u, int B, float &s) {
-  const double d = ldexp((double)u, -40);
-  const float f = (float)d;
-  if ((double)f != d || (long long)ldexp((double)f, 40) != u) return false;
-  if (!(f >= ldexpf(1.0f, B) && f < ldexpf(1.0f, B + 1))) return false;
-  s = f;
+// Advance a running sum s that lies in binade B by du units of 2^-40 (a multiple of that binade's
+// ulp 2^(B-23)), in integer arithmetic on the float's significand. False when s is not in binade B,
+// du is not a whole number of ulps, or the result leaves the binade - an assumption of the
+// classification failed, and the caller falls back to the serial loop.
+__device__ __forceinline__ bool advance(float &s, int B, long long du) {
+  const uint32_t bits = __float_as_uint(s);
+  if (B < -17 || B > 22 || (int)(bits >> 23) != B + 127) return false;
+  const int sh = B + 17;
+  if (du < 0 || (du & ((1ll << sh) - 1)) != 0) return false;
+  const long long m = (long long)((bits & 0x7FFFFFu) | 0x800000u) + (du >> sh);
+  if (m >= (1ll << 24)) return false;
+  s = __uint_as_float(((uint32_t)(B + 127) << 23) | ((uint32_t)m & 0x7FFFFFu));
   return true;
 }
 
@@ -306,6 +311,11 @@ __device__ __forceinline__ Special ld_spec(const Special *p) {
   return x;
 }
 
+#ifdef BKV_EXPERIMENT_TS
+#define TS(i) do { if (tid == 0) a.dbg[h * 8 + (i)] = wall_clock64(); } while (0)
+#else
+#define TS(i) do { } while (0)
+#endif
 __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
   constexpr int NT = 256, EPT = kE2Chunk / NT;       // 4 keys per thread
   __shared__ double shd[NT / 64];
@@ -321,10 +331,14 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
   __shared__ long long w_k[kWalkBatch * kMaxSpecial];
   __shared__ float w_e[kWalkBatch * kMaxSpecial];
   __shared__ int w_b[kWalkBatch * kMaxSpecial];
+  __shared__ int w_du[kWalkBatch * kMaxSpecial];
   const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int64_t j0 = (int64_t)c * kE2Chunk;
   const int n = (int)min((int64_t)kE2Chunk, (int64_t)a.nfill - j0);
   const float2 *st = a.stats + (size_t)h * a.nch_qk;
+#ifdef BKV_EXPERIMENT_TS
+  if (tid == 0 && c == 0) a.dbg[h * 8 + 5] = wall_clock64();
+#endif
 
   float m = -INFINITY;
   for (int i = tid; i < a.nch_qk; i += NT) m = fmaxf(m, st[i].x);
@@ -397,11 +411,19 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
     r.blast = s_bin[n - 1];
     st_rec(&a.rec[(size_t)h * a.nch + c], r);
   }
+#ifdef BKV_EXPERIMENT_NOWALK
+  return;
+#endif
   __builtin_amdgcn_s_waitcnt(0);      // this thread's write-through stores have completed
   __syncthreads();
   if (tid == 0) s_last = atomicAdd(&a.counters[h * kCounterStride], 1u) == (unsigned)(a.nch - 1) ? 1u : 0u;
   __syncthreads();
   if (!s_last) return;
+  TS(0);
+#ifdef BKV_EXPERIMENT_NOWALK2
+  if (tid == 0) { a.sum[h] = 1.0f; a.status[h] = 0; }
+  return;
+#endif
 
   // ---- the walk (last workgroup of head h). Every field of a special is resolved in parallel -
   // its global key index, the global increment prefix before it, the binade of the step before
@@ -432,46 +454,89 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
     }
     if (tid == 0) w_off[nb] = csum;
     __syncthreads();
-    for (int i = tid; i < nb * kMaxSpecial; i += NT) {
-      const int cc = i / kMaxSpecial, j = i % kMaxSpecial;
-      if (j < min(w_cnt[cc], kMaxSpecial)) {
-        const Special x = ld_spec(&a.spec[((size_t)h * a.nch + cb + cc) * kMaxSpecial + j]);
-        const int o = w_off[cc] + j, pos = x.meta & 0xFFFF, bf = (x.meta >> 16) & 0xFF;
-        int bprev;
-        if (bf == 255) bprev = cc > 0 ? w_blast[cc - 1] : blast_prev;
-        else bprev = bf == 0 ? kNoBinade : bf - 128;
-        w_i[o] = w_ibase[cc] + x.ipre;
-        w_k[o] = (long long)(cb + cc) * kE2Chunk + pos;
-        w_e[o] = x.e;
-        w_b[o] = bprev;
+    TS(1);
+    // one special per thread: its chunk by binary search over the offsets, then a single load
+    for (int o = tid; o < csum; o += NT) {
+      int lo = 0, hi = nb - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (w_off[mid] <= o) lo = mid; else hi = mid - 1;
       }
+      const int cc = lo, j = o - w_off[cc];
+      const Special x = ld_spec(&a.spec[((size_t)h * a.nch + cb + cc) * kMaxSpecial + j]);
+      const int pos = x.meta & 0xFFFF, bf = (x.meta >> 16) & 0xFF;
+      int bprev;
+      if (bf == 255) bprev = cc > 0 ? w_blast[cc - 1] : blast_prev;
+      else bprev = bf == 0 ? kNoBinade : bf - 128;
+      w_i[o] = w_ibase[cc] + x.ipre;
+      w_k[o] = (long long)(cb + cc) * kE2Chunk + pos;
+      w_e[o] = x.e;
+      w_b[o] = bprev;
     }
     __syncthreads();
-    if (tid == 0) {
-      for (int cc = 0; cc < nb && ok; ++cc) {
-        if (w_cnt[cc] > kMaxSpecial) { ok = false; break; }   // handled by the serial fallback
+    TS(2);
+    // per special, in parallel: the segment before it as a whole number of ulps of its binade
+    // (du < 0: empty segment), checked for divisibility; any overflowed chunk forces the fallback
+    bool bad = false;
+    for (int o = tid; o < csum; o += NT) {
+      const long long di = w_i[o] - (o > 0 ? w_i[o - 1] : i_prev);
+      const long long gap = w_k[o] - (o > 0 ? w_k[o - 1] : k_prev);
+      int du = -1;
+      if (gap > 1) {
+        const int B = w_b[o];
+        if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24))
+          bad = true;
+        else
+          du = (int)(di >> (B + 17));
+      } else if (di != 0) {
+        bad = true;
       }
-      for (int o = 0; o < csum && ok; ++o) {
-        const long long kk = w_k[o], ii = w_i[o];
-        if (kk - k_prev > 1) {                   // a segment of non-special steps precedes it
-          long long u;
-          if (!to_units(s, w_b[o], u) || !from_units(u + (ii - i_prev), w_b[o], s)) { ok = false; break; }
-        } else if (ii != i_prev) { ok = false; break; }
-        s = __fadd_rn(s, w_e[o]);
-        k_prev = kk;
-        i_prev = ii;
+      w_du[o] = du;
+    }
+    for (int cc = tid; cc < nb; cc += NT) bad |= w_cnt[cc] > kMaxSpecial;
+    if (__syncthreads_or(bad)) ok = false;
+    TS(6);
+#ifdef BKV_EXPERIMENT_TS
+    if (tid == 0) a.dbg[h * 8 + 7] = csum;
+#endif
+    if (tid < 64) {
+      // the serial chain on wave 0: lane i holds special base+i; the chain itself is wave-uniform
+      // (readlane), so it runs on the scalar unit except for the one fp32 add per special.
+      const int lane = tid;
+      bool good = ok;
+      for (int base = 0; base < csum; base += 64) {
+        const int o = base + lane;
+        const int du_l = o < csum ? w_du[o] : -1, b_l = o < csum ? w_b[o] : 0;
+        const float e_l = o < csum ? w_e[o] : 0.0f;
+        const int cnt = min(64, csum - base);
+        for (int i = 0; i < cnt; ++i) {
+          const int du = __builtin_amdgcn_readlane(du_l, i);
+          const int b = __builtin_amdgcn_readlane(b_l, i);
+          const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), i));
+          if (du >= 0) {
+            const uint32_t bits = __float_as_uint(s);
+            const uint32_t m = ((bits & 0x7FFFFFu) | 0x800000u) + (uint32_t)du;
+            good = good && (int)(bits >> 23) == b + 127 && m < (1u << 24);
+            s = __uint_as_float(((uint32_t)(b + 127) << 23) | (m & 0x7FFFFFu));
+          }
+          s = __fadd_rn(s, ev);
+        }
       }
-      s_last = ok ? 1u : 0u;
+      if (tid == 0) s_last = good ? 1u : 0u;
     }
     __syncthreads();
+    if (csum > 0) {                              // every thread carries the last special forward
+      k_prev = w_k[csum - 1];
+      i_prev = w_i[csum - 1];
+    }
+    TS(3);
     ok = s_last != 0;
     ibase_run += tsum;
     blast_prev = w_blast[nb - 1];
     __syncthreads();
   }
   if (tid == 0 && ok && (int64_t)a.nfill - 1 - k_prev > 0) {   // the trailing segment
-    long long u;
-    if (!to_units(s, blast_prev, u) || !from_units(u + (ibase_run - i_prev), blast_prev, s)) ok = false;
+    if (!advance(s, blast_prev, ibase_run - i_prev)) ok = false;
   }
   if (tid == 0) s_last = ok ? 1u : 0u;
   __syncthreads();
@@ -493,6 +558,7 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
     a.sum[h] = s;
     a.status[h] = s_last ? 0u : 1u;
   }
+  TS(4);
 }
 
 // ------------------------------------------------------------------ PV over the fp16 probabilities

@@ -67,6 +67,7 @@ struct EArgs {
   unsigned *counters;            // [nh]
   float *sum;                    // [nh] the exact serial sum
   unsigned *status;              // [nh] 1 when the walker fell back to the serial loop
+  unsigned long long *dbg;       // [nh][8] phase timestamps of the walker (experiment builds)
 };
 
 struct PvArgs {
@@ -91,7 +92,7 @@ struct RedArgs {
 struct DecodePlan {
   int qk_chunk, nch_qk, nch_e, pv_chunk, nch_pv;
   int64_t ld;
-  size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_part,
+  size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_dbg, off_part,
       total;
 };
 
