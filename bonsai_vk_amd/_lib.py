@@ -19,7 +19,7 @@ ERRORS = {
 EXPORTS = [
     "bkv_geom_check", "bkv_slot_bytes", "bkv_max_positions", "bkv_kv_append", "bkv_attn_decode",
     "bkv_decode_step", "bkv_attn_prefill_chunk", "bkv_workspace_bytes", "bkv_strerror",
-    "bkv_last_hip_error", "bkv_version", "bkv_debug_layout",
+    "bkv_last_hip_error", "bkv_version", "bkv_debug_layout", "bkv_workspace_init", "bkv_decode_path",
 ]
 
 
@@ -72,6 +72,8 @@ def lib():
         "bkv_last_hip_error": (ctypes.c_char_p, []),
         "bkv_version": (ctypes.c_char_p, []),
         "bkv_debug_layout": (i32, [D, u32, ctypes.POINTER(ctypes.c_uint64)]),
+        "bkv_workspace_init": (i32, [D, P, sz, P]),
+        "bkv_decode_path": (i32, [D, u32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

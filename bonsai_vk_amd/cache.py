@@ -123,6 +123,8 @@ class KvCache:
         self.max_ctx = max_ctx or self.max_positions
         ws = lib().bkv_workspace_bytes(ctypes.byref(d), BKV_OP_DECODE, self.max_ctx)
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=self.device)
+        check(lib().bkv_workspace_init(ctypes.byref(d), self.workspace.data_ptr(), ws, self._stream()),
+              "bkv_workspace_init")
 
     # ---------------------------------------------------------------- helpers
     @staticmethod
@@ -194,7 +196,13 @@ class KvCache:
         need = lib().bkv_workspace_bytes(ctypes.byref(self.desc), BKV_OP_PREFILL, max_ctx)
         if getattr(self, "_pws", None) is None or self._pws.numel() < need:
             self._pws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            check(lib().bkv_workspace_init(ctypes.byref(self.desc), self._pws.data_ptr(), need,
+                                           self._stream()), "bkv_workspace_init")
         return self._pws
+
+    def decode_path(self, nfill):
+        """1: fused single launch, 0: split path"""
+        return lib().bkv_decode_path(ctypes.byref(self.desc), nfill)
 
     # ---------------------------------------------------------------- inspection
     def debug_intermediates(self, nfill):
@@ -206,7 +214,7 @@ class KvCache:
         ws = self.workspace
         f = lambda off, n: ws[off:off + 4 * n].view(torch.float32)
         nh = self.nh
-        score = f(o_s, nh * ld).view(nh, ld)[:, :nfill].cpu()
+        score = f(o_s, nh * ld).view(nh, ld)[:, :nfill].cpu() if o_s else None
         e = f(o_e, nh * ld).view(nh, ld)[:, :nfill].cpu()
         ssum = f(o_sum, nh).cpu()
         status = ws[o_st:o_st + 4 * nh].view(torch.int32).cpu()

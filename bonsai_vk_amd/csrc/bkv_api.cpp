@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/bkv.h"
@@ -32,7 +33,13 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // chunks: 256 keys. PV: enough workgroups to cover the chip (512 at nkv = 4) with 16..512 keys each.
 // Every array is sized by a bound that grows monotonically with n, so a workspace sized for max_ctx
 // fits every n <= max_ctx.
-DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
+// BKV_DECODE=split selects the four-launch path (read on every call, so tests can switch it)
+static bool force_split() {
+  const char *e = std::getenv("BKV_DECODE");
+  return e && std::strcmp(e, "split") == 0;
+}
+
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
   DecodePlan p;
   p.qk_chunk = qk_keys_per_wg(kfmt);
   p.nch_qk = (int)cdiv(n, p.qk_chunk);
@@ -42,7 +49,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
   p.ld = cdiv(n, kE2Chunk) * kE2Chunk;
   const int64_t nq_bound = cdiv(n, 128);
   const int64_t np_bound = std::max<int64_t>(128, cdiv(n, kPvMaxChunk));
-  size_t o = 0;
+  size_t o = kSyncBytes;
   p.off_score = o;  o += align256((size_t)nh * p.ld * sizeof(float));
   p.off_e = o;      o += align256((size_t)nh * p.ld * sizeof(float));
   p.off_stats = o;  o += align256((size_t)nh * nq_bound * sizeof(float2));
@@ -53,7 +60,31 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t n) {
   p.off_status = o; o += align256((size_t)nh * sizeof(unsigned));
   p.off_dbg = o;    o += align256((size_t)nh * 8 * sizeof(unsigned long long));
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
-  p.total = o;
+  size_t total = o;
+  // the fused single-launch path: as many 256-key workgroups per KV group as stay resident
+  const int cap = fused_max_workgroups(kfmt, vfmt);
+  p.gg = 0;
+  p.rsub = 0;
+  if (cap >= nkv) {
+    const int64_t rs = cdiv(n, (int64_t)(cap / nkv) * 256);
+    const int64_t gg = cdiv(n, rs * 256);          // no workgroup without keys
+    if (rs <= kRMax) {
+      p.gg = (int)gg;
+      p.rsub = (int)rs;
+      size_t f = kSyncBytes;
+      p.f_stats = f;  f += align256((size_t)nh * gg * sizeof(float2));
+      p.f_sub = f;    f += align256((size_t)nkv * 8 * kGqa * kHd * sizeof(float));
+      p.f_rec = f;    f += align256((size_t)nh * gg * sizeof(ChunkRec));
+      p.f_spec = f;   f += align256((size_t)nh * gg * kMaxSpecial * sizeof(Special));
+      p.f_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
+      p.f_sum = f;    f += align256((size_t)nh * sizeof(float));
+      p.f_status = f; f += align256((size_t)nh * sizeof(unsigned));
+      p.f_part = f;   f += align256((size_t)nkv * gg * kGqa * kHd * sizeof(float));
+      p.f_total = f;
+      total = std::max(total, f);
+    }
+  }
+  p.total = total;
   return p;
 }
 
@@ -131,10 +162,32 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if ((gate == nullptr) != (out_gated == nullptr)) return BKV_EINVAL;
   if (!ws) return BKV_EWORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return BKV_EALIGN;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, nfill);
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
   if (ws_bytes < p.total) return BKV_EWORKSPACE;
   char *w = (char *)ws;
   const LayerView L = view(d, layer);
+
+  if (p.gg > 0 && !force_split()) {
+    FusedArgs fa{};
+    fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub;
+    fa.ld = p.ld; fa.q = q;
+    if (fused) fa.ap = *fused;
+    fa.gate = gate; fa.out = out; fa.out_gated = out_gated;
+    fa.stats = (float2 *)(w + p.f_stats);
+    fa.mxenc = (unsigned *)(w + kSyncMaxOffset);   // fixed: the slots outlive a call
+    fa.nh = d->nh;
+    fa.subpart = (float *)(w + p.f_sub);
+    fa.rec = (ChunkRec *)(w + p.f_rec);
+    fa.spec = (Special *)(w + p.f_spec);
+    fa.e = (float *)(w + p.f_e);
+    fa.sum = (float *)(w + p.f_sum);
+    fa.status = (unsigned *)(w + p.f_status);
+    fa.part = (float *)(w + p.f_part);
+    fa.sync = (unsigned *)w;
+    const hipError_t e = launch_fused(fa, d->k_fmt, d->v_fmt, fused != nullptr, st);
+    if (e == hipSuccess) return BKV_OK;
+    (void)hipGetLastError();           // e.g. a cooperative grid the device cannot hold: split path
+  }
 
   QkArgs qa{};
   qa.L = L; qa.nkv = d->nkv; qa.nfill = nfill; qa.nch = p.nch_qk; qa.ld = p.ld; qa.scale = d->scale;
@@ -247,7 +300,7 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
   if (check(d) || max_ctx == 0) return 0;
   if (op != BKV_OP_DECODE && op != BKV_OP_PREFILL) return 0;
-  return plan_decode(d->nh, d->nkv, d->k_fmt, max_ctx).total;
+  return plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total;
 }
 
 const char *bkv_strerror(int err) {
@@ -268,14 +321,30 @@ int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
   const int rc = check(d);
   if (rc) return rc;
   if (!out || nfill == 0) return BKV_EINVAL;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, nfill);
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
+  const bool fz = p.gg > 0 && !force_split();
   out[0] = (uint64_t)p.ld;
-  out[1] = p.off_score;
-  out[2] = p.off_e;
-  out[3] = p.off_sum;
-  out[4] = p.off_status;
+  out[1] = fz ? 0 : p.off_score;
+  out[2] = fz ? p.f_e : p.off_e;
+  out[3] = fz ? p.f_sum : p.off_sum;
+  out[4] = fz ? p.f_status : p.off_status;
   out[5] = p.total;
   return BKV_OK;
+}
+
+int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  const int rc = check(d);
+  if (rc) return rc;
+  if (!workspace) return BKV_EWORKSPACE;
+  if (((uintptr_t)workspace & 255u) != 0) return BKV_EALIGN;
+  if (ws_bytes < kSyncBytes) return BKV_EWORKSPACE;
+  return hip_fail(launch_workspace_init((unsigned *)workspace, (int)(kSyncBytes / sizeof(unsigned)), stream));
+}
+
+int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill) {
+  if (check(d) || nfill == 0) return -1;
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
+  return (p.gg > 0 && !force_split()) ? 1 : 0;
 }
 
 const char *bkv_last_hip_error(void) { return g_hip_err; }

@@ -198,3 +198,32 @@ __device__ __forceinline__ double block_sum_f64(double v, double *sh) {
 }
 
 }  // namespace bkv
+
+namespace bkv {
+// K independent exclusive prefix sums over the workgroup at once; tot[k] receives the totals.
+// sh: (NT/64)*K scratch slots.
+template <int NT, int K, typename T>
+__device__ __forceinline__ void block_excl_scan_k(const T (&v)[K], T (&ex)[K], T (&tot)[K], T *sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  T inc[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) inc[k] = wave_incl_scan(v[k], lane);
+  if (lane == 63)
+#pragma unroll
+    for (int k = 0; k < K; ++k) sh[w * K + k] = inc[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    T base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) {
+      const T x = sh[i * K + k];
+      if (i < w) base += x;
+      t += x;
+    }
+    ex[k] = base + inc[k] - v[k];
+    tot[k] = t;
+  }
+  __syncthreads();
+}
+}  // namespace bkv

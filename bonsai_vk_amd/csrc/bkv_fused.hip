@@ -1,0 +1,593 @@
+// bkv_fused.hip - one cooperative launch per layer and decode token: append, QK in the reference's
+// order, the exact serial softmax sum, PV over fp16 probabilities and the partition merge.
+//
+// Workgroup w serves KV group g = w % nkv and keys [wi*R*256, (wi+1)*R*256) with wi = w / nkv, in R
+// sub-chunks of 256 keys (one key per thread). The phases that need every workgroup of a group are
+// joined by arrival counters: a workgroup counts itself in, the last one to arrive does the phase's
+// group-wide step (global max; the walk to the exact sum; nothing for the merge) and raises the
+// phase flag, and every workgroup waits for the flag only after it has arrived itself. The launch is
+// cooperative, so all workgroups are resident and every wait is reached by its producers; each wait
+// is also bounded and records an error word instead of hanging.
+// While a workgroup waits for the exact sum, the first V sub-chunk is already in its registers.
+#include "bkv_common.h"
+#include "bkv_device.h"
+#include "bkv_internal.h"
+
+namespace bkv {
+
+constexpr unsigned kSpinLimit = 1u << 24;
+
+// float <-> unsigned with the same order (for atomicMax); 0 orders below every float
+__device__ __forceinline__ unsigned ordered_bits(float f) {
+  const unsigned u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_ordered_bits(unsigned o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+__device__ __forceinline__ void st_f2(float2 *p, float2 v) {
+  st_agent(reinterpret_cast<unsigned long long *>(p),
+           (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)__float_as_uint(v.y) << 32));
+}
+__device__ __forceinline__ float2 ld_f2(const float2 *p) {
+  const unsigned long long u = ld_agent(reinterpret_cast<const unsigned long long *>(p));
+  return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+
+// Arrival of workgroup idx of n at a phase. Counting is two-level to keep same-address atomics
+// short: idx goes to sub-counter idx % 8, and the last arrival of each sub-group counts into the main
+// counter. Each counter is reset by its last arrival, ready for the next call. Returns true (in every
+// thread) for the overall last arrival.
+constexpr int kSub = 8;
+__device__ __forceinline__ bool arrive(unsigned *cnt, unsigned *sub, int idx, int n, unsigned *sh) {
+  __builtin_amdgcn_s_waitcnt(0);           // this thread's write-through stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int k = idx % kSub, members = (n - k + kSub - 1) / kSub, nsub = n < kSub ? n : kSub;
+    unsigned last = 0u;
+    if (atomicAdd(sub + k * kCounterStride, 1u) == (unsigned)(members - 1)) {
+      st_agent(sub + k * kCounterStride, 0u);
+      if (atomicAdd(cnt, 1u) == (unsigned)(nsub - 1)) {
+        st_agent(cnt, 0u);
+        last = 1u;
+      }
+    }
+    *sh = last;
+  }
+  __syncthreads();
+  return *sh != 0;
+}
+// the last arrival raises the phase flag after its own stores completed
+__device__ __forceinline__ void publish(unsigned *flag, unsigned gen) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) st_agent(flag, gen);
+}
+__device__ __forceinline__ void wait_flag(const unsigned *flag, unsigned gen, unsigned *err) {
+  if (threadIdx.x == 0) {
+    unsigned spins = 0;
+    while (ld_agent(flag) != gen) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > kSpinLimit) {
+        atomicOr(err, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- the walk of one head (one wave)
+// Records rec[c] / specials spec[c][..] of the group's workgroups in key order, each covering kpw
+// keys. The fields of every special (global key index, global increment prefix, binade of the step
+// before it, the whole ulps of the segment before it) are resolved in parallel across the wave into
+// LDS; the serial chain then only carries the running sum (wave-uniform, readlane per special).
+constexpr int kWalkWg = 128;       // workgroups per group the scratch holds
+constexpr int kWalkCap = 384;      // specials per head the scratch holds (more: serial fallback)
+struct WalkScratch {
+  long long wg_ib[kWalkWg];
+  int wg_off[kWalkWg + 1], wg_bp[kWalkWg];
+  long long sk[kWalkCap], si[kWalkCap];
+  float se[kWalkCap];
+  int sb[kWalkCap], sdu[kWalkCap];
+};
+
+__device__ bool walk_head(const ChunkRec *rec, const Special *spec, int gg, int64_t kpw, int64_t nfill,
+                          WalkScratch &w, float &s_out) {
+  const int lane = threadIdx.x & 63;
+  if (gg > kWalkWg) return false;
+  long long ibase = 0;
+  int obase = 0, blast_prev = kNoBinade;
+  bool over = false;
+  for (int cb = 0; cb < gg; cb += 64) {
+    const int c = cb + lane;
+    ChunkRec r;
+    r.tot = 0; r.nsp = 0; r.blast = kNoBinade;
+    if (c < gg) r = ld_rec(&rec[c]);
+    over |= r.nsp > kMaxSpecial;
+    const int cnt = min(r.nsp, kMaxSpecial);
+    const long long incl = wave_incl_scan<long long>(r.tot, lane);
+    const int oincl = wave_incl_scan<int>(cnt, lane);
+    int bp = __shfl_up(r.blast, 1);
+    if (lane == 0) bp = blast_prev;
+    if (c < gg) {
+      w.wg_ib[c] = ibase + incl - r.tot;
+      w.wg_off[c] = obase + oincl - cnt;
+      w.wg_bp[c] = bp;
+    }
+    const int nb = min(64, gg - cb);
+    ibase += __shfl(incl, 63);
+    obase += __shfl(oincl, 63);
+    blast_prev = __shfl(r.blast, nb - 1);
+  }
+  if (lane == 0) w.wg_off[gg] = obase;
+  if (__any(over) || obase > kWalkCap) return false;
+  const int T = obase;
+  __builtin_amdgcn_wave_barrier();
+  for (int o = lane; o < T; o += 64) {
+    int lo = 0, hi = gg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (w.wg_off[mid] <= o) lo = mid; else hi = mid - 1;
+    }
+    const Special x = ld_spec(&spec[(size_t)lo * kMaxSpecial + (o - w.wg_off[lo])]);
+    const int bf = (x.meta >> 16) & 0xFF;
+    w.si[o] = w.wg_ib[lo] + x.ipre;
+    w.sk[o] = (long long)lo * kpw + (x.meta & 0xFFFF);
+    w.se[o] = x.e;
+    w.sb[o] = bf == 255 ? w.wg_bp[lo] : (bf == 0 ? kNoBinade : bf - 128);
+  }
+  __builtin_amdgcn_wave_barrier();
+  bool bad = false;
+  for (int o = lane; o < T; o += 64) {
+    const long long gap = w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+    const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+    int du = -1;
+    if (gap > 1) {
+      const int B = w.sb[o];
+      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24))
+        bad = true;
+      else
+        du = (int)(di >> (B + 17));
+    } else if (di != 0) {
+      bad = true;
+    }
+    w.sdu[o] = du;
+  }
+  if (__any(bad)) return false;
+  __builtin_amdgcn_wave_barrier();
+  float s = 0.0f;
+  bool good = true;
+  for (int base = 0; base < T; base += 64) {
+    const int o = base + lane;
+    const int du_l = o < T ? w.sdu[o] : -1, b_l = o < T ? w.sb[o] : 0;
+    const float e_l = o < T ? w.se[o] : 0.0f;
+    const int cnt = min(64, T - base);
+    for (int i = 0; i < cnt; ++i) {
+      const int du = __builtin_amdgcn_readlane(du_l, i);
+      const int b = __builtin_amdgcn_readlane(b_l, i);
+      const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), i));
+      if (du >= 0) {
+        const uint32_t bits = __float_as_uint(s);
+        const uint32_t m = ((bits & 0x7FFFFFu) | 0x800000u) + (uint32_t)du;
+        good = good && (int)(bits >> 23) == b + 127 && m < (1u << 24);
+        s = __uint_as_float(((uint32_t)(b + 127) << 23) | (m & 0x7FFFFFu));
+      }
+      s = __fadd_rn(s, ev);
+    }
+  }
+  // the trailing segment after the last special
+  const long long k_last = T > 0 ? w.sk[T - 1] : -1, i_last = T > 0 ? w.si[T - 1] : 0;
+  if (good && nfill - 1 - k_last > 0) good = advance(s, blast_prev, ibase - i_last);
+  s_out = s;
+  return good;
+}
+
+#ifdef BKV_EXPERIMENT_TS
+// phase timestamps of workgroup (w) into the sync area's upper half: [w][16] u64
+#define FTS(i) do { if (threadIdx.x == 0 && blockIdx.x < 256) reinterpret_cast<unsigned long long *>(a.sync + 32768)[blockIdx.x * 16 + (i)] = wall_clock64(); } while (0)
+#else
+#define FTS(i) do { } while (0)
+#endif
+template <int KF, int VF, bool FUSE>
+__global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
+  constexpr int NT = 256;
+  constexpr int UPR = KF == BKV_Q8_0 ? 17 : 33;         // LDS uint4 per K row (data + scale / pad)
+  constexpr int DPR = KF == BKV_Q8_0 ? 16 : 32;
+  constexpr int RB = row_bytes(KF);
+  using VR = KRow<VF>;
+  constexpr int VIT = NT / (4 * VR::KPW);                // PV steps per sub-chunk per lane
+  __shared__ uint4 tile[NT * UPR];
+  __shared__ float shf[NT / 64 + 1];
+  __shared__ double shd[NT / 64];
+  __shared__ long long shl[NT / 64];
+  __shared__ int shi[NT / 64];
+  __shared__ double shd4[NT / 64 * kGqa];
+  __shared__ long long shl4[NT / 64 * kGqa];
+  __shared__ int shi4[NT / 64 * kGqa];
+  __shared__ unsigned s_flag;
+  __shared__ float s_m[kGqa], s_sum[kGqa];
+  __shared__ double s_p0[kGqa];
+
+  const int w = blockIdx.x, nkv = a.nkv, g = w % nkv, wi = w / nkv, gg = a.gg, R = a.rsub;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t kbase = (int64_t)wi * R * NT;
+  const LayerView &L = a.L;
+  unsigned *sync = a.sync;
+  // sync words, one 256 B line each: per group 32 lines (3 counters, 3 flags, 3 x 8 sub-counters),
+  // then the generation, the end-of-call counter (+ 8 sub-counters) and the error word
+  unsigned *gl = sync + (size_t)g * 32 * kCounterStride;
+  unsigned *cntA = gl, *cntB = gl + kCounterStride, *cntC = gl + 2 * kCounterStride;
+  unsigned *flA = gl + 3 * kCounterStride, *flB = gl + 4 * kCounterStride, *flC = gl + 5 * kCounterStride;
+  unsigned *subA = gl + 6 * kCounterStride, *subB = gl + 14 * kCounterStride, *subC = gl + 22 * kCounterStride;
+  unsigned *top = sync + (size_t)nkv * 32 * kCounterStride;
+  unsigned *genp = top, *cntD = top + kCounterStride, *subD = top + 2 * kCounterStride;
+  unsigned *err = top + 10 * kCounterStride;
+  const unsigned gen = ld_agent(genp) + 1u;
+  FTS(0);
+
+  if (FUSE) {
+    if (tid < 64 && (int64_t)a.ap.pos >= kbase && (int64_t)a.ap.pos < kbase + (int64_t)R * NT)
+      append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, tid);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- QK
+  float qv[kGqa][kHd / 16];
+  load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
+  float sc[kRMax][kGqa];
+  float mloc[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) mloc[h] = -INFINITY;
+  __syncthreads();
+  asm volatile("s_nop 4");
+#pragma unroll
+  for (int r = 0; r < kRMax; ++r) {
+    if (r < R) {
+      const int64_t j0 = kbase + (int64_t)r * NT;
+      const int n = (int)max((int64_t)0, min((int64_t)NT, (int64_t)a.nfill - j0));
+      for (int i = tid; i < n * DPR; i += NT) {
+        const int row = i / DPR, col = i % DPR;
+        const int64_t slot = slot_of(L, j0 + row);
+        tile[row * UPR + col] = *reinterpret_cast<const uint4 *>(L.kd + (slot * nkv + g) * RB + col * 16);
+      }
+      if (KF == BKV_Q8_0) {
+        for (int row = tid; row < n; row += NT) {
+          const int64_t slot = slot_of(L, j0 + row);
+          tile[row * UPR + 16] = *reinterpret_cast<const uint4 *>(L.ks + (slot * nkv + g) * kScaleRowBytes);
+        }
+      }
+      __syncthreads();
+      float acc[kGqa];
+      qk_row_dot<KF>(tile + tid * UPR, qv, acc);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        sc[r][h] = acc[h];
+        if (tid < n) mloc[h] = fmaxf(mloc[h], acc[h] * a.scale);
+      }
+      __syncthreads();
+    }
+  }
+  FTS(1);
+  // the workgroup's (max, sum exp) per head
+  float lsum[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    mloc[h] = block_max<NT>(mloc[h], shf);
+    float l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r)
+      if (r < R && kbase + (int64_t)r * NT + tid < (int64_t)a.nfill) l += __expf(sc[r][h] * a.scale - mloc[h]);
+    l = wave_sum(l);
+    if (lane == 0) shf[wave] = l;
+    __syncthreads();
+    lsum[h] = (shf[0] + shf[1]) + (shf[2] + shf[3]);
+    __syncthreads();
+  }
+  if (tid < kGqa) {
+    float m = mloc[0], l = lsum[0];
+#pragma unroll
+    for (int h = 1; h < kGqa; ++h)
+      if (tid == h) { m = mloc[h]; l = lsum[h]; }
+    st_f2(&a.stats[(size_t)(g * kGqa + tid) * gg + wi], make_float2(m, l));
+    atomicMax(&a.mxenc[(gen & 1u) * a.nh + g * kGqa + tid], ordered_bits(m));
+  }
+  // the other slot of the running max is the next call's: clear it (0 = empty)
+  if (w == 0 && tid < a.nh) st_agent(&a.mxenc[((gen + 1u) & 1u) * a.nh + tid], 0u);
+
+  // ---------------------------------------------------------------- phase A: global max
+  FTS(2);
+  if (arrive(cntA, subA, wi, gg, &s_flag)) publish(flA, gen);
+  // V sub-chunk 0 into registers (q8_0 V) while the group finishes QK and the max is published
+  uint4 vreg[VF == BKV_Q8_0 ? VIT : 1];
+  uint32_t vsw[VF == BKV_Q8_0 ? VIT : 1];
+  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
+  if constexpr (VF == BKV_Q8_0) {
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int row = wave * VR::KPW + vkk + it * 4 * VR::KPW;
+      const int64_t j = kbase + row;
+      const int64_t slot = slot_of(L, j < (int64_t)a.nfill ? j : 0);
+      vreg[it] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(VF) + vsub * 16);
+      vsw[it] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+    }
+  }
+  FTS(3);
+  wait_flag(flA, gen, err);
+  FTS(4);
+  if (tid < kGqa) s_m[tid] = from_ordered_bits(ld_agent(&a.mxenc[(gen & 1u) * a.nh + g * kGqa + tid]));
+  __syncthreads();
+  // approximate fp64 position of this workgroup's first key on each head's running sum
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    double p = 0.0;
+    for (int i = tid; i < wi; i += NT) {
+      const float2 st = ld_f2(&a.stats[(size_t)(g * kGqa + h) * gg + i]);
+      p += (double)st.y * exp((double)st.x - (double)s_m[h]);
+    }
+    p = block_sum_f64<NT>(p, shd);
+    if (tid == 0) s_p0[h] = p;
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- e, classification, records
+  // LDS reuse: the K tile is free now. s_bin[h][k] binade of key k (kNoBinade if special),
+  // later s_pp[h][k] the fp16 probabilities.
+  int *s_bin = reinterpret_cast<int *>(tile);
+  float ev[kRMax][kGqa];
+  long long itot[kGqa];
+  int nspc[kGqa];
+  double carry[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) { itot[h] = 0; nspc[h] = 0; carry[h] = s_p0[h]; }
+  Special *spec_g = a.spec + (size_t)(g * kGqa) * gg * kMaxSpecial;
+#pragma unroll
+  for (int r = 0; r < kRMax; ++r) {
+    if (r < R) {
+      const int64_t j = kbase + (int64_t)r * NT + tid;
+      const bool valid = j < (int64_t)a.nfill;
+      double ed[kGqa], ex[kGqa], td[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        ev[r][h] = valid ? exp_cr(sc[r][h] * a.scale - s_m[h]) : 0.0f;
+        if (valid) st_agent(&a.e[(size_t)(g * kGqa + h) * a.ld + j], ev[r][h]);
+        ed[h] = (double)ev[r][h];
+      }
+      block_excl_scan_k<NT, kGqa, double>(ed, ex, td, shd4);
+      bool sp[kGqa];
+      long long inc[kGqa], ipre[kGqa], tl[kGqa];
+      int isp[kGqa], idx[kGqa], tn[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        sp[h] = false;
+        int bin = kNoBinade;
+        inc[h] = 0;
+        if (valid) classify(carry[h] + ex[h], carry[h] + ex[h] + ed[h], ev[r][h], sp[h], bin, inc[h]);
+        carry[h] += td[h];
+        s_bin[h * kRMax * NT + r * NT + tid] = (valid && !sp[h]) ? bin : kNoBinade;
+        isp[h] = (valid && sp[h]) ? 1 : 0;
+      }
+      block_excl_scan_k<NT, kGqa, long long>(inc, ipre, tl, shl4);
+      block_excl_scan_k<NT, kGqa, int>(isp, idx, tn, shi4);     // its barriers publish s_bin too
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        const long long ip = itot[h] + ipre[h];
+        const int id = nspc[h] + idx[h];
+        itot[h] += tl[h];
+        nspc[h] += tn[h];
+        if (valid && sp[h] && id < kMaxSpecial) {
+          const int pos = r * NT + tid;
+          const int bprev = pos > 0 ? s_bin[h * kRMax * NT + pos - 1] : 127;
+          Special x;
+          x.ipre = ip;
+          x.e = ev[r][h];
+          x.meta = pos | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+          st_spec(&spec_g[((size_t)h * gg + wi) * kMaxSpecial + id], x);
+        }
+      }
+    }
+  }
+  if (tid < kGqa) {
+    const int h = tid;
+    const int64_t nk = max((int64_t)0, min((int64_t)R * NT, (int64_t)a.nfill - kbase));
+    ChunkRec rc;
+    rc.tot = h == 0 ? itot[0] : h == 1 ? itot[1] : h == 2 ? itot[2] : itot[3];
+    rc.nsp = h == 0 ? nspc[0] : h == 1 ? nspc[1] : h == 2 ? nspc[2] : nspc[3];
+    rc.blast = nk > 0 ? s_bin[h * kRMax * NT + (int)nk - 1] : kNoBinade;
+    st_rec(&a.rec[(size_t)(g * kGqa + h) * gg + wi], rc);
+  }
+
+  // ---------------------------------------------------------------- phase B: the exact sums
+  FTS(5);
+  if (arrive(cntB, subB, wi, gg, &s_flag)) {
+    // wave h walks head g*4+h; LDS scratch: the K tile, a quarter per wave
+    const int hh = g * kGqa + wave;
+    WalkScratch *ws = reinterpret_cast<WalkScratch *>(tile) + wave;
+    float s = 0.0f;
+    bool good = walk_head(a.rec + (size_t)hh * gg, a.spec + (size_t)hh * gg * kMaxSpecial, gg,
+                          (int64_t)R * NT, (int64_t)a.nfill, *ws, s);
+    if (!good) {
+      // fallback: the serial loop itself over the stored e of this head
+      float ss = 0.0f;
+      for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
+        const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
+        const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
+        for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+      }
+      s = ss;
+    }
+    if (lane == 0) {
+      st_agent(&a.sum[hh], s);
+      st_agent(&a.status[hh], good ? 0u : 1u);
+    }
+    publish(flB, gen);
+  }
+  FTS(6);
+  wait_flag(flB, gen, err);
+  FTS(7);
+  if (tid < kGqa) s_sum[tid] = ld_agent(&a.sum[g * kGqa + tid]);
+  __syncthreads();
+
+  // ---------------------------------------------------------------- p16 and PV
+  float *s_pp = reinterpret_cast<float *>(tile);         // [kGqa][kRMax*NT]
+#pragma unroll
+  for (int r = 0; r < kRMax; ++r)
+    if (r < R)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) s_pp[h * kRMax * NT + r * NT + tid] = round_f16(ev[r][h] / s_sum[h]);
+  __syncthreads();
+  float acc[kGqa][VR::EPL];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) acc[h][i] = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kRMax; ++r) {
+    if (r < R) {
+      const int64_t j0 = kbase + (int64_t)r * NT;
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int row = wave * VR::KPW + vkk + it * 4 * VR::KPW;
+        const int64_t j = j0 + row;
+        const bool valid = j < (int64_t)a.nfill;
+        uint4 wv;
+        uint32_t sw = 0;
+        bool pre = false;
+        if constexpr (VF == BKV_Q8_0) {
+          if (r == 0) {
+            wv = vreg[it];
+            sw = vsw[it];
+            pre = true;
+          }
+        }
+        if (!pre) {
+          const int64_t slot = slot_of(L, valid ? j : 0);
+          wv = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(VF) + vsub * 16);
+          if (VF == BKV_Q8_0)
+            sw = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+        }
+        float vsc = 1.0f;
+        if (VF == BKV_Q8_0) vsc = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+        float p[kGqa];
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) p[h] = valid ? s_pp[h * kRMax * NT + r * NT + row] : 0.0f;
+        v_accum<VF>(wv, vsc, p, acc);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) {
+      float v = acc[h][i];
+      if (VR::LPR == 16) v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[h][i] = v;
+    }
+  __syncthreads();
+  float *s_red = reinterpret_cast<float *>(tile);          // [4 waves][kGqa][kHd]
+  if (vkk == 0) {
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int i = 0; i < VR::EPL; ++i) s_red[(wave * kGqa + h) * kHd + vsub * VR::EPL + i] = acc[h][i];
+  }
+  __syncthreads();
+  float *part_g = a.part + (size_t)g * gg * kGqa * kHd;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    const float v = s_red[(0 * kGqa + h) * kHd + tid] + s_red[(1 * kGqa + h) * kHd + tid] +
+                    s_red[(2 * kGqa + h) * kHd + tid] + s_red[(3 * kGqa + h) * kHd + tid];
+    st_agent(&part_g[((size_t)wi * kGqa + h) * kHd + tid], v);
+  }
+
+  FTS(8);
+  // ---------------------------------------------------------------- phase C: merge + gate
+  // Two-level, no waiting: the last arrival of each sub-group (wi % 8) sums its members' partials
+  // in member order into a sub-partial, and the last of those sums the sub-partials in order.
+  {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int k = wi % kSub, members = (gg - k + kSub - 1) / kSub, nsub = gg < kSub ? gg : kSub;
+    if (tid == 0) s_flag = atomicAdd(subC + k * kCounterStride, 1u) == (unsigned)(members - 1) ? 1u : 0u;
+    __syncthreads();
+    if (s_flag) {
+      if (tid == 0) st_agent(subC + k * kCounterStride, 0u);
+      float *sp = a.subpart + ((size_t)g * kSub + k) * kGqa * kHd;
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        float v = 0.0f;
+        for (int m = 0; m < members; ++m)
+          v += ld_agent(&part_g[((size_t)(k + m * kSub) * kGqa + h) * kHd + tid]);
+        st_agent(&sp[h * kHd + tid], v);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) {
+        s_flag = atomicAdd(cntC, 1u) == (unsigned)(nsub - 1) ? 1u : 0u;
+        if (s_flag) st_agent(cntC, 0u);
+      }
+      __syncthreads();
+      if (s_flag) {
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          float v = 0.0f;
+          for (int kk = 0; kk < nsub; ++kk)
+            v += ld_agent(&a.subpart[(((size_t)g * kSub + kk) * kGqa + h) * kHd + tid]);
+          const size_t oi = ((size_t)g * kGqa + h) * kHd + tid;
+          a.out[oi] = v;
+          if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+        }
+      }
+    }
+    FTS(9);
+  }
+  FTS(10);
+  // ---------------------------------------------------------------- end of call: next generation
+  if (arrive(cntD, subD, blockIdx.x, gridDim.x, &s_flag) && tid == 0) st_agent(genp, gen);
+}
+
+__global__ void workspace_init_kernel(unsigned *sync, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) sync[i] = 0u;
+}
+
+hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st) {
+  hipLaunchKernelGGL(workspace_init_kernel, dim3(1), dim3(256), 0, st, sync, nwords);
+  return hipGetLastError();
+}
+
+template <int KF, int VF, bool FUSE>
+static int fused_capacity() {
+  static int cap = -1;
+  if (cap < 0) {
+    int dev = 0, per = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fused_kernel<KF, VF, FUSE>, 256, 0) != hipSuccess)
+      cap = 0;
+    else
+      cap = per * pr.multiProcessorCount;
+  }
+  return cap;
+}
+
+int fused_max_workgroups(int kf, int vf) {
+  BKV_FMT_SWITCH(kf, vf, { return fused_capacity<KF_, VF_, false>(); });
+  return 0;
+}
+
+hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st) {
+  const dim3 grid(a.gg * a.nkv), block(256);
+  void *args[] = {const_cast<FusedArgs *>(&a)};
+  hipError_t e = hipErrorInvalidValue;
+  BKV_FMT_SWITCH(kf, vf, {
+    if (fuse)
+      e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, true>), grid, block, args, 0, st);
+    else
+      e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, false>), grid, block, args, 0, st);
+  });
+  return e;
+}
+
+}  // namespace bkv

@@ -88,17 +88,59 @@ struct RedArgs {
   float *out, *out_gated;
 };
 
+constexpr int kRMax = 4;           // 256-key sub-chunks per workgroup of the fused kernel
+constexpr size_t kSyncBytes = 256 * 1024;  // counters / flags at the start of every workspace
+constexpr size_t kSyncMaxOffset = 192 * 1024;   // the fused kernel's running-max slots [2][nh]
+
+struct FusedArgs {
+  LayerView L;
+  int nkv;
+  uint32_t nfill;
+  float scale;
+  int gg, rsub;                  // workgroups per KV group, 256-key sub-chunks per workgroup
+  int64_t ld;
+  const float *q;                // [nh][hd]
+  AppendArgs ap;
+  const float *gate;
+  float *out, *out_gated;
+  float2 *stats;                 // [nh][gg]
+  unsigned *mxenc;               // [2][nh] running max (order-preserving bits), by call parity
+  int nh;
+  float *subpart;                // [nkv][8][kGqa][hd]
+  ChunkRec *rec;                 // [nh][gg]
+  Special *spec;                 // [nh][gg][kMaxSpecial]
+  float *e;                      // [nh][ld]
+  float *sum;                    // [nh]
+  unsigned *status;              // [nh]
+  float *part;                   // [nkv][gg][kGqa][hd]
+  unsigned *sync;                // kSyncBytes
+};
+
+#define BKV_FMT_SWITCH(KF, VF, ...)                                                    \
+  do {                                                                                \
+    if ((KF) == BKV_Q8_0 && (VF) == BKV_Q8_0) { constexpr int KF_ = 1, VF_ = 1; __VA_ARGS__; } \
+    else if ((KF) == BKV_Q8_0) { constexpr int KF_ = 1, VF_ = 0; __VA_ARGS__; }       \
+    else if ((VF) == BKV_Q8_0) { constexpr int KF_ = 0, VF_ = 1; __VA_ARGS__; }       \
+    else { constexpr int KF_ = 0, VF_ = 0; __VA_ARGS__; }                             \
+  } while (0)
+
 // decode partition plan and workspace layout for nfill keys
 struct DecodePlan {
   int qk_chunk, nch_qk, nch_e, pv_chunk, nch_pv;
   int64_t ld;
   size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_dbg, off_part,
       total;
+  // fused path (gg == 0: not available for this nfill)
+  int gg, rsub;
+  size_t f_stats, f_sub, f_rec, f_spec, f_e, f_sum, f_status, f_part, f_total;
 };
 
-DecodePlan plan_decode(int nh, int nkv, int kfmt, int64_t nfill);
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill);
 int qk_keys_per_wg(int kfmt);
 
+int fused_max_workgroups(int kf, int vf);
+hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st);
+hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st);
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);
 hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, const RedArgs &ra,
                          int kf, int vf, bool fuse, hipStream_t st);

@@ -116,6 +116,16 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
                            const float *q, const float *gate, float *out, float *out_gated,
                            void *workspace, size_t ws_bytes, hipStream_t stream);
 
+/* Prepare a workspace for its first use: zeroes the synchronisation words at its start (a small
+ * kernel on `stream`, no memset). Call once after allocating it; the caller must not write into the
+ * workspace afterwards. */
+int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Which decode implementation a call with nfill keys takes on the current device: 1 = the fused
+ * single cooperative launch, 0 = the four-launch split path (also forced by BKV_DECODE=split),
+ * -1 = bad arguments. */
+int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill);
+
 /* Workspace needed by op (enum bkv_op) for contexts up to max_ctx positions (prefill: max_ctx is
  * pos0 + n_q, the chunk is bounded by BKV_PREFILL_MAX_Q). Returns 0 on a bad descriptor.      */
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx);

@@ -11,6 +11,16 @@ from tests.gpu_util import fill, pair, qg, report, same_bytes, say
 
 TOL = 1e-4
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["fused", "split"])
+def path(request, monkeypatch):
+    """Run a test through both decode implementations (the library reads BKV_DECODE per call)."""
+    if request.param == "split":
+        monkeypatch.setenv("BKV_DECODE", "split")
+    else:
+        monkeypatch.delenv("BKV_DECODE", raising=False)
+    return request.param
 FMTS = [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16), (BKV_F16, BKV_Q8_0), (BKV_Q8_0, BKV_F16)]
 
 
@@ -35,8 +45,8 @@ def test_append_bit_exact(kf, vf):
 
 @pytest.mark.parametrize("kf,vf", FMTS)
 @pytest.mark.parametrize("nfill", [1, 17, 256, 1000, 4097])
-def test_decode_matches_oracle(kf, vf, nfill):
-    say(f"decode kf={kf} vf={vf} nfill={nfill}")
+def test_decode_matches_oracle(kf, vf, nfill, path):
+    say(f"decode kf={kf} vf={vf} nfill={nfill} path={path}")
     dev, host = pair(1, nfill, kf, vf)
     fill(dev, host, 0, nfill, seed=nfill)
     q, g = qg(nfill, 0)
@@ -58,7 +68,7 @@ def test_config1_f16_256():
     assert report("config1", out.cpu().numpy(), want) <= TOL
 
 
-def test_config2_decode_step_8_layers():
+def test_config2_decode_step_8_layers(path):
     """8 layers at 4096 context, q8_0 K+V, one token appended per layer with the
     fused decode_step, then GQA attention; cache bytes bit-exact afterwards."""
     n = 4096
@@ -79,7 +89,7 @@ def test_config2_decode_step_8_layers():
     assert worst <= TOL
 
 
-def test_decode_step_equals_append_then_decode():
+def test_decode_step_equals_append_then_decode(path):
     n = 2000
     a, _ = pair(1, n + 1, BKV_Q8_0, BKV_Q8_0)
     b, host = pair(1, n + 1, BKV_Q8_0, BKV_Q8_0)
@@ -96,7 +106,7 @@ def test_decode_step_equals_append_then_decode():
     assert all(torch.equal(x, y) for x, y in zip(a.host_arrays(), b.host_arrays()) if x is not None)
 
 
-def test_deterministic_repeat():
+def test_deterministic_repeat(path):
     n = 20000
     dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
     fill(dev, host, 0, n, seed=5)
@@ -111,7 +121,7 @@ def test_deterministic_repeat():
 
 @pytest.mark.parametrize("kf,vf,n,seed", [(BKV_Q8_0, BKV_Q8_0, 4097, 1), (BKV_F16, BKV_F16, 3000, 7),
                                           (BKV_Q8_0, BKV_Q8_0, 40000, 2)])
-def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed):
+def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed, path):
     """The intermediates the reference's bitwise gate (BONSAI_QCHECK stages A/B) compares: every score,
     every e_j = exp(s_j*scale - max) and the serial fp32 softmax sum match the oracle bit for bit, and
     so do the fp16 probabilities formed from them."""
@@ -123,7 +133,11 @@ def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed):
     out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
     torch.cuda.synchronize()
     score, e, ssum, status = dev.debug_intermediates(n)
-    assert oracle.bit_diff(score.numpy(), sc) == 0
+    say(f"decode path {dev.decode_path(n)}")
+    if score is not None:                     # the fused path keeps scores in registers
+        assert oracle.bit_diff(score.numpy(), sc) == 0
+    e_want = np.exp((sc * np.float32(0.0625) - (sc * np.float32(0.0625)).max(axis=1, keepdims=True)).astype(np.float64)).astype(np.float32)
+    assert oracle.bit_diff(e.numpy(), e_want) == 0
     assert int(status.sum()) == 0, "the exact walk fell back to the serial loop"
     p_gpu = (e.numpy() / ssum.numpy()[:, None]).astype(np.float32)
     assert oracle.bit_diff(p_gpu, pr) == 0
@@ -131,7 +145,7 @@ def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed):
     assert report("out", out.cpu().numpy(), want) <= TOL
 
 
-def test_identical_keys_uniform_attention():
+def test_identical_keys_uniform_attention(path):
     """All scores equal: every e_j = 1 and the serial sum is exactly n; p = 1/n in fp16."""
     n = 5000
     dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
