@@ -61,14 +61,17 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
   p.off_dbg = o;    o += align256((size_t)nh * 8 * sizeof(unsigned long long));
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
   size_t total = o;
-  // the fused single-launch path: as many 256-key workgroups per KV group as stay resident
+  // the fused single-launch path: as many workgroups per KV group as stay resident
   const int cap = fused_max_workgroups(kfmt, vfmt);
   p.gg = 0;
   p.rsub = 0;
   if (cap >= nkv) {
-    const int64_t rs = cdiv(n, (int64_t)(cap / nkv) * 256);
-    const int64_t gg = cdiv(n, rs * 256);          // no workgroup without keys
+    const int64_t pass = fused_keys_per_pass(kfmt);
+    const int64_t kpw = cdiv(n, std::min<int64_t>({cdiv(n, pass), cap / nkv, (int64_t)kFusedMaxGroupWgs}));
+    const int64_t rs = cdiv(kpw, pass);
+    const int64_t gg = cdiv(n, kpw);               // no workgroup without keys
     if (rs <= kRMax) {
+      p.kpw = (int)kpw;
       p.gg = (int)gg;
       p.rsub = (int)rs;
       size_t f = kSyncBytes;
@@ -169,7 +172,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
 
   if (p.gg > 0 && !force_split()) {
     FusedArgs fa{};
-    fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub;
+    fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub; fa.kpw = p.kpw;
     fa.ld = p.ld; fa.q = q;
     if (fused) fa.ap = *fused;
     fa.gate = gate; fa.out = out; fa.out_gated = out_gated;

@@ -1,8 +1,8 @@
 // bkv_fused.hip - one cooperative launch per layer and decode token: append, QK in the reference's
 // order, the exact serial softmax sum, PV over fp16 probabilities and the partition merge.
 //
-// Workgroup w serves KV group g = w % nkv and keys [wi*R*256, (wi+1)*R*256) with wi = w / nkv, in R
-// sub-chunks of 256 keys (one key per thread). The phases that need every workgroup of a group are
+// Workgroup w serves KV group g = w % nkv and keys [wi*kpw, (wi+1)*kpw) with wi = w / nkv, in R
+// passes of NT keys (one key per thread; NT = 192 for q8_0 K, 128 for fp16 K). The phases that need every workgroup of a group are
 // joined by arrival counters: a workgroup counts itself in, the last one to arrive does the phase's
 // group-wide step (global max; the walk to the exact sum; nothing for the merge) and raises the
 // phase flag, and every workgroup waits for the flag only after it has arrived itself. The launch is
@@ -83,12 +83,13 @@ __device__ __forceinline__ void wait_flag(const unsigned *flag, unsigned gen, un
 // keys. The fields of every special (global key index, global increment prefix, binade of the step
 // before it, the whole ulps of the segment before it) are resolved in parallel across the wave into
 // LDS; the serial chain then only carries the running sum (wave-uniform, readlane per special).
-constexpr int kWalkWg = 128;       // workgroups per group the scratch holds
+constexpr int kWalkWg = kFusedMaxGroupWgs;   // workgroups per group the scratch holds
 constexpr int kWalkCap = 384;      // specials per head the scratch holds (more: serial fallback)
 struct WalkScratch {
   long long wg_ib[kWalkWg];
   int wg_off[kWalkWg + 1], wg_bp[kWalkWg];
-  long long sk[kWalkCap], si[kWalkCap];
+  long long si[kWalkCap];
+  int sk[kWalkCap];
   float se[kWalkCap];
   int sb[kWalkCap], sdu[kWalkCap];
 };
@@ -134,7 +135,7 @@ __device__ bool walk_head(const ChunkRec *rec, const Special *spec, int gg, int6
     const Special x = ld_spec(&spec[(size_t)lo * kMaxSpecial + (o - w.wg_off[lo])]);
     const int bf = (x.meta >> 16) & 0xFF;
     w.si[o] = w.wg_ib[lo] + x.ipre;
-    w.sk[o] = (long long)lo * kpw + (x.meta & 0xFFFF);
+    w.sk[o] = (int)(lo * kpw + (x.meta & 0xFFFF));
     w.se[o] = x.e;
     w.sb[o] = bf == 255 ? w.wg_bp[lo] : (bf == 0 ? kNoBinade : bf - 128);
   }
@@ -190,15 +191,41 @@ __device__ bool walk_head(const ChunkRec *rec, const Special *spec, int gg, int6
 #else
 #define FTS(i) do { } while (0)
 #endif
+// threads (= keys per pass) of a fused workgroup: 192 for q8_0 K (3 per CU: 52 KB K tile),
+// 128 for fp16 K (2 per CU: 67 KB)
+template <int KF>
+struct FusedCfg {
+  static constexpr int NT = KF == BKV_Q8_0 ? 192 : 128;
+  static constexpr int MINB = KF == BKV_Q8_0 ? 3 : 2;
+};
+
+// q8_0 V data rows [j0, j0+n) of group g into the LDS tile, 256 B per row (16 lanes read a row's
+// 256 contiguous bytes: conflict-free); the block scales stay in registers.
+// Rows [n, NT) are zero-filled so that the PV loop needs no bounds test.
+template <int NT>
+__device__ __forceinline__ void load_v_tile(uint4 *tile, const LayerView &L, int nkv, int g, int64_t j0, int n) {
+  for (int i = threadIdx.x; i < NT * 16; i += NT) {
+    const int row = i >> 4, col = i & 15;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < n) {
+      const int64_t slot = slot_of(L, j0 + row);
+      v = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(BKV_Q8_0) + col * 16);
+    }
+    tile[i] = v;
+  }
+}
+
 template <int KF, int VF, bool FUSE>
-__global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
-  constexpr int NT = 256;
+__global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_kernel(FusedArgs a) {
+  constexpr int NT = FusedCfg<KF>::NT, NW = NT / 64;
   constexpr int UPR = KF == BKV_Q8_0 ? 17 : 33;         // LDS uint4 per K row (data + scale / pad)
   constexpr int DPR = KF == BKV_Q8_0 ? 16 : 32;
   constexpr int RB = row_bytes(KF);
   using VR = KRow<VF>;
-  constexpr int VIT = NT / (4 * VR::KPW);                // PV steps per sub-chunk per lane
+  constexpr int VIT = NT / (NW * VR::KPW);               // PV steps per sub-chunk per lane
   __shared__ uint4 tile[NT * UPR];
+  static_assert(VF != BKV_Q8_0 || sizeof(tile) >= NT * 256 + kGqa * NT * 2, "V tile + fp16 p must fit");
+  static_assert(sizeof(tile) >= kGqa * sizeof(WalkScratch), "walk scratch must fit the K tile");
   __shared__ float shf[NT / 64 + 1];
   __shared__ double shd[NT / 64];
   __shared__ long long shl[NT / 64];
@@ -212,7 +239,8 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
 
   const int w = blockIdx.x, nkv = a.nkv, g = w % nkv, wi = w / nkv, gg = a.gg, R = a.rsub;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t kbase = (int64_t)wi * R * NT;
+  const int64_t kbase = (int64_t)wi * a.kpw;
+  const int64_t kend = min((int64_t)a.nfill, kbase + (int64_t)a.kpw);   // this workgroup's keys
   const LayerView &L = a.L;
   unsigned *sync = a.sync;
   // sync words, one 256 B line each: per group 32 lines (3 counters, 3 flags, 3 x 8 sub-counters),
@@ -228,7 +256,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   FTS(0);
 
   if (FUSE) {
-    if (tid < 64 && (int64_t)a.ap.pos >= kbase && (int64_t)a.ap.pos < kbase + (int64_t)R * NT)
+    if (tid < 64 && (int64_t)a.ap.pos >= kbase && (int64_t)a.ap.pos < kend)
       append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, tid);
     __syncthreads();
   }
@@ -246,7 +274,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   for (int r = 0; r < kRMax; ++r) {
     if (r < R) {
       const int64_t j0 = kbase + (int64_t)r * NT;
-      const int n = (int)max((int64_t)0, min((int64_t)NT, (int64_t)a.nfill - j0));
+      const int n = (int)max((int64_t)0, min((int64_t)NT, kend - j0));
       for (int i = tid; i < n * DPR; i += NT) {
         const int row = i / DPR, col = i % DPR;
         const int64_t slot = slot_of(L, j0 + row);
@@ -278,11 +306,14 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
     float l = 0.0f;
 #pragma unroll
     for (int r = 0; r < kRMax; ++r)
-      if (r < R && kbase + (int64_t)r * NT + tid < (int64_t)a.nfill) l += __expf(sc[r][h] * a.scale - mloc[h]);
+      if (r < R && kbase + (int64_t)r * NT + tid < kend) l += __expf(sc[r][h] * a.scale - mloc[h]);
     l = wave_sum(l);
     if (lane == 0) shf[wave] = l;
     __syncthreads();
-    lsum[h] = (shf[0] + shf[1]) + (shf[2] + shf[3]);
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += shf[i];
+    lsum[h] = t;
     __syncthreads();
   }
   if (tid < kGqa) {
@@ -299,20 +330,6 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   // ---------------------------------------------------------------- phase A: global max
   FTS(2);
   if (arrive(cntA, subA, wi, gg, &s_flag)) publish(flA, gen);
-  // V sub-chunk 0 into registers (q8_0 V) while the group finishes QK and the max is published
-  uint4 vreg[VF == BKV_Q8_0 ? VIT : 1];
-  uint32_t vsw[VF == BKV_Q8_0 ? VIT : 1];
-  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
-  if constexpr (VF == BKV_Q8_0) {
-#pragma unroll
-    for (int it = 0; it < VIT; ++it) {
-      const int row = wave * VR::KPW + vkk + it * 4 * VR::KPW;
-      const int64_t j = kbase + row;
-      const int64_t slot = slot_of(L, j < (int64_t)a.nfill ? j : 0);
-      vreg[it] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(VF) + vsub * 16);
-      vsw[it] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-    }
-  }
   FTS(3);
   wait_flag(flA, gen, err);
   FTS(4);
@@ -346,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   for (int r = 0; r < kRMax; ++r) {
     if (r < R) {
       const int64_t j = kbase + (int64_t)r * NT + tid;
-      const bool valid = j < (int64_t)a.nfill;
+      const bool valid = j < kend;
       double ed[kGqa], ex[kGqa], td[kGqa];
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
@@ -390,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   }
   if (tid < kGqa) {
     const int h = tid;
-    const int64_t nk = max((int64_t)0, min((int64_t)R * NT, (int64_t)a.nfill - kbase));
+    const int64_t nk = max((int64_t)0, kend - kbase);
     ChunkRec rc;
     rc.tot = h == 0 ? itot[0] : h == 1 ? itot[1] : h == 2 ? itot[2] : itot[3];
     rc.nsp = h == 0 ? nspc[0] : h == 1 ? nspc[1] : h == 2 ? nspc[2] : nspc[3];
@@ -401,27 +418,43 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   // ---------------------------------------------------------------- phase B: the exact sums
   FTS(5);
   if (arrive(cntB, subB, wi, gg, &s_flag)) {
-    // wave h walks head g*4+h; LDS scratch: the K tile, a quarter per wave
-    const int hh = g * kGqa + wave;
-    WalkScratch *ws = reinterpret_cast<WalkScratch *>(tile) + wave;
-    float s = 0.0f;
-    bool good = walk_head(a.rec + (size_t)hh * gg, a.spec + (size_t)hh * gg * kMaxSpecial, gg,
-                          (int64_t)R * NT, (int64_t)a.nfill, *ws, s);
-    if (!good) {
-      // fallback: the serial loop itself over the stored e of this head
-      float ss = 0.0f;
-      for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
-        const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
-        const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
-        for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+    // each wave walks heads wave, wave+NW, ...; LDS scratch: the K tile, one WalkScratch per head
+    for (int h = wave; h < kGqa; h += NW) {
+      const int hh = g * kGqa + h;
+      WalkScratch *ws = reinterpret_cast<WalkScratch *>(tile) + h;
+      float s = 0.0f;
+      bool good = walk_head(a.rec + (size_t)hh * gg, a.spec + (size_t)hh * gg * kMaxSpecial, gg,
+                            (int64_t)a.kpw, (int64_t)a.nfill, *ws, s);
+      if (!good) {
+        // fallback: the serial loop itself over the stored e of this head
+        float ss = 0.0f;
+        for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
+          const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
+          const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
+          for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+        }
+        s = ss;
       }
-      s = ss;
-    }
-    if (lane == 0) {
-      st_agent(&a.sum[hh], s);
-      st_agent(&a.status[hh], good ? 0u : 1u);
+      if (lane == 0) {
+        st_agent(&a.sum[hh], s);
+        st_agent(&a.status[hh], good ? 0u : 1u);
+      }
     }
     publish(flB, gen);
+    __syncthreads();                       // walk scratch released
+  }
+  // q8_0 V pass 0 into the LDS tile and its block scales into registers, while the walk runs
+  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
+  uint32_t vsw[VF == BKV_Q8_0 ? VIT : 1];
+  if constexpr (VF == BKV_Q8_0) {
+    const int n0 = (int)max((int64_t)0, min((int64_t)NT, kend - kbase));
+    load_v_tile<NT>(tile, L, nkv, g, kbase, n0);
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int row = wave * VR::KPW + vkk + it * NW * VR::KPW;
+      const int64_t slot = slot_of(L, row < n0 ? kbase + row : kbase);
+      vsw[it] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+    }
   }
   FTS(6);
   wait_flag(flB, gen, err);
@@ -430,48 +463,63 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   __syncthreads();
 
   // ---------------------------------------------------------------- p16 and PV
-  float *s_pp = reinterpret_cast<float *>(tile);         // [kGqa][kRMax*NT]
-#pragma unroll
-  for (int r = 0; r < kRMax; ++r)
-    if (r < R)
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h) s_pp[h * kRMax * NT + r * NT + tid] = round_f16(ev[r][h] / s_sum[h]);
-  __syncthreads();
+  // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296) in LDS after the V
+  // rows; out += p16 * V over this workgroup's keys, 4 heads per V row read.
   float acc[kGqa][VR::EPL];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
     for (int i = 0; i < VR::EPL; ++i) acc[h][i] = 0.0f;
+  _Float16 *s_p16 = reinterpret_cast<_Float16 *>(reinterpret_cast<char *>(tile) + (VF == BKV_Q8_0 ? NT * 256 : 0));
 #pragma unroll
   for (int r = 0; r < kRMax; ++r) {
     if (r < R) {
       const int64_t j0 = kbase + (int64_t)r * NT;
-#pragma unroll
-      for (int it = 0; it < VIT; ++it) {
-        const int row = wave * VR::KPW + vkk + it * 4 * VR::KPW;
-        const int64_t j = j0 + row;
-        const bool valid = j < (int64_t)a.nfill;
-        uint4 wv;
-        uint32_t sw = 0;
-        bool pre = false;
+      const int n = (int)max((int64_t)0, min((int64_t)NT, kend - j0));
+      if (r > 0) {
+        __syncthreads();                    // pass r-1 done with the tile
         if constexpr (VF == BKV_Q8_0) {
-          if (r == 0) {
-            wv = vreg[it];
-            sw = vsw[it];
-            pre = true;
+          load_v_tile<NT>(tile, L, nkv, g, j0, n);
+#pragma unroll
+          for (int it = 0; it < VIT; ++it) {
+            const int row = wave * VR::KPW + vkk + it * NW * VR::KPW;
+            const int64_t slot = slot_of(L, row < n ? j0 + row : j0);
+            vsw[it] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
           }
         }
-        if (!pre) {
-          const int64_t slot = slot_of(L, valid ? j : 0);
-          wv = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(VF) + vsub * 16);
-          if (VF == BKV_Q8_0)
-            sw = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-        }
-        float vsc = 1.0f;
-        if (VF == BKV_Q8_0) vsc = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-        float p[kGqa];
+      }
+      {
+        // the 4 heads' probabilities of key tid side by side: one 8-byte LDS read per V row
+        _Float16 pk[kGqa];
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h) p[h] = valid ? s_pp[h * kRMax * NT + r * NT + row] : 0.0f;
+        for (int h = 0; h < kGqa; ++h) pk[h] = (_Float16)(tid < n ? ev[r][h] / s_sum[h] : 0.0f);
+        uint2 pw;
+        pw.x = (uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16);
+        pw.y = (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16);
+        reinterpret_cast<uint2 *>(s_p16)[tid] = pw;
+      }
+      __syncthreads();
+#pragma unroll (VF == BKV_Q8_0 ? VIT : 4)
+      for (int it = 0; it < VIT; ++it) {
+        const int row = wave * VR::KPW + vkk + it * NW * VR::KPW;
+        const bool valid = row < n;
+        uint4 wv;
+        float vsc = 1.0f;
+        if constexpr (VF == BKV_Q8_0) {
+          wv = tile[row * 16 + vsub];       // zero beyond n
+          const uint32_t sw = vsw[it];
+          vsc = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+        } else {
+          const int64_t slot = slot_of(L, valid ? j0 + row : j0);
+          wv = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(VF) + vsub * 16);
+          if (!valid) wv = make_uint4(0u, 0u, 0u, 0u);
+        }
+        const uint2 pw = reinterpret_cast<const uint2 *>(s_p16)[row];   // zero beyond n
+        float p[kGqa];
+        p[0] = f16_to_f32(pw.x & 0xFFFFu);
+        p[1] = f16_to_f32(pw.x >> 16);
+        p[2] = f16_to_f32(pw.y & 0xFFFFu);
+        p[3] = f16_to_f32(pw.y >> 16);
         v_accum<VF>(wv, vsc, p, acc);
       }
     }
@@ -486,7 +534,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
       acc[h][i] = v;
     }
   __syncthreads();
-  float *s_red = reinterpret_cast<float *>(tile);          // [4 waves][kGqa][kHd]
+  float *s_red = reinterpret_cast<float *>(tile);          // [NW waves][kGqa][kHd]
   if (vkk == 0) {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h)
@@ -495,14 +543,16 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
   }
   __syncthreads();
   float *part_g = a.part + (size_t)g * gg * kGqa * kHd;
+  for (int d = tid; d < kHd; d += NT) {
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    const float v = s_red[(0 * kGqa + h) * kHd + tid] + s_red[(1 * kGqa + h) * kHd + tid] +
-                    s_red[(2 * kGqa + h) * kHd + tid] + s_red[(3 * kGqa + h) * kHd + tid];
-    st_agent(&part_g[((size_t)wi * kGqa + h) * kHd + tid], v);
+    for (int h = 0; h < kGqa; ++h) {
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) v += s_red[(i * kGqa + h) * kHd + d];
+      st_agent(&part_g[((size_t)wi * kGqa + h) * kHd + d], v);
+    }
   }
 
-  FTS(8);
   // ---------------------------------------------------------------- phase C: merge + gate
   // Two-level, no waiting: the last arrival of each sub-group (wi % 8) sums its members' partials
   // in member order into a sub-partial, and the last of those sums the sub-partials in order.
@@ -515,12 +565,14 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
     if (s_flag) {
       if (tid == 0) st_agent(subC + k * kCounterStride, 0u);
       float *sp = a.subpart + ((size_t)g * kSub + k) * kGqa * kHd;
+      for (int d = tid; d < kHd; d += NT) {
 #pragma unroll
-      for (int h = 0; h < kGqa; ++h) {
-        float v = 0.0f;
-        for (int m = 0; m < members; ++m)
-          v += ld_agent(&part_g[((size_t)(k + m * kSub) * kGqa + h) * kHd + tid]);
-        st_agent(&sp[h * kHd + tid], v);
+        for (int h = 0; h < kGqa; ++h) {
+          float v = 0.0f;
+          for (int m = 0; m < members; ++m)
+            v += ld_agent(&part_g[((size_t)(k + m * kSub) * kGqa + h) * kHd + d]);
+          st_agent(&sp[h * kHd + d], v);
+        }
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -530,14 +582,16 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FusedArgs a) {
       }
       __syncthreads();
       if (s_flag) {
+        for (int d = tid; d < kHd; d += NT) {
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          float v = 0.0f;
-          for (int kk = 0; kk < nsub; ++kk)
-            v += ld_agent(&a.subpart[(((size_t)g * kSub + kk) * kGqa + h) * kHd + tid]);
-          const size_t oi = ((size_t)g * kGqa + h) * kHd + tid;
-          a.out[oi] = v;
-          if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+          for (int h = 0; h < kGqa; ++h) {
+            float v = 0.0f;
+            for (int kk = 0; kk < nsub; ++kk)
+              v += ld_agent(&a.subpart[(((size_t)g * kSub + kk) * kGqa + h) * kHd + d]);
+            const size_t oi = ((size_t)g * kGqa + h) * kHd + d;
+            a.out[oi] = v;
+            if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+          }
         }
       }
     }
@@ -564,7 +618,7 @@ static int fused_capacity() {
     int dev = 0, per = 0;
     hipDeviceProp_t pr;
     if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fused_kernel<KF, VF, FUSE>, 256, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fused_kernel<KF, VF, FUSE>, FusedCfg<KF>::NT, 0) != hipSuccess)
       cap = 0;
     else
       cap = per * pr.multiProcessorCount;
@@ -572,16 +626,19 @@ static int fused_capacity() {
   return cap;
 }
 
+int fused_keys_per_pass(int kf) { return kf == BKV_Q8_0 ? FusedCfg<1>::NT : FusedCfg<0>::NT; }
+
 int fused_max_workgroups(int kf, int vf) {
   BKV_FMT_SWITCH(kf, vf, { return fused_capacity<KF_, VF_, false>(); });
   return 0;
 }
 
 hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st) {
-  const dim3 grid(a.gg * a.nkv), block(256);
+  const dim3 grid(a.gg * a.nkv);
   void *args[] = {const_cast<FusedArgs *>(&a)};
   hipError_t e = hipErrorInvalidValue;
   BKV_FMT_SWITCH(kf, vf, {
+    const dim3 block(FusedCfg<KF_>::NT);
     if (fuse)
       e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, true>), grid, block, args, 0, st);
     else

@@ -88,7 +88,9 @@ struct RedArgs {
   float *out, *out_gated;
 };
 
-constexpr int kRMax = 4;           // 256-key sub-chunks per workgroup of the fused kernel
+constexpr int kRMax = 2;                     // key passes per workgroup of the fused kernel
+// workgroups per KV group of the fused launch at most (the walker's LDS scratch holds this many)
+constexpr int kFusedMaxGroupWgs = 192;
 constexpr size_t kSyncBytes = 256 * 1024;  // counters / flags at the start of every workspace
 constexpr size_t kSyncMaxOffset = 192 * 1024;   // the fused kernel's running-max slots [2][nh]
 
@@ -98,6 +100,7 @@ struct FusedArgs {
   uint32_t nfill;
   float scale;
   int gg, rsub;                  // workgroups per KV group, 256-key sub-chunks per workgroup
+  int kpw;                       // keys per workgroup (the last one may hold fewer)
   int64_t ld;
   const float *q;                // [nh][hd]
   AppendArgs ap;
@@ -131,7 +134,7 @@ struct DecodePlan {
   size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_dbg, off_part,
       total;
   // fused path (gg == 0: not available for this nfill)
-  int gg, rsub;
+  int gg, rsub, kpw;
   size_t f_stats, f_sub, f_rec, f_spec, f_e, f_sum, f_status, f_part, f_total;
 };
 
@@ -139,6 +142,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill);
 int qk_keys_per_wg(int kfmt);
 
 int fused_max_workgroups(int kf, int vf);
+int fused_keys_per_pass(int kf);
 hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st);
 hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st);
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);
