@@ -65,7 +65,9 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
   const int cap = fused_max_workgroups(kfmt, vfmt);
   p.gg = 0;
   p.rsub = 0;
-  if (cap >= nkv) {
+  // the sync lines of all groups and the 11 top lines must end below the running-max slots
+  const bool sync_fits = ((size_t)nkv * kGroupLines + 11) * kCounterStride * sizeof(unsigned) <= kSyncMaxOffset;
+  if (cap >= nkv && sync_fits) {
     const int64_t pass = fused_keys_per_pass(kfmt);
     const int64_t kpw = cdiv(n, std::min<int64_t>({cdiv(n, pass), cap / nkv, (int64_t)kFusedMaxGroupWgs}));
     const int64_t rs = cdiv(kpw, pass);
@@ -76,7 +78,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
       p.rsub = (int)rs;
       size_t f = kSyncBytes;
       p.f_stats = f;  f += align256((size_t)nh * gg * sizeof(float2));
-      p.f_sub = f;    f += align256((size_t)nkv * 8 * kGqa * kHd * sizeof(float));
+      p.f_sub = f;    f += align256((size_t)nkv * kMergeSub * kGqa * kHd * sizeof(float));
       p.f_rec = f;    f += align256((size_t)nh * gg * sizeof(ChunkRec));
       p.f_spec = f;   f += align256((size_t)nh * gg * kMaxSpecial * sizeof(Special));
       p.f_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));

@@ -47,17 +47,8 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
     __syncthreads();
   }
   constexpr int RB = row_bytes(KF);
-  for (int i = tid; i < n * T::DPR; i += NT) {
-    const int r = i / T::DPR, col = i % T::DPR;
-    const int64_t slot = slot_of(L, j0 + r);
-    tile[r * T::UPR + col] = *reinterpret_cast<const uint4 *>(L.kd + (slot * a.nkv + g) * RB + col * 16);
-  }
-  if (KF == BKV_Q8_0) {
-    for (int r = tid; r < n; r += NT) {
-      const int64_t slot = slot_of(L, j0 + r);
-      tile[r * T::UPR + 16] = *reinterpret_cast<const uint4 *>(L.ks + (slot * a.nkv + g) * kScaleRowBytes);
-    }
-  }
+  stage_rows<NT, T::KEYS, T::DPR, T::UPR>(tile, L.kd, RB, L, a.nkv, g, j0, n);
+  if (KF == BKV_Q8_0) stage_rows<NT, T::KEYS, 1, T::UPR>(tile + 16, L.ks, kScaleRowBytes, L, a.nkv, g, j0, n);
   float qv[kGqa][kHd / 16];
   load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
   __syncthreads();

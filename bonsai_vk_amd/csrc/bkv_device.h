@@ -244,6 +244,36 @@ __device__ __forceinline__ Special ld_spec(const Special *p) {
   return x;
 }
 
+// ------------------------------------------------------------------ row staging into LDS
+// Rows [0, n) of one KV head's array (COLS x 16 B per row, row_bytes_ apart per head slot) at
+// positions j0.. into tile[row * STRIDE + col]; rows [n, ROWS) are zero-filled. Every load of a batch
+// is issued before the first LDS store, and out-of-range rows read position j0 (or 0) so the batch
+// is straight-line code: the batch costs one memory latency, not one per load.
+template <int NT, int ROWS, int COLS, int STRIDE, int BATCH = 8>
+__device__ __forceinline__ void stage_rows(uint4 *tile, const uint8_t *base, int row_bytes_, const LayerView &L,
+                                           int nkv, int g, int64_t j0, int n) {
+  static_assert((ROWS * COLS) % NT == 0, "whole rows per pass");
+  constexpr int PER = ROWS * COLS / NT;
+  constexpr int B = PER < BATCH ? PER : BATCH;
+  static_assert(PER % B == 0, "whole batches");
+#pragma unroll
+  for (int b = 0; b < PER; b += B) {
+    uint4 t[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = threadIdx.x + (b + u) * NT, row = i / COLS, col = i % COLS;
+      const int64_t pos = n > 0 ? j0 + min(row, n - 1) : 0;
+      const uint4 v = *reinterpret_cast<const uint4 *>(base + (slot_of(L, pos) * nkv + g) * (int64_t)row_bytes_ + col * 16);
+      t[u] = row < n ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = threadIdx.x + (b + u) * NT, row = i / COLS, col = i % COLS;
+      tile[row * STRIDE + col] = t[u];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ PV over the fp16 probabilities
 template <int VF>
 struct KRow {

@@ -1,14 +1,17 @@
-// bkv_fused.hip - one cooperative launch per layer and decode token: append, QK in the reference's
-// order, the exact serial softmax sum, PV over fp16 probabilities and the partition merge.
+// bkv_fused.hip - one launch per layer and decode token: append, QK in the reference's order, the
+// exact serial softmax sum, PV over fp16 probabilities and the partition merge.
 //
 // Workgroup w serves KV group g = w % nkv and keys [wi*kpw, (wi+1)*kpw) with wi = w / nkv, in R
-// passes of NT keys (one key per thread; NT = 192 for q8_0 K, 128 for fp16 K). The phases that need every workgroup of a group are
-// joined by arrival counters: a workgroup counts itself in, the last one to arrive does the phase's
-// group-wide step (global max; the walk to the exact sum; nothing for the merge) and raises the
-// phase flag, and every workgroup waits for the flag only after it has arrived itself. The launch is
-// cooperative, so all workgroups are resident and every wait is reached by its producers; each wait
-// is also bounded and records an error word instead of hanging.
-// While a workgroup waits for the exact sum, the first V sub-chunk is already in its registers.
+// passes of NT keys (one key per thread; NT = 192 for q8_0 K, 128 for fp16 K). The phases that need
+// every workgroup of a group are joined by arrival counters: a workgroup counts itself in, the last
+// one to arrive does the phase's group-wide step (global max; the walk to the exact sum; the final
+// merge) and raises the phase flag, and every workgroup waits for the flag only after it has arrived
+// itself. The grid is sized so that all workgroups are resident at once, so every wait is reached by
+// its producers; each wait is also bounded and records an error word instead of hanging.
+// While the walk runs, the other workgroups stage their first V pass into LDS.
+#include <cstdlib>
+#include <cstring>
+
 #include "bkv_common.h"
 #include "bkv_device.h"
 #include "bkv_internal.h"
@@ -40,6 +43,7 @@ __device__ __forceinline__ float2 ld_f2(const float2 *p) {
 // counter. Each counter is reset by its last arrival, ready for the next call. Returns true (in every
 // thread) for the overall last arrival.
 constexpr int kSub = 8;
+constexpr int kMergeBatch = 12;   // partials whose loads are in flight together in the merge
 __device__ __forceinline__ bool arrive(unsigned *cnt, unsigned *sub, int idx, int n, unsigned *sh) {
   __builtin_amdgcn_s_waitcnt(0);           // this thread's write-through stores have completed
   __syncthreads();
@@ -78,11 +82,14 @@ __device__ __forceinline__ void wait_flag(const unsigned *flag, unsigned gen, un
   __syncthreads();
 }
 
-// ---------------------------------------------------------------- the walk of one head (one wave)
+// ---------------------------------------------------------------- the walk (one wave, 1..NHW heads)
 // Records rec[c] / specials spec[c][..] of the group's workgroups in key order, each covering kpw
 // keys. The fields of every special (global key index, global increment prefix, binade of the step
 // before it, the whole ulps of the segment before it) are resolved in parallel across the wave into
-// LDS; the serial chain then only carries the running sum (wave-uniform, readlane per special).
+// LDS. The serial chain then carries only the running sum: per special, the bits of the sum advance
+// by the segment's ulps (an integer add, valid while the sum stays in the recorded binade) and the
+// special's e is added in fp32. The binade conditions are checked afterwards, in parallel, on the
+// sums recorded before each step. A wave walks its heads' chains interleaved.
 constexpr int kWalkWg = kFusedMaxGroupWgs;   // workgroups per group the scratch holds
 constexpr int kWalkCap = 384;      // specials per head the scratch holds (more: serial fallback)
 struct WalkScratch {
@@ -91,103 +98,197 @@ struct WalkScratch {
   long long si[kWalkCap];
   int sk[kWalkCap];
   float se[kWalkCap];
-  int sb[kWalkCap], sdu[kWalkCap];
+  int sck[kWalkCap];               // binade exponent field the step must start and end in, -1: no advance
+  int sdu[kWalkCap];               // ulps the sum advances by before the special (0: none)
 };
 
-__device__ bool walk_head(const ChunkRec *rec, const Special *spec, int gg, int64_t kpw, int64_t nfill,
-                          WalkScratch &w, float &s_out) {
+#ifdef BKV_EXPERIMENT_TS
+#define WTS(q, i) do { if (tsp[q] && (threadIdx.x & 63) == 0) tsp[q][i] = (unsigned)wall_clock64(); } while (0)
+#else
+#define WTS(q, i) do { } while (0)
+#endif
+
+template <int NHW>
+__device__ void walk_heads(const ChunkRec *const *rec, const Special *const *spec, int nhere, int gg,
+                           int64_t kpw, int64_t nfill, WalkScratch *const *ws, float *s_out, bool *good_out,
+                           unsigned *const *tsp) {
   const int lane = threadIdx.x & 63;
-  if (gg > kWalkWg) return false;
-  long long ibase = 0;
-  int obase = 0, blast_prev = kNoBinade;
-  bool over = false;
-  for (int cb = 0; cb < gg; cb += 64) {
-    const int c = cb + lane;
-    ChunkRec r;
-    r.tot = 0; r.nsp = 0; r.blast = kNoBinade;
-    if (c < gg) r = ld_rec(&rec[c]);
-    over |= r.nsp > kMaxSpecial;
-    const int cnt = min(r.nsp, kMaxSpecial);
-    const long long incl = wave_incl_scan<long long>(r.tot, lane);
-    const int oincl = wave_incl_scan<int>(cnt, lane);
-    int bp = __shfl_up(r.blast, 1);
-    if (lane == 0) bp = blast_prev;
-    if (c < gg) {
-      w.wg_ib[c] = ibase + incl - r.tot;
-      w.wg_off[c] = obase + oincl - cnt;
-      w.wg_bp[c] = bp;
+  constexpr int kRounds = (kWalkWg + 63) / 64;
+  int T[NHW], blast_last[NHW];
+  long long itot[NHW];
+  bool ok[NHW];
+  // 1. every record of every head in one round trip, then the prefix scans
+  ChunkRec r[NHW][kRounds];
+#pragma unroll
+  for (int q = 0; q < NHW; ++q)
+#pragma unroll
+    for (int rr = 0; rr < kRounds; ++rr) {
+      const int c = rr * 64 + lane;
+      r[q][rr].tot = 0; r[q][rr].nsp = 0; r[q][rr].blast = kNoBinade;
+      if (q < nhere && c < gg) r[q][rr] = ld_rec(&rec[q][c]);
     }
-    const int nb = min(64, gg - cb);
-    ibase += __shfl(incl, 63);
-    obase += __shfl(oincl, 63);
-    blast_prev = __shfl(r.blast, nb - 1);
-  }
-  if (lane == 0) w.wg_off[gg] = obase;
-  if (__any(over) || obase > kWalkCap) return false;
-  const int T = obase;
-  __builtin_amdgcn_wave_barrier();
-  for (int o = lane; o < T; o += 64) {
-    int lo = 0, hi = gg - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (w.wg_off[mid] <= o) lo = mid; else hi = mid - 1;
-    }
-    const Special x = ld_spec(&spec[(size_t)lo * kMaxSpecial + (o - w.wg_off[lo])]);
-    const int bf = (x.meta >> 16) & 0xFF;
-    w.si[o] = w.wg_ib[lo] + x.ipre;
-    w.sk[o] = (int)(lo * kpw + (x.meta & 0xFFFF));
-    w.se[o] = x.e;
-    w.sb[o] = bf == 255 ? w.wg_bp[lo] : (bf == 0 ? kNoBinade : bf - 128);
-  }
-  __builtin_amdgcn_wave_barrier();
-  bool bad = false;
-  for (int o = lane; o < T; o += 64) {
-    const long long gap = w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
-    const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
-    int du = -1;
-    if (gap > 1) {
-      const int B = w.sb[o];
-      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24))
-        bad = true;
-      else
-        du = (int)(di >> (B + 17));
-    } else if (di != 0) {
-      bad = true;
-    }
-    w.sdu[o] = du;
-  }
-  if (__any(bad)) return false;
-  __builtin_amdgcn_wave_barrier();
-  float s = 0.0f;
-  bool good = true;
-  for (int base = 0; base < T; base += 64) {
-    const int o = base + lane;
-    const int du_l = o < T ? w.sdu[o] : -1, b_l = o < T ? w.sb[o] : 0;
-    const float e_l = o < T ? w.se[o] : 0.0f;
-    const int cnt = min(64, T - base);
-    for (int i = 0; i < cnt; ++i) {
-      const int du = __builtin_amdgcn_readlane(du_l, i);
-      const int b = __builtin_amdgcn_readlane(b_l, i);
-      const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), i));
-      if (du >= 0) {
-        const uint32_t bits = __float_as_uint(s);
-        const uint32_t m = ((bits & 0x7FFFFFu) | 0x800000u) + (uint32_t)du;
-        good = good && (int)(bits >> 23) == b + 127 && m < (1u << 24);
-        s = __uint_as_float(((uint32_t)(b + 127) << 23) | (m & 0x7FFFFFu));
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    ok[q] = q < nhere && gg <= kWalkWg;
+    long long ibase = 0;
+    int obase = 0, blast_prev = kNoBinade;
+    bool over = false;
+    WalkScratch &w = *ws[q];
+#pragma unroll
+    for (int rr = 0; rr < kRounds; ++rr) {
+      if (rr * 64 < gg) {
+        const int c = rr * 64 + lane;
+        const ChunkRec x = r[q][rr];
+        over |= x.nsp > kMaxSpecial;
+        const int cnt = min(x.nsp, kMaxSpecial);
+        const long long incl = wave_incl_scan<long long>(x.tot, lane);
+        const int oincl = wave_incl_scan<int>(cnt, lane);
+        int bp = __shfl_up(x.blast, 1);
+        if (lane == 0) bp = blast_prev;
+        if (q < nhere && c < gg) {
+          w.wg_ib[c] = ibase + incl - x.tot;
+          w.wg_off[c] = obase + oincl - cnt;
+          w.wg_bp[c] = bp;
+        }
+        const int nb = min(64, gg - rr * 64);
+        ibase += __shfl(incl, 63);
+        obase += __shfl(oincl, 63);
+        blast_prev = __shfl(x.blast, nb - 1);
       }
-      s = __fadd_rn(s, ev);
+    }
+    if (q < nhere && lane == 0) w.wg_off[gg] = obase;
+    ok[q] = ok[q] && !__any(over) && obase <= kWalkCap;
+    T[q] = ok[q] ? obase : 0;
+    itot[q] = ibase;
+    blast_last[q] = blast_prev;
+    WTS(q, 0);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 2. the specials, resolved to global key index, increment prefix and starting binade (the loads
+  // of all heads are issued before any is used)
+  {
+    int Tm = 0;
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) Tm = max(Tm, T[q]);
+    for (int o = lane; o < Tm; o += 64) {
+      int lo[NHW];
+      Special x[NHW];
+#pragma unroll
+      for (int q = 0; q < NHW; ++q) {
+        const WalkScratch &w = *ws[q];
+        int l = 0, hi = gg - 1;
+        if (o < T[q]) {
+          while (l < hi) {
+            const int mid = (l + hi + 1) >> 1;
+            if (w.wg_off[mid] <= o) l = mid; else hi = mid - 1;
+          }
+        }
+        lo[q] = l;
+      }
+#pragma unroll
+      for (int q = 0; q < NHW; ++q)
+        if (o < T[q]) x[q] = ld_spec(&spec[q][(size_t)lo[q] * kMaxSpecial + (o - ws[q]->wg_off[lo[q]])]);
+#pragma unroll
+      for (int q = 0; q < NHW; ++q) {
+        if (o < T[q]) {
+          WalkScratch &w = *ws[q];
+          const int bf = (x[q].meta >> 16) & 0xFF;
+          w.si[o] = w.wg_ib[lo[q]] + x[q].ipre;
+          w.sk[o] = (int)(lo[q] * kpw + (x[q].meta & 0xFFFF));
+          w.se[o] = x[q].e;
+          w.sck[o] = bf == 255 ? w.wg_bp[lo[q]] : (bf == 0 ? kNoBinade : bf - 128);   // binade B for now
+        }
+      }
     }
   }
-  // the trailing segment after the last special
-  const long long k_last = T > 0 ? w.sk[T - 1] : -1, i_last = T > 0 ? w.si[T - 1] : 0;
-  if (good && nfill - 1 - k_last > 0) good = advance(s, blast_prev, ibase - i_last);
-  s_out = s;
-  return good;
+  __builtin_amdgcn_wave_barrier();
+  // 3. per special: the ulps of the segment before it in its binade
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    WalkScratch &w = *ws[q];
+    WTS(q, 1);
+    bool bad = false;
+    for (int o = lane; o < T[q]; o += 64) {
+      const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+      const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+      int du = 0, ck = -1;
+      if (gap > 1) {
+        const int B = w.sck[o];
+        if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24)) {
+          bad = true;
+        } else {
+          du = (int)(di >> (B + 17));
+          ck = B + 127;
+        }
+      } else if (di != 0) {
+        bad = true;
+      }
+      w.sdu[o] = du;
+      w.sck[o] = ck;
+    }
+    ok[q] = ok[q] && !__any(bad);
+    if (!ok[q]) T[q] = 0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 4. the chains, 16 steps per unrolled block; entries past T are du 0, e 0 (no change)
+  float s[NHW];
+  bool bad[NHW];
+  int Tm = 0;
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) { s[q] = 0.0f; bad[q] = false; Tm = max(Tm, T[q]); WTS(q, 2); }
+  for (int base = 0; base < Tm; base += 64) {
+    const int o = base + lane;
+    int du_l[NHW], ck_l[NHW];
+    float e_l[NHW];
+    uint32_t pre[NHW];
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) {
+      const bool in = o < T[q];
+      du_l[q] = in ? ws[q]->sdu[o] : 0;
+      ck_l[q] = in ? ws[q]->sck[o] : -1;
+      e_l[q] = in ? ws[q]->se[o] : 0.0f;
+      pre[q] = 0u;
+    }
+    const int cnt = min(64, Tm - base);
+    for (int j0 = 0; j0 < cnt; j0 += 16) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = j0 + jj;
+#pragma unroll
+        for (int q = 0; q < NHW; ++q) {
+          const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l[q], j);
+          const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l[q]), j));
+          const uint32_t bits = __float_as_uint(s[q]);
+          pre[q] = lane == j ? bits : pre[q];
+          s[q] = __fadd_rn(__uint_as_float(bits + du), ev);
+        }
+      }
+    }
+    // the binade conditions of this block's steps: start in binade ck, no carry out of it
+#pragma unroll
+    for (int q = 0; q < NHW; ++q)
+      if (ck_l[q] >= 0)
+        bad[q] |= (int)(pre[q] >> 23) != ck_l[q] || (int)((pre[q] + (uint32_t)du_l[q]) >> 23) != ck_l[q];
+  }
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    WTS(q, 3);
+    bool good = ok[q] && !__any(bad[q]);
+    // the trailing segment after the last special
+    const long long k_last = T[q] > 0 ? ws[q]->sk[T[q] - 1] : -1, i_last = T[q] > 0 ? ws[q]->si[T[q] - 1] : 0;
+    float sq = s[q];
+    if (good && nfill - 1 - k_last > 0) good = advance(sq, blast_last[q], itot[q] - i_last);
+    s_out[q] = sq;
+    good_out[q] = good;
+#ifdef BKV_EXPERIMENT_TS
+    if (tsp[q] && lane == 0) tsp[q][4] = T[q];
+#endif
+  }
 }
 
 #ifdef BKV_EXPERIMENT_TS
-// phase timestamps of workgroup (w) into the sync area's upper half: [w][16] u64
-#define FTS(i) do { if (threadIdx.x == 0 && blockIdx.x < 256) reinterpret_cast<unsigned long long *>(a.sync + 32768)[blockIdx.x * 16 + (i)] = wall_clock64(); } while (0)
+// phase timestamps of workgroup (w) into the sync area's upper half: [w][16] u32
+#define FTS(i) do { if (threadIdx.x == 0 && blockIdx.x < 768) (a.sync + 32768)[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
 #else
 #define FTS(i) do { } while (0)
 #endif
@@ -200,19 +301,10 @@ struct FusedCfg {
 };
 
 // q8_0 V data rows [j0, j0+n) of group g into the LDS tile, 256 B per row (16 lanes read a row's
-// 256 contiguous bytes: conflict-free); the block scales stay in registers.
-// Rows [n, NT) are zero-filled so that the PV loop needs no bounds test.
+// 256 contiguous bytes: conflict-free), zero beyond n; the block scales stay in registers.
 template <int NT>
 __device__ __forceinline__ void load_v_tile(uint4 *tile, const LayerView &L, int nkv, int g, int64_t j0, int n) {
-  for (int i = threadIdx.x; i < NT * 16; i += NT) {
-    const int row = i >> 4, col = i & 15;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (row < n) {
-      const int64_t slot = slot_of(L, j0 + row);
-      v = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * row_bytes(BKV_Q8_0) + col * 16);
-    }
-    tile[i] = v;
-  }
+  stage_rows<NT, NT, 16, 16, 4>(tile, L.vd, row_bytes(BKV_Q8_0), L, nkv, g, j0, n);
 }
 
 template <int KF, int VF, bool FUSE>
@@ -243,13 +335,14 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
   const int64_t kend = min((int64_t)a.nfill, kbase + (int64_t)a.kpw);   // this workgroup's keys
   const LayerView &L = a.L;
   unsigned *sync = a.sync;
-  // sync words, one 256 B line each: per group 32 lines (3 counters, 3 flags, 3 x 8 sub-counters),
-  // then the generation, the end-of-call counter (+ 8 sub-counters) and the error word
-  unsigned *gl = sync + (size_t)g * 32 * kCounterStride;
+  // sync words, one 256 B line each: per group kGroupLines lines (3 counters, 3 flags, 8 + 8
+  // sub-counters of phases A and B, kMergeSub of the merge), then the generation, the end-of-call
+  // counter (+ 8 sub-counters) and the error word
+  unsigned *gl = sync + (size_t)g * kGroupLines * kCounterStride;
   unsigned *cntA = gl, *cntB = gl + kCounterStride, *cntC = gl + 2 * kCounterStride;
   unsigned *flA = gl + 3 * kCounterStride, *flB = gl + 4 * kCounterStride, *flC = gl + 5 * kCounterStride;
   unsigned *subA = gl + 6 * kCounterStride, *subB = gl + 14 * kCounterStride, *subC = gl + 22 * kCounterStride;
-  unsigned *top = sync + (size_t)nkv * 32 * kCounterStride;
+  unsigned *top = sync + (size_t)nkv * kGroupLines * kCounterStride;
   unsigned *genp = top, *cntD = top + kCounterStride, *subD = top + 2 * kCounterStride;
   unsigned *err = top + 10 * kCounterStride;
   const unsigned gen = ld_agent(genp) + 1u;
@@ -275,17 +368,8 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
     if (r < R) {
       const int64_t j0 = kbase + (int64_t)r * NT;
       const int n = (int)max((int64_t)0, min((int64_t)NT, kend - j0));
-      for (int i = tid; i < n * DPR; i += NT) {
-        const int row = i / DPR, col = i % DPR;
-        const int64_t slot = slot_of(L, j0 + row);
-        tile[row * UPR + col] = *reinterpret_cast<const uint4 *>(L.kd + (slot * nkv + g) * RB + col * 16);
-      }
-      if (KF == BKV_Q8_0) {
-        for (int row = tid; row < n; row += NT) {
-          const int64_t slot = slot_of(L, j0 + row);
-          tile[row * UPR + 16] = *reinterpret_cast<const uint4 *>(L.ks + (slot * nkv + g) * kScaleRowBytes);
-        }
-      }
+      stage_rows<NT, NT, DPR, UPR>(tile, L.kd, RB, L, nkv, g, j0, n);
+      if (KF == BKV_Q8_0) stage_rows<NT, NT, 1, UPR>(tile + 16, L.ks, kScaleRowBytes, L, nkv, g, j0, n);
       __syncthreads();
       float acc[kGqa];
       qk_row_dot<KF>(tile + tid * UPR, qv, acc);
@@ -418,26 +502,48 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
   // ---------------------------------------------------------------- phase B: the exact sums
   FTS(5);
   if (arrive(cntB, subB, wi, gg, &s_flag)) {
-    // each wave walks heads wave, wave+NW, ...; LDS scratch: the K tile, one WalkScratch per head
-    for (int h = wave; h < kGqa; h += NW) {
-      const int hh = g * kGqa + h;
-      WalkScratch *ws = reinterpret_cast<WalkScratch *>(tile) + h;
-      float s = 0.0f;
-      bool good = walk_head(a.rec + (size_t)hh * gg, a.spec + (size_t)hh * gg * kMaxSpecial, gg,
-                            (int64_t)a.kpw, (int64_t)a.nfill, *ws, s);
-      if (!good) {
-        // fallback: the serial loop itself over the stored e of this head
-        float ss = 0.0f;
-        for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
-          const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
-          const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
-          for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+    // wave w walks heads w, w+NW, ... interleaved; LDS scratch: the K tile, one WalkScratch per head
+    constexpr int NHW = (kGqa + NW - 1) / NW;
+    const ChunkRec *rp[NHW];
+    const Special *spp[NHW];
+    WalkScratch *wsp[NHW];
+    unsigned *tsp[NHW];
+    float sres[NHW];
+    bool gres[NHW];
+    int nhere = 0;
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) {
+      const int h = min(wave + q * NW, kGqa - 1), hh = g * kGqa + h;
+      if (wave + q * NW < kGqa) nhere = q + 1;
+      rp[q] = a.rec + (size_t)hh * gg;
+      spp[q] = a.spec + (size_t)hh * gg * kMaxSpecial;
+      wsp[q] = reinterpret_cast<WalkScratch *>(tile) + h;
+#ifdef BKV_EXPERIMENT_TS
+      tsp[q] = a.sync + 32768 + 768 * 16 + hh * 8;
+#else
+      tsp[q] = nullptr;
+#endif
+    }
+    walk_heads<NHW>(rp, spp, nhere, gg, (int64_t)a.kpw, (int64_t)a.nfill, wsp, sres, gres, tsp);
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) {
+      if (q < nhere) {
+        const int hh = g * kGqa + wave + q * NW;
+        float s = sres[q];
+        if (!gres[q]) {
+          // fallback: the serial loop itself over the stored e of this head
+          float ss = 0.0f;
+          for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
+            const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
+            const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
+            for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+          }
+          s = ss;
         }
-        s = ss;
-      }
-      if (lane == 0) {
-        st_agent(&a.sum[hh], s);
-        st_agent(&a.status[hh], good ? 0u : 1u);
+        if (lane == 0) {
+          st_agent(&a.sum[hh], s);
+          st_agent(&a.status[hh], gres[q] ? 0u : 1u);
+        }
       }
     }
     publish(flB, gen);
@@ -499,7 +605,7 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
         reinterpret_cast<uint2 *>(s_p16)[tid] = pw;
       }
       __syncthreads();
-#pragma unroll (VF == BKV_Q8_0 ? VIT : 4)
+#pragma unroll VF == BKV_Q8_0 ? VIT : 4
       for (int it = 0; it < VIT; ++it) {
         const int row = wave * VR::KPW + vkk + it * NW * VR::KPW;
         const bool valid = row < n;
@@ -543,37 +649,62 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
   }
   __syncthreads();
   float *part_g = a.part + (size_t)g * gg * kGqa * kHd;
-  for (int d = tid; d < kHd; d += NT) {
+  constexpr int kPairs = kGqa * kHd / 2;                  // a partial is [kGqa][kHd] fp32
+  constexpr int PIT = (kPairs + NT - 1) / NT;
+  for (int i = 0; i < PIT; ++i) {
+    const int pr = tid + i * NT;
+    if (pr < kPairs) {
+      float2 v = make_float2(0.0f, 0.0f);
 #pragma unroll
-    for (int h = 0; h < kGqa; ++h) {
-      float v = 0.0f;
-#pragma unroll
-      for (int i = 0; i < NW; ++i) v += s_red[(i * kGqa + h) * kHd + d];
-      st_agent(&part_g[((size_t)wi * kGqa + h) * kHd + d], v);
+      for (int wv = 0; wv < NW; ++wv) {
+        v.x += s_red[wv * kGqa * kHd + 2 * pr];
+        v.y += s_red[wv * kGqa * kHd + 2 * pr + 1];
+      }
+      st_f2(reinterpret_cast<float2 *>(part_g + (size_t)wi * kGqa * kHd) + pr, v);
     }
   }
 
   // ---------------------------------------------------------------- phase C: merge + gate
-  // Two-level, no waiting: the last arrival of each sub-group (wi % 8) sums its members' partials
+  // Two-level, no waiting: the last arrival of each sub-group (wi % kMergeSub) sums its members' partials
   // in member order into a sub-partial, and the last of those sums the sub-partials in order.
+  // The loads are issued kMergeBatch partials at a time so their latencies overlap.
   {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const int k = wi % kSub, members = (gg - k + kSub - 1) / kSub, nsub = gg < kSub ? gg : kSub;
+    const int k = wi % kMergeSub, members = (gg - k + kMergeSub - 1) / kMergeSub;
+    const int nsub = gg < kMergeSub ? gg : kMergeSub;
     if (tid == 0) s_flag = atomicAdd(subC + k * kCounterStride, 1u) == (unsigned)(members - 1) ? 1u : 0u;
     __syncthreads();
     if (s_flag) {
       if (tid == 0) st_agent(subC + k * kCounterStride, 0u);
-      float *sp = a.subpart + ((size_t)g * kSub + k) * kGqa * kHd;
-      for (int d = tid; d < kHd; d += NT) {
+      float2 acc2[PIT];
+      // sum of cnt blocks src + (first + m*step) * kGqa*kHd, m = 0..cnt-1, in m order
+      auto sum_blocks = [&](const float *src, int first, int step, int cnt) {
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          float v = 0.0f;
-          for (int m = 0; m < members; ++m)
-            v += ld_agent(&part_g[((size_t)(k + m * kSub) * kGqa + h) * kHd + d]);
-          st_agent(&sp[h * kHd + d], v);
+        for (int i = 0; i < PIT; ++i) acc2[i] = make_float2(0.0f, 0.0f);
+        for (int m0 = 0; m0 < cnt; m0 += kMergeBatch) {
+          float2 t[kMergeBatch][PIT];
+#pragma unroll
+          for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < PIT; ++i) {
+              const int pr = tid + i * NT;
+              t[u][i] = (m0 + u < cnt && pr < kPairs)
+                            ? ld_f2(reinterpret_cast<const float2 *>(src + (size_t)(first + (m0 + u) * step) * kGqa * kHd) + pr)
+                            : make_float2(0.0f, 0.0f);
+            }
+#pragma unroll
+          for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < PIT; ++i)
+              if (m0 + u < cnt) { acc2[i].x += t[u][i].x; acc2[i].y += t[u][i].y; }
         }
-      }
+      };
+      sum_blocks(part_g, k, kMergeSub, members);
+      float2 *sp = reinterpret_cast<float2 *>(a.subpart + ((size_t)g * kMergeSub + k) * kGqa * kHd);
+#pragma unroll
+      for (int i = 0; i < PIT; ++i)
+        if (tid + i * NT < kPairs) st_f2(sp + tid + i * NT, acc2[i]);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (tid == 0) {
@@ -582,15 +713,19 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
       }
       __syncthreads();
       if (s_flag) {
-        for (int d = tid; d < kHd; d += NT) {
+        sum_blocks(a.subpart + (size_t)g * kMergeSub * kGqa * kHd, 0, 1, nsub);
 #pragma unroll
-          for (int h = 0; h < kGqa; ++h) {
-            float v = 0.0f;
-            for (int kk = 0; kk < nsub; ++kk)
-              v += ld_agent(&a.subpart[(((size_t)g * kSub + kk) * kGqa + h) * kHd + d]);
-            const size_t oi = ((size_t)g * kGqa + h) * kHd + d;
-            a.out[oi] = v;
-            if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+        for (int i = 0; i < PIT; ++i) {
+          const int pr = tid + i * NT;
+          if (pr < kPairs) {
+            const size_t oi = (size_t)g * kGqa * kHd + 2 * pr;   // out is [nh][kHd], head g*kGqa+h
+            const float2 v = acc2[i];
+            *reinterpret_cast<float2 *>(a.out + oi) = v;
+            if (a.gate) {
+              const float2 gt = *reinterpret_cast<const float2 *>(a.gate + oi);
+              *reinterpret_cast<float2 *>(a.out_gated + oi) =
+                  make_float2(v.x * (1.0f / (1.0f + exp_cr(-gt.x))), v.y * (1.0f / (1.0f + exp_cr(-gt.y))));
+            }
           }
         }
       }
@@ -633,16 +768,23 @@ int fused_max_workgroups(int kf, int vf) {
   return 0;
 }
 
+// The grid never exceeds what the occupancy query says is resident at once on the device, so on a
+// device not held by other long-running kernels every workgroup is running and each wait is reached
+// by its producers. A plain launch is the default (a cooperative launch costs ~18 us more per call on
+// ROCm 7); BKV_FUSED_LAUNCH=cooperative asks the runtime to guarantee co-residency instead. Either
+// way every wait is bounded and records an error word rather than hanging.
 hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st) {
+  const char *ev = getenv("BKV_FUSED_LAUNCH");
+  const bool cooperative = ev && strcmp(ev, "cooperative") == 0;
   const dim3 grid(a.gg * a.nkv);
   void *args[] = {const_cast<FusedArgs *>(&a)};
   hipError_t e = hipErrorInvalidValue;
   BKV_FMT_SWITCH(kf, vf, {
     const dim3 block(FusedCfg<KF_>::NT);
-    if (fuse)
-      e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, true>), grid, block, args, 0, st);
-    else
-      e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, false>), grid, block, args, 0, st);
+    const void *fn = fuse ? reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, true>)
+                          : reinterpret_cast<const void *>(&fused_kernel<KF_, VF_, false>);
+    e = cooperative ? hipLaunchCooperativeKernel(fn, grid, block, args, 0, st)
+                    : hipLaunchKernel(fn, grid, block, args, 0, st);
   });
   return e;
 }

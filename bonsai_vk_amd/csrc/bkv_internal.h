@@ -91,6 +91,10 @@ struct RedArgs {
 constexpr int kRMax = 2;                     // key passes per workgroup of the fused kernel
 // workgroups per KV group of the fused launch at most (the walker's LDS scratch holds this many)
 constexpr int kFusedMaxGroupWgs = 192;
+// merge sub-groups of the fused kernel (the sub-partials buffer holds kMergeSub per KV group) and the
+// 256 B sync lines each KV group uses: 3 counters, 3 flags, 8 + 8 phase sub-counters, kMergeSub
+constexpr int kMergeSub = 16;
+constexpr int kGroupLines = 22 + kMergeSub;
 constexpr size_t kSyncBytes = 256 * 1024;  // counters / flags at the start of every workspace
 constexpr size_t kSyncMaxOffset = 192 * 1024;   // the fused kernel's running-max slots [2][nh]
 
@@ -109,7 +113,7 @@ struct FusedArgs {
   float2 *stats;                 // [nh][gg]
   unsigned *mxenc;               // [2][nh] running max (order-preserving bits), by call parity
   int nh;
-  float *subpart;                // [nkv][8][kGqa][hd]
+  float *subpart;                // [nkv][kMergeSub][kGqa][hd]
   ChunkRec *rec;                 // [nh][gg]
   Special *spec;                 // [nh][gg][kMaxSpecial]
   float *e;                      // [nh][ld]
