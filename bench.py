@@ -45,6 +45,24 @@ def gen_cache(cache, n, seed, layers):
     torch.cuda.synchronize()
 
 
+def kernel_name(cache, n):
+    """The launch(es) one decode_step call makes at n keys."""
+    return ("fused_kernel (one launch per layer: append, QK, exact sum, PV, merge)"
+            if cache.decode_path(n) == 1 else
+            "qk_kernel + e_kernel + pv_kernel + merge_kernel (four launches per layer)")
+
+
+def measured_traffic(cache, n):
+    """HBM bytes per launch of the fused kernel at this workload, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/), or None when that summary is absent or the call
+    takes the split path."""
+    path = os.path.join(ROOT, "profiles", "fused_kernel_q8_32k_traffic.json")
+    if cache.decode_path(n) != 1 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def cpu_baseline(ctx, seed=2):
     """The CPU oracle (serial per head row, OpenMP over the 16 rows of a layer) on a bounded sample:
     one layer's decode step at ctx+1 keys, scaled to 8 layers. Returns the baseline object."""
@@ -62,7 +80,7 @@ def cpu_baseline(ctx, seed=2):
     while True:
         host.decode(0, n, q, nthreads=cores)
         reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+        if time.perf_counter() - t0 > 10.0 or reps >= 1000:
             break
     per_layer = (time.perf_counter() - t0) / reps
     t1 = time.perf_counter()
@@ -83,6 +101,9 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gate", action="store_true", help="also read the gate and write GOUT")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="after the timed region, copy a MIB MiB buffer once (a reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the KV path is sharded across GPUs by "
@@ -93,13 +114,14 @@ def main():
     from bonsai_vk_amd import BKV_Q8_0, KvCache
 
     L, K, W, ctx = args.layers, args.steps, args.warmup, args.ctx
-    cap = ctx + K + 1
+    RP = 16                                 # roofline pass: steps after the timed region
+    cap = ctx + K + RP + 1
     cache = KvCache(n_layers=L, cap=cap, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=cap)
     prefill = ctx - W                       # warmup appends positions ctx-W .. ctx-1
     gen_cache(cache, prefill, seed=2, layers=L)
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
-    nstep = W + K
+    nstep = W + K + RP
     knew = torch.randn(nstep, L, 1, 4, 256, generator=g, device="cuda")
     vnew = torch.randn(nstep, L, 1, 4, 256, generator=g, device="cuda") * 0.5
     q = torch.randn(nstep, L, 16, 256, generator=g, device="cuda")
@@ -107,37 +129,47 @@ def main():
     out = torch.empty(L, 16, 256, device="cuda")
     og = torch.empty(L, 16, 256, device="cuda") if args.gate else None
 
-    def step(i, ev=None):
+    def step(i):
         pos = prefill + i
         for layer in range(L):
-            if ev is not None:
-                ev[layer][0].record()
             cache.decode_step(layer, pos, knew[i, layer], vnew[i, layer], q[i, layer],
                               None if gate is None else gate[i, layer], out[layer],
                               None if og is None else og[layer])
-            if ev is not None:
-                ev[layer][1].record()
 
     for i in range(W):
         step(i)
     torch.cuda.synchronize()
-    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(L)]
-           for _ in range(K)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
     for i in range(K):
-        step(W + i, evs[i])
+        step(W + i)
     t_end.record()
     torch.cuda.synchronize()
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / K
-    call_ms = [evs[i][l][0].elapsed_time(evs[i][l][1]) for i in range(K) for l in range(L)]
-    avg_call_s = sum(call_ms) / len(call_ms) / 1e3
     ns = [ctx + 1 + i for i in range(K)]
     bytes_step = sum(L * algorithmic_bytes(n, args.gate) for n in ns) / K
-    achieved = bytes_step / L / avg_call_s / 1e9
+
+    # roofline pass (not part of the timed region): HIP events on the launch stream at step
+    # boundaries only, so the per-launch average carries no per-call event overhead
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(RP + 1)]
+    evs[0].record()
+    for i in range(RP):
+        step(W + K + i)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    avg_call_s = sum(evs[i].elapsed_time(evs[i + 1]) for i in range(RP)) / RP / L / 1e3
+    rp_bytes = sum(algorithmic_bytes(ctx + 1 + K + i, args.gate) for i in range(RP)) / RP
+    achieved = rp_bytes / avg_call_s / 1e9
+
+    if args.copy_calib:
+        src = torch.empty(args.copy_calib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     line = {
         "metric": "us/token decode attn+KV append at 32K ctx (8 layers); achieved HBM GB/s % peak",
@@ -149,9 +181,11 @@ def main():
                                "(BASELINE config 3)", "ctx": ctx, "layers": L, "nh": 16, "nkv": 4,
                    "hd": 256, "gate": bool(args.gate)},
         "achieved_gbs_step": round(bytes_step / (ms_step / 1e3) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "bkv_decode_step (one layer: qk+pv+merge launches)",
+        "roofline": {"bound": "hbm", "kernel": kernel_name(cache, ns[0]),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(cache, ns[0]),
+                     "algorithmic_bytes": round(rp_bytes),
                      "avg_call_us": round(avg_call_s * 1e6, 3)},
     }
     if not args.no_cpu:

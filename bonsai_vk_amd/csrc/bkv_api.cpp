@@ -29,10 +29,11 @@ static inline int64_t next_pow2(int64_t x) {
 }
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Partition sizes. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16 keys). Probability
-// chunks: 256 keys. PV: enough workgroups to cover the chip (512 at nkv = 4) with 16..512 keys each.
-// Every array is sized by a bound that grows monotonically with n, so a workspace sized for max_ctx
-// fits every n <= max_ctx.
+// Partition sizes of the split path. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16
+// keys). Probability chunks: kE2Chunk keys. PV: enough workgroups to cover the chip (512 at nkv = 4)
+// with 16..512 keys each. The fused path: as many workgroups per KV group as stay resident (at most
+// kFusedMaxGroupWgs), each with kpw consecutive keys in at most kRMax passes. Every array is sized
+// by a bound that grows monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx.
 // BKV_DECODE=split selects the four-launch path (read on every call, so tests can switch it)
 static bool force_split() {
   const char *e = std::getenv("BKV_DECODE");
@@ -165,6 +166,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if (nfill == 0 || (int64_t)nfill > max_positions(d)) return BKV_ECAP;
   if (!aligned16(q) || !aligned16(out)) return q && out ? BKV_EALIGN : BKV_EINVAL;
   if ((gate == nullptr) != (out_gated == nullptr)) return BKV_EINVAL;
+  if (gate && (!aligned16(gate) || !aligned16(out_gated))) return BKV_EALIGN;
   if (!ws) return BKV_EWORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return BKV_EALIGN;
   const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
