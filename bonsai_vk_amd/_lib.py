@@ -4,7 +4,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbkv.so")
+# BKV_LIBRARY points the binding at another build of the same sources (e.g. one compiled with
+# per-phase timestamps for profiling); the default is the in-tree libbkv.so
+LIB_PATH = os.environ.get("BKV_LIBRARY") or os.path.join(HERE, "libbkv.so")
 
 BKV_F16, BKV_Q8_0 = 0, 1
 BKV_OP_DECODE, BKV_OP_PREFILL = 0, 1

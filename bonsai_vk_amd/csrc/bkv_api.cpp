@@ -34,10 +34,16 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // with 16..512 keys each. The fused path: as many workgroups per KV group as stay resident (at most
 // kFusedMaxGroupWgs), each with kpw consecutive keys in at most kRMax passes. Every array is sized
 // by a bound that grows monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx.
-// BKV_DECODE=split selects the four-launch path (read on every call, so tests can switch it)
-static bool force_split() {
+// BKV_DECODE selects a decode implementation: "split" (four launches), "fused" (the older single
+// launch) or "resident" (the default). Read on every call, so tests can switch it.
+enum { kPathSplit = 0, kPathFused = 1, kPathResident = 2 };
+static int forced_path() {
   const char *e = std::getenv("BKV_DECODE");
-  return e && std::strcmp(e, "split") == 0;
+  if (!e) return -1;
+  if (std::strcmp(e, "split") == 0) return kPathSplit;
+  if (std::strcmp(e, "fused") == 0) return kPathFused;
+  if (std::strcmp(e, "resident") == 0) return kPathResident;
+  return -1;
 }
 
 DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
@@ -90,8 +96,46 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
       total = std::max(total, f);
     }
   }
+  // the resident path: one workgroup per CU, up to kResMaxG per KV group, >= 64 keys each
+  p.rG = 0;
+  const int rcap = resident_max_workgroups(kfmt, vfmt);
+  const bool rsync_fits = kResSyncOffset + ((size_t)nkv * kResGroupLines + 1) * kCounterStride * sizeof(unsigned) <= kSyncBytes;
+  const bool rtags_fit = kResTagOffset + (size_t)nh * kResMaxGroupWgs * 3 * sizeof(unsigned long long) <= kResSyncOffset;
+  if (rcap >= nkv && rsync_fits && rtags_fit) {
+    const int64_t gmax = std::min<int64_t>(rcap / nkv, kResMaxGroupWgs);
+    const int64_t kpw = cdiv(n, std::min<int64_t>(gmax, cdiv(n, 64)));
+    if (kpw <= (int64_t)kResMaxPass * kResNT) {
+      p.rkpw = (int)kpw;
+      p.rG = (int)cdiv(n, kpw);
+      p.rvres = vfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
+      size_t f = kSyncBytes;
+      p.r_spec = f;   f += align256((size_t)nh * gmax * kMaxSpecial * sizeof(Special));
+      p.r_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
+      p.r_sum = f;    f += align256((size_t)nh * sizeof(float));
+      p.r_status = f; f += align256((size_t)nh * sizeof(unsigned));
+      p.r_part = f;   f += align256((size_t)nkv * gmax * kGqa * kHd * sizeof(float));
+      p.r_total = f;
+      total = std::max(total, f);
+    }
+  }
   p.total = total;
   return p;
+}
+
+// BKV_KEEP_INTERMEDIATES=1: the resident path also writes every e_j into the workspace (where
+// bkv_debug_layout says) for parity diagnostics; the other paths always do
+static bool keep_intermediates() {
+  const char *e = std::getenv("BKV_KEEP_INTERMEDIATES");
+  return e && std::strcmp(e, "1") == 0;
+}
+
+// which implementation a decode of this plan takes
+static int choose_path(const DecodePlan &p) {
+  const int f = forced_path();
+  if (f == kPathSplit) return kPathSplit;
+  if (f == kPathFused) return p.gg > 0 ? kPathFused : kPathSplit;
+  if (p.rG > 0) return kPathResident;
+  return p.gg > 0 ? kPathFused : kPathSplit;
 }
 
 static bool aligned16(const void *p) { return p && ((uintptr_t)p & 15u) == 0; }
@@ -174,7 +218,28 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   char *w = (char *)ws;
   const LayerView L = view(d, layer);
 
-  if (p.gg > 0 && !force_split()) {
+  const int path = choose_path(p);
+  if (path == kPathResident) {
+    ResArgs ra{};
+    ra.L = L; ra.nkv = d->nkv; ra.nh = d->nh; ra.nfill = nfill; ra.scale = d->scale;
+    ra.G = p.rG; ra.kpw = p.rkpw; ra.ld = p.ld; ra.q = q;
+    if (fused) ra.ap = *fused;
+    ra.gate = gate; ra.out = out; ra.out_gated = out_gated;
+    ra.tstats = (unsigned long long *)(w + kResTagOffset);
+    ra.trec = ra.tstats + (size_t)d->nh * kResMaxGroupWgs;
+    ra.spec = (Special *)(w + p.r_spec);
+    ra.e = (float *)(w + p.r_e);
+    ra.keep_e = keep_intermediates() ? 1 : 0;
+    ra.sum = (float *)(w + p.r_sum);
+    ra.status = (unsigned *)(w + p.r_status);
+    ra.part = (float *)(w + p.r_part);
+    ra.sync = (unsigned *)(w + kResSyncOffset);
+#ifdef BKV_EXPERIMENT_TS
+    ra.ts = (unsigned *)w + 32768;
+#endif
+    return hip_fail(launch_resident(ra, d->k_fmt, d->v_fmt, p.rvres, st));
+  }
+  if (path == kPathFused) {
     FusedArgs fa{};
     fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub; fa.kpw = p.kpw;
     fa.ld = p.ld; fa.q = q;
@@ -329,12 +394,12 @@ int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
   if (rc) return rc;
   if (!out || nfill == 0) return BKV_EINVAL;
   const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
-  const bool fz = p.gg > 0 && !force_split();
+  const int path = choose_path(p);
   out[0] = (uint64_t)p.ld;
-  out[1] = fz ? 0 : p.off_score;
-  out[2] = fz ? p.f_e : p.off_e;
-  out[3] = fz ? p.f_sum : p.off_sum;
-  out[4] = fz ? p.f_status : p.off_status;
+  out[1] = path == kPathSplit ? p.off_score : 0;
+  out[2] = path == kPathResident ? p.r_e : path == kPathFused ? p.f_e : p.off_e;
+  out[3] = path == kPathResident ? p.r_sum : path == kPathFused ? p.f_sum : p.off_sum;
+  out[4] = path == kPathResident ? p.r_status : path == kPathFused ? p.f_status : p.off_status;
   out[5] = p.total;
   return BKV_OK;
 }
@@ -350,8 +415,7 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
 
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill) {
   if (check(d) || nfill == 0) return -1;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
-  return (p.gg > 0 && !force_split()) ? 1 : 0;
+  return choose_path(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill));
 }
 
 const char *bkv_last_hip_error(void) { return g_hip_err; }

@@ -99,6 +99,18 @@ __device__ __forceinline__ int64_t slot_of(const LayerView &L, int64_t pos) {
   return (int64_t)L.bt[pg] * L.page + (pos - pg * L.page);
 }
 
+// slot_of with the layout fixed at compile time (no branch between a row's index math and its
+// loads); paged positions use 32-bit arithmetic (positions < 2^31)
+template <bool PG>
+__device__ __forceinline__ int64_t slot_t(const LayerView &L, int64_t pos) {
+  if constexpr (!PG) {
+    return pos;
+  } else {
+    const uint32_t p = (uint32_t)pos, pg = p / (uint32_t)L.page;
+    return (int64_t)L.bt[pg] * L.page + (int64_t)(p - pg * (uint32_t)L.page);
+  }
+}
+
 // bytes of one head row of the data array, per format
 __host__ __device__ constexpr int row_bytes(int fmt) { return fmt == BKV_F16 ? kHd * 2 : kHd; }
 // bytes of one head row of the scale array (q8_0 only)
@@ -118,8 +130,36 @@ __device__ __forceinline__ float round_f16_uniform(float x) {
   return f16_to_f32(f32_to_f16_rne(x));
 }
 
-// exp of a float argument, correctly rounded to float (through the f64 exp)
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+// exp of a float argument, correctly rounded to float: the value of (float)exp((double)x).
+// Fast path: x = k ln2 + r (|r| <= ln2/2, ln2 split so that k*ln2_hi is exact), exp(r) by its
+// Taylor polynomial to degree 11 in fp64 (truncation < 2^-50, rounding ~2^-52), scaled by 2^k and
+// rounded once to float. When the fp64 value lies within 64 units of its last place of a float
+// rounding boundary, or x is outside the float-normal range of the result, the library fp64 exp
+// decides. Checked exhaustively on the host against (float)exp((double)x) for every float in
+// [-104, 89]: no mismatch; 0.1% of those floats (nearly all outside (-87, 88)) take the library path.
+__device__ __forceinline__ float exp_cr(float xf) {
+  const double x = xf;
+  if (!(x > -87.0 && x < 88.0)) return (float)exp(x);
+  const double kd = rint(x * 0x1.71547652b82fep0);
+  double r = fma(-kd, 0x1.62e42fee00000p-1, x);
+  r = fma(-kd, 0x1.a39ef35793c76p-33, r);
+  double p = 0x1.ae64567f544e4p-26;        // 1/11!
+  p = fma(p, r, 0x1.27e4fb7789f5cp-22);    // 1/10!
+  p = fma(p, r, 0x1.71de3a556c734p-19);
+  p = fma(p, r, 0x1.a01a01a01a01ap-16);
+  p = fma(p, r, 0x1.a01a01a01a01ap-13);
+  p = fma(p, r, 0x1.6c16c16c16c17p-10);
+  p = fma(p, r, 0x1.1111111111111p-7);
+  p = fma(p, r, 0x1.5555555555555p-5);
+  p = fma(p, r, 0x1.5555555555555p-3);
+  p = fma(p, r, 0x1.0000000000000p-1);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  const double y = ldexp(p, (int)kd);
+  const long long low = (long long)(__double_as_longlong(y) & 0x1FFFFFFFll) - 0x10000000ll;
+  if (low >= -64 && low <= 64) return (float)exp(x);
+  return (float)y;
+}
 
 // ------------------------------------------------------------------ workgroup scans (NT threads)
 template <typename T>

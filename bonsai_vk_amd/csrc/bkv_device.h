@@ -244,6 +244,15 @@ __device__ __forceinline__ Special ld_spec(const Special *p) {
   return x;
 }
 
+__device__ __forceinline__ void st_f2(float2 *p, float2 v) {
+  st_agent(reinterpret_cast<unsigned long long *>(p),
+           (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)__float_as_uint(v.y) << 32));
+}
+__device__ __forceinline__ float2 ld_f2(const float2 *p) {
+  const unsigned long long u = ld_agent(reinterpret_cast<const unsigned long long *>(p));
+  return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+
 // ------------------------------------------------------------------ row staging into LDS
 // Rows [0, n) of one KV head's array (COLS x 16 B per row, row_bytes_ apart per head slot) at
 // positions j0.. into tile[row * STRIDE + col]; rows [n, ROWS) are zero-filled. Every load of a batch
@@ -306,6 +315,214 @@ __device__ __forceinline__ void v_accum(const uint4 w, float vsc, const float (&
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) acc[h][i] = fmaf(p[h], x, acc[h][i]);
     }
+  }
+}
+
+
+// ---------------------------------------------------------------- the walk (one wave, 1..NHW heads)
+// Records rec[c] / specials spec[c][..] of the group's workgroups in key order, each covering kpw
+// keys. The fields of every special (global key index, global increment prefix, binade of the step
+// before it, the whole ulps of the segment before it) are resolved in parallel across the wave into
+// LDS. The serial chain then carries only the running sum: per special, the bits of the sum advance
+// by the segment's ulps (an integer add, valid while the sum stays in the recorded binade) and the
+// special's e is added in fp32. The binade conditions are checked afterwards, in parallel, on the
+// sums recorded before each step. A wave walks its heads' chains interleaved.
+// WG: workgroups per group the scratch holds; CAP: specials per head (more: serial fallback)
+template <int WG, int CAP>
+struct WalkScratchT {
+  static constexpr int kWg = WG, kCap = CAP;
+  long long wg_ib[WG];
+  int wg_off[WG + 1], wg_bp[WG];
+  long long si[CAP];
+  int sk[CAP];
+  float se[CAP];
+  int sck[CAP];                    // binade exponent field the step must start and end in, -1: no advance
+  int sdu[CAP];                    // ulps the sum advances by before the special (0: none)
+};
+using WalkScratch = WalkScratchT<kFusedMaxGroupWgs, 384>;
+
+#ifdef BKV_EXPERIMENT_TS
+#define WTS(q, i) do { if (tsp[q] && (threadIdx.x & 63) == 0) tsp[q][i] = (unsigned)wall_clock64(); } while (0)
+#else
+#define WTS(q, i) do { } while (0)
+#endif
+
+template <int NHW, typename WS>
+__device__ void walk_heads(const ChunkRec *const *rec, const Special *const *spec, int nhere, int gg,
+                           int64_t kpw, int64_t nfill, WS *const *ws, float *s_out, bool *good_out,
+                           unsigned *const *tsp) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kWalkWg = WS::kWg, kWalkCap = WS::kCap;
+  constexpr int kRounds = (kWalkWg + 63) / 64;
+  int T[NHW], blast_last[NHW];
+  long long itot[NHW];
+  bool ok[NHW];
+  // 1. every record of every head in one round trip, then the prefix scans
+  ChunkRec r[NHW][kRounds];
+#pragma unroll
+  for (int q = 0; q < NHW; ++q)
+#pragma unroll
+    for (int rr = 0; rr < kRounds; ++rr) {
+      const int c = rr * 64 + lane;
+      r[q][rr].tot = 0; r[q][rr].nsp = 0; r[q][rr].blast = kNoBinade;
+      if (q < nhere && c < gg) r[q][rr] = ld_rec(&rec[q][c]);
+    }
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    ok[q] = q < nhere && gg <= kWalkWg;
+    long long ibase = 0;
+    int obase = 0, blast_prev = kNoBinade;
+    bool over = false;
+    WS &w = *ws[q];
+#pragma unroll
+    for (int rr = 0; rr < kRounds; ++rr) {
+      if (rr * 64 < gg) {
+        const int c = rr * 64 + lane;
+        const ChunkRec x = r[q][rr];
+        over |= x.nsp > kMaxSpecial;
+        const int cnt = min(x.nsp, kMaxSpecial);
+        const long long incl = wave_incl_scan<long long>(x.tot, lane);
+        const int oincl = wave_incl_scan<int>(cnt, lane);
+        int bp = __shfl_up(x.blast, 1);
+        if (lane == 0) bp = blast_prev;
+        if (q < nhere && c < gg) {
+          w.wg_ib[c] = ibase + incl - x.tot;
+          w.wg_off[c] = obase + oincl - cnt;
+          w.wg_bp[c] = bp;
+        }
+        const int nb = min(64, gg - rr * 64);
+        ibase += __shfl(incl, 63);
+        obase += __shfl(oincl, 63);
+        blast_prev = __shfl(x.blast, nb - 1);
+      }
+    }
+    if (q < nhere && lane == 0) w.wg_off[gg] = obase;
+    ok[q] = ok[q] && !__any(over) && obase <= kWalkCap;
+    T[q] = ok[q] ? obase : 0;
+    itot[q] = ibase;
+    blast_last[q] = blast_prev;
+    WTS(q, 0);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 2. the specials, resolved to global key index, increment prefix and starting binade (the loads
+  // of all heads are issued before any is used)
+  {
+    int Tm = 0;
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) Tm = max(Tm, T[q]);
+    for (int o = lane; o < Tm; o += 64) {
+      int lo[NHW];
+      Special x[NHW];
+#pragma unroll
+      for (int q = 0; q < NHW; ++q) {
+        const WS &w = *ws[q];
+        int l = 0, hi = gg - 1;
+        if (o < T[q]) {
+          while (l < hi) {
+            const int mid = (l + hi + 1) >> 1;
+            if (w.wg_off[mid] <= o) l = mid; else hi = mid - 1;
+          }
+        }
+        lo[q] = l;
+      }
+#pragma unroll
+      for (int q = 0; q < NHW; ++q)
+        if (o < T[q]) x[q] = ld_spec(&spec[q][(size_t)lo[q] * kMaxSpecial + (o - ws[q]->wg_off[lo[q]])]);
+#pragma unroll
+      for (int q = 0; q < NHW; ++q) {
+        if (o < T[q]) {
+          WS &w = *ws[q];
+          const int bf = (x[q].meta >> 16) & 0xFF;
+          w.si[o] = w.wg_ib[lo[q]] + x[q].ipre;
+          w.sk[o] = (int)(lo[q] * kpw + (x[q].meta & 0xFFFF));
+          w.se[o] = x[q].e;
+          w.sck[o] = bf == 255 ? w.wg_bp[lo[q]] : (bf == 0 ? kNoBinade : bf - 128);   // binade B for now
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 3. per special: the ulps of the segment before it in its binade
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    WS &w = *ws[q];
+    WTS(q, 1);
+    bool bad = false;
+    for (int o = lane; o < T[q]; o += 64) {
+      const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+      const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+      int du = 0, ck = -1;
+      if (gap > 1) {
+        const int B = w.sck[o];
+        if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24)) {
+          bad = true;
+        } else {
+          du = (int)(di >> (B + 17));
+          ck = B + 127;
+        }
+      } else if (di != 0) {
+        bad = true;
+      }
+      w.sdu[o] = du;
+      w.sck[o] = ck;
+    }
+    ok[q] = ok[q] && !__any(bad);
+    if (!ok[q]) T[q] = 0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 4. the chains, 16 steps per unrolled block; entries past T are du 0, e 0 (no change)
+  float s[NHW];
+  bool bad[NHW];
+  int Tm = 0;
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) { s[q] = 0.0f; bad[q] = false; Tm = max(Tm, T[q]); WTS(q, 2); }
+  for (int base = 0; base < Tm; base += 64) {
+    const int o = base + lane;
+    int du_l[NHW], ck_l[NHW];
+    float e_l[NHW];
+    uint32_t pre[NHW];
+#pragma unroll
+    for (int q = 0; q < NHW; ++q) {
+      const bool in = o < T[q];
+      du_l[q] = in ? ws[q]->sdu[o] : 0;
+      ck_l[q] = in ? ws[q]->sck[o] : -1;
+      e_l[q] = in ? ws[q]->se[o] : 0.0f;
+      pre[q] = 0u;
+    }
+    const int cnt = min(64, Tm - base);
+    for (int j0 = 0; j0 < cnt; j0 += 16) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = j0 + jj;
+#pragma unroll
+        for (int q = 0; q < NHW; ++q) {
+          const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l[q], j);
+          const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l[q]), j));
+          const uint32_t bits = __float_as_uint(s[q]);
+          pre[q] = lane == j ? bits : pre[q];
+          s[q] = __fadd_rn(__uint_as_float(bits + du), ev);
+        }
+      }
+    }
+    // the binade conditions of this block's steps: start in binade ck, no carry out of it
+#pragma unroll
+    for (int q = 0; q < NHW; ++q)
+      if (ck_l[q] >= 0)
+        bad[q] |= (int)(pre[q] >> 23) != ck_l[q] || (int)((pre[q] + (uint32_t)du_l[q]) >> 23) != ck_l[q];
+  }
+#pragma unroll
+  for (int q = 0; q < NHW; ++q) {
+    WTS(q, 3);
+    bool good = ok[q] && !__any(bad[q]);
+    // the trailing segment after the last special
+    const long long k_last = T[q] > 0 ? ws[q]->sk[T[q] - 1] : -1, i_last = T[q] > 0 ? ws[q]->si[T[q] - 1] : 0;
+    float sq = s[q];
+    if (good && nfill - 1 - k_last > 0) good = advance(sq, blast_last[q], itot[q] - i_last);
+    s_out[q] = sq;
+    good_out[q] = good;
+#ifdef BKV_EXPERIMENT_TS
+    if (tsp[q] && lane == 0) tsp[q][4] = T[q];
+#endif
   }
 }
 

@@ -123,6 +123,41 @@ struct FusedArgs {
   unsigned *sync;                // kSyncBytes
 };
 
+// ------------------------------------------------------------------ the resident decode kernel
+// One 512-thread workgroup per CU, G workgroups per KV group, every workgroup resident; a
+// workgroup holds up to kResMaxPass*512 keys (scores and e in registers); with q8_0 V and at most
+// 512 + kResTail keys it keeps its V rows in LDS, streamed in behind the exact-sum walk.
+constexpr int kResNT = 512;
+constexpr int kResMaxPass = 4;
+constexpr int kResTail = 16;                   // keys past kResNT a q8_0-V workgroup may hold
+constexpr int kResMaxGroupWgs = 64;           // workgroups per KV group at most (walk scratch)
+constexpr int kResGroupLines = 9;              // generation + 2 parities x 4 phase counters
+constexpr size_t kResSyncOffset = 200 * 1024;  // inside the sync area, clear of the other paths
+constexpr size_t kResTagOffset = 144 * 1024;   // tagged statistics, then tagged records (48 KiB)
+
+struct ResArgs {
+  LayerView L;
+  int nkv, nh;
+  uint32_t nfill;
+  float scale;
+  int G, kpw;                    // workgroups per KV group, keys per workgroup
+  int64_t ld;
+  const float *q;                // [nh][hd]
+  AppendArgs ap;                 // decode_step: the token to append first (ap.k null: none)
+  const float *gate;
+  float *out, *out_gated;
+  unsigned long long *tstats;    // [nh][kResMaxGroupWgs] tagged (max, sum exp) per workgroup
+  unsigned long long *trec;      // [nh][kResMaxGroupWgs][2] tagged chunk records
+  Special *spec;                 // [nh][G][kMaxSpecial]
+  float *e;                      // [nh][ld]: written when keep_e (diagnostics) or on the fallback
+  int keep_e;
+  float *sum;                    // [nh]
+  unsigned *status;              // [nh]
+  float *part;                   // [nkv][G][kGqa][hd]
+  unsigned *sync;                // the resident kernel's sync lines
+  unsigned *ts;                  // phase timestamps (experiment builds), or null
+};
+
 #define BKV_FMT_SWITCH(KF, VF, ...)                                                    \
   do {                                                                                \
     if ((KF) == BKV_Q8_0 && (VF) == BKV_Q8_0) { constexpr int KF_ = 1, VF_ = 1; __VA_ARGS__; } \
@@ -140,6 +175,10 @@ struct DecodePlan {
   // fused path (gg == 0: not available for this nfill)
   int gg, rsub, kpw;
   size_t f_stats, f_sub, f_rec, f_spec, f_e, f_sum, f_status, f_part, f_total;
+  // resident path (rG == 0: not available for this nfill)
+  int rG, rkpw;
+  bool rvres;
+  size_t r_spec, r_e, r_sum, r_status, r_part, r_total;
 };
 
 DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill);
@@ -148,6 +187,8 @@ int qk_keys_per_wg(int kfmt);
 int fused_max_workgroups(int kf, int vf);
 int fused_keys_per_pass(int kf);
 hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st);
+int resident_max_workgroups(int kf, int vf);
+hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st);
 hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st);
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);
 hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, const RedArgs &ra,

@@ -1,0 +1,1124 @@
+// bkv_resident.hip - the default decode kernel: one launch per layer and token, one 512-thread
+// workgroup per CU, every workgroup resident for the whole call.
+//
+// Workgroup w serves KV group g = w % nkv and the kpw consecutive keys starting at (w / nkv) * kpw,
+// one key per thread and pass (at most kResMaxPass passes). Per call:
+//  1. The workgroup whose range holds pos appends the new token (decode_step). Each wave stages
+//     its 64 K rows through a private LDS tile with coalesced loads; q16 of the group's 4 query heads
+//     sits in registers, and each lane computes its key's 4 scores in the reference's order. For
+//     q8_0 V with kpw <= 32 * kResVSlots, the V rows are loaded into registers right behind the K
+//     rows, so the V stream overlaps the QK arithmetic and the barriers.
+//  2. Barrier A (the group's workgroups): per-workgroup (max, sum exp) give the global max and
+//     each workgroup's fp64 position on the running sum.
+//  3. e_j = exp(s_j*scale - max) correctly rounded, each step of the serial fp32 sum classified as
+//     an exact integer increment or a special; per-workgroup record and specials.
+//  4. Barrier B: every workgroup walks the group's records itself to the exact serial sums (no
+//     second hand-off for the result).
+//  5. p16 = f16(e/sum) into LDS, PV over the workgroup's rows (from registers, or streamed), one
+//     [4][256] partial per workgroup.
+//  6. Barrier C: workgroup i sums slice i of the group's partials in workgroup order and applies the
+//     gate.
+// Barriers count arrivals on per-group counters (two sets, alternating by call parity; each call
+// clears the set the next one uses). Every wait is bounded and records an error word on timeout.
+#include <cstdlib>
+#include <cstring>
+
+#include "bkv_common.h"
+#include "bkv_device.h"
+#include "bkv_internal.h"
+
+namespace bkv {
+
+constexpr unsigned kResSpin = 1u << 21;   // polls per wait (seconds) before the error word is set
+constexpr int kUPR = 17;            // LDS uint4 per staged K row: 16 data + the q8_0 scale uint4
+constexpr int kResNW = kResNT / 64;
+constexpr int kResXBytes = 23040;    // LDS beside the K tiles (160 KiB in all)
+constexpr int8_t kNoBin8 = -128;     // kNoBinade in the int8 binade map
+
+#ifdef BKV_EXPERIMENT_TS
+#define RTS(i) do { if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+#define RTSW(i, wv) do { if (threadIdx.x == 64 * (wv) && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+#else
+#define RTSW(i, wv) do { } while (0)
+#define RTS(i) do { } while (0)
+#endif
+
+// every LDS access of this wave issued so far has completed, and the compiler keeps memory
+// operations on their side of this point
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Arrive at a group barrier and wait until n workgroups have arrived. Waves below storing_waves
+// first wait for their own stores (write-through stores complete at the device coherence point;
+// the other waves have none this call needs, and their loads stay in flight), then one atomic per
+// workgroup. The wait is bounded: a timeout sets the error word and lets the kernel finish.
+__device__ __forceinline__ void group_barrier(unsigned *cnt, unsigned n, unsigned *err,
+                                              int storing_waves = kResNT / 64) {
+  if ((int)(threadIdx.x >> 6) < storing_waves) __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicAdd(cnt, 1u);
+    unsigned spins = 0;
+    while (ld_agent(cnt) < n) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kResSpin) {
+        atomicOr(err, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Chunk ch of the K rows of this wave's keys j0 .. j0+63 (rows >= n repeat row n-1) into
+// kt[row * kUPR + col]: 16 uint4 per row (q8_0: the whole 256 B row; fp16: half a row), and for
+// q8_0 the row's 16 B of block scales at column 16. Load i reads rows 4i..4i+3, 16 lanes per row.
+// LDS address (32-bit, LDS aperture) of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+template <int KF, bool PG>
+__device__ __forceinline__ void stage_k_wave(uint4 *kt, const LayerView &L, int nkv, int g, int64_t j0,
+                                             int n, int ch) {
+  // direct-to-LDS: load i writes the 64 consecutive tile slots 64 i .. 64 i + 63 (row = slot / kUPR,
+  // column = slot % kUPR); column 16 is the q8_0 scale row (for fp16 K an unused copy of column 0).
+  // Issued as inline asm, so the compiler neither waits for these loads nor counts them: the caller
+  // waits with wait_vm<N>() before reading the tile, N = vector memory operations issued since.
+  const int lane = threadIdx.x & 63;
+  constexpr int RB = row_bytes(KF);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(kt));
+#pragma unroll
+  for (int i = 0; i < kUPR; ++i) {
+    const int slotx = 64 * i + lane, row = slotx / kUPR, col = slotx - row * kUPR;
+    const int64_t sl = slot_t<PG>(L, j0 + min(row, n - 1));
+    const uint8_t *src = (KF == BKV_Q8_0 && col == 16)
+                             ? L.ks + (sl * nkv + g) * kScaleRowBytes
+                             : L.kd + (sl * nkv + g) * RB + (ch * 16 + (col & 15)) * 16;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(base + 1024u * i) : "memory", "m0");
+  }
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Resident q8_0 V. The rows 32s + 4*vw + kk (s < kResVTiles, kk < 4) that wave vw consumes in PV
+// live in vw's K tile once the scores are done: slot s holds 64 x 16 B (lane l: bytes 16*(l%16)..
+// of row 32s + 4*vw + l/16) at tile + 1024 s, and the rows' 16 B block-scale rows follow at
+// tile + 16 KiB + 16 (4s + kk). Waves kResNW/2.. issue these direct-to-LDS loads for their own tile
+// and for the tile of wave w - kResNW/2, so that the other half's memory queues stay free for the
+// barriers and the walk (loads return in issue order). Rows >= nk repeat row nk-1; their
+// probabilities are zero.
+constexpr int kResVTiles = 16;
+template <bool PG>
+__device__ __forceinline__ void load_v_tile(uint4 *tile, int vw, const LayerView &L, int nkv, int g,
+                                            int64_t kb, int nk) {
+  const int lane = threadIdx.x & 63, vsub = lane & 15, vkk = lane >> 4;
+  {
+    const int s = lane >> 2, kk = lane & 3;
+    const int k = min(s * 32 + vw * 4 + kk, nk - 1);
+    const int64_t slot = slot_t<PG>(L, kb + k);
+    __builtin_amdgcn_global_load_lds(
+        (const void __attribute__((address_space(1))) *)(L.vs + (slot * nkv + g) * kScaleRowBytes),
+        (void __attribute__((address_space(3))) *)(tile + kResVTiles * 64), 16, 0, 0);
+  }
+  // every slot is loaded (slots past nk repeat row nk-1), so slot s has landed once at most
+  // kResVTiles-1-s of this wave's loads are outstanding
+#pragma unroll
+  for (int s = 0; s < kResVTiles; ++s) {
+    const int k = min(s * 32 + vw * 4 + vkk, nk - 1);
+    const int64_t slot = slot_t<PG>(L, kb + k);
+    __builtin_amdgcn_global_load_lds(
+        (const void __attribute__((address_space(1))) *)(L.vd + (slot * nkv + g) * kHd + vsub * 16),
+        (void __attribute__((address_space(3))) *)(tile + s * 64), 16, 0, 0);
+  }
+}
+
+// the register-resident variant: lane (wave, vkk, vsub) slot s holds bytes 16*vsub.. of row
+// 32 s + 4 wave + vkk and that row's block-pair scale word (rows >= nk repeat row nk-1)
+template <bool PG>
+__device__ __forceinline__ void load_v_regs(uint4 (&vd)[kResVTiles], uint32_t (&vs)[kResVTiles], const LayerView &L,
+                                            int nkv, int g, int64_t kb, int nk) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, vsub = lane & 15, vkk = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < kResVTiles; ++s) {
+    const int64_t slot = slot_t<PG>(L, kb + min(s * 32 + wave * 4 + vkk, nk - 1));
+    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+    vs[s] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+  }
+}
+constexpr int kVLoads = 2 * kResVTiles;      // vector loads load_v_regs issues per wave
+
+// PV over the resident slots, waiting for slot S only: out += p16 * V for the wave's rows
+// 32 s + 4 wave + vkk, 16 elements per lane (attn_vk.h:194-205; q8_0 V = f16(scale) * int8)
+template <int S>
+struct VSlots {
+  static __device__ __forceinline__ void run(const uint4 *kt, const uint32_t *tsc, int nk, int wave, int vkk,
+                                             int vsub, int lane, const uint2 *s_p16,
+                                             float (&acc)[kGqa][16]) {
+    VSlots<S - 1>::run(kt, tsc, nk, wave, vkk, vsub, lane, s_p16, acc);
+    constexpr int s = S - 1;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kResVTiles - 1 - s) : "memory");
+    if (s * 32 < nk) {
+      const int k = s * 32 + wave * 4 + vkk;
+      const uint2 pw = k < nk ? s_p16[k] : make_uint2(0u, 0u);
+      const float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
+                             f16_to_f32(pw.y >> 16)};
+      const uint32_t sw = tsc[(s * 4 + vkk) * 4 + (vsub >> 2)];
+      const float vsc = k < nk ? f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu)) : 0.0f;
+      v_accum<BKV_Q8_0>(kt[s * 64 + lane], vsc, p, acc);
+    }
+  }
+};
+template <>
+struct VSlots<0> {
+  static __device__ __forceinline__ void run(const uint4 *, const uint32_t *, int, int, int, int, int, const uint2 *,
+                                             float (&)[kGqa][16]) {}
+};
+
+// fp16 K, half row CH (dims 128*CH .. 128*CH+127): acc = acc + q16_d * k_d in ascending d, exact
+// products (attn_vk.h:156-170)
+template <int CH>
+__device__ __forceinline__ void qk_f16_half(const uint4 *row, const float (&qv)[kGqa][kHd / 16],
+                                            float (&acc)[kGqa]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) Dot16<16>::run(acc[h], qv[h][CH * 8 + j], x);
+  }
+}
+
+// ---------------------------------------------------------------- the walk (one wave, one head)
+// walk_heads (bkv_device.h) for a group of at most 64 workgroups whose records the wave already
+// holds (lane c: record of workgroup c, valid for c < gg).
+template <typename WS>
+__device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t kpw, int64_t nfill, WS &w,
+                         float &s_out, bool &good_out) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kWalkCap = WS::kCap;
+  static_assert(WS::kWg <= 64, "one record per lane");
+  bool ok = gg <= WS::kWg;
+  // 1. prefix scans over the records
+  const bool in = lane < gg;
+  const long long tot = in ? x.tot : 0;
+  const int cnt = in ? min(x.nsp, kMaxSpecial) : 0;
+  const bool over = in && x.nsp > kMaxSpecial;
+  const long long incl = wave_incl_scan<long long>(tot, lane);
+  const int oincl = wave_incl_scan<int>(cnt, lane);
+  int bp = __shfl_up(in ? x.blast : kNoBinade, 1);
+  if (lane == 0) bp = kNoBinade;
+  if (in) {
+    w.wg_ib[lane] = incl - tot;
+    w.wg_off[lane] = oincl - cnt;
+    w.wg_bp[lane] = bp;
+  }
+  const int T0 = __shfl(oincl, 63);
+  if (lane == 0) w.wg_off[gg] = T0;
+  const long long itot = __shfl(incl, 63);
+  const int blast_last = __shfl(in ? x.blast : kNoBinade, gg - 1);
+  ok = ok && !__any(over) && T0 <= kWalkCap;
+  const int T = ok ? T0 : 0;
+  __builtin_amdgcn_wave_barrier();
+  // 2. the specials, resolved to global key index, increment prefix and starting binade
+  for (int o = lane; o < T; o += 64) {
+    int l = 0, hi = gg - 1;
+    while (l < hi) {
+      const int mid = (l + hi + 1) >> 1;
+      if (w.wg_off[mid] <= o) l = mid; else hi = mid - 1;
+    }
+    const Special sx = ld_spec(&spec[(size_t)l * kMaxSpecial + (o - w.wg_off[l])]);
+    const int bf = (sx.meta >> 16) & 0xFF;
+    w.si[o] = w.wg_ib[l] + sx.ipre;
+    w.sk[o] = (int)(l * kpw + (sx.meta & 0xFFFF));
+    w.se[o] = sx.e;
+    w.sck[o] = bf == 255 ? w.wg_bp[l] : (bf == 0 ? kNoBinade : bf - 128);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 3. per special: the ulps of the segment before it in its binade
+  bool bad = false;
+  for (int o = lane; o < T; o += 64) {
+    const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+    const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+    int du = 0, ck = -1;
+    if (gap > 1) {
+      const int B = w.sck[o];
+      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24)) {
+        bad = true;
+      } else {
+        du = (int)(di >> (B + 17));
+        ck = B + 127;
+      }
+    } else if (di != 0) {
+      bad = true;
+    }
+    w.sdu[o] = du;
+    w.sck[o] = ck;
+  }
+  ok = ok && !__any(bad);
+  const int Tc = ok ? T : 0;
+  __builtin_amdgcn_wave_barrier();
+  // 4. the chain, 16 steps per unrolled block; entries past Tc are du 0, e 0 (no change)
+  float s = 0.0f;
+  bool bad2 = false;
+  for (int base = 0; base < Tc; base += 64) {
+    const int o = base + lane;
+    const bool inn = o < Tc;
+    const int du_l = inn ? w.sdu[o] : 0, ck_l = inn ? w.sck[o] : -1;
+    const float e_l = inn ? w.se[o] : 0.0f;
+    uint32_t pre = 0u;
+    const int n = min(64, Tc - base);
+    for (int j0 = 0; j0 < n; j0 += 16) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = j0 + jj;
+        const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l, j);
+        const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), j));
+        const uint32_t bits = __float_as_uint(s);
+        pre = lane == j ? bits : pre;
+        s = __fadd_rn(__uint_as_float(bits + du), ev);
+      }
+    }
+    if (ck_l >= 0) bad2 |= (int)(pre >> 23) != ck_l || (int)((pre + (uint32_t)du_l) >> 23) != ck_l;
+  }
+  bool good = ok && !__any(bad2);
+  const long long k_last = Tc > 0 ? w.sk[Tc - 1] : -1, i_last = Tc > 0 ? w.si[Tc - 1] : 0;
+  if (good && nfill - 1 - k_last > 0) good = advance(s, blast_last, itot - i_last);
+  s_out = s;
+  good_out = good;
+}
+
+// ---------------------------------------------------------------- tagged hand-off words
+// A per-workgroup value and its arrival in one 64-bit store: the two low bits carry the call's tag
+// (1 or 2 by call parity; 0 = cleared). Every call clears the entries of workgroups it does not
+// run, so an entry read during a call holds that call's tag, the previous call's tag, or 0.
+__device__ __forceinline__ unsigned long long pack_stats(float m, float l, unsigned tag) {
+  return ((unsigned long long)__float_as_uint(m) << 32) | ((__float_as_uint(l) & ~3u) | tag);
+}
+// record: tot (< 2^51) in w0 bits 2.., nsp in w1 bits 2..17, blast+128 (0: none) in bits 18..25
+__device__ __forceinline__ void pack_rec(const ChunkRec &r, unsigned tag, unsigned long long &w0,
+                                         unsigned long long &w1) {
+  w0 = ((unsigned long long)r.tot << 2) | tag;
+  const unsigned b = r.blast == kNoBinade ? 0u : (unsigned)(r.blast + 128);
+  w1 = ((unsigned long long)(unsigned)r.nsp << 2) | ((unsigned long long)b << 18) | tag;
+}
+__device__ __forceinline__ ChunkRec unpack_rec(unsigned long long w0, unsigned long long w1) {
+  ChunkRec r;
+  r.tot = (long long)(w0 >> 2);
+  r.nsp = (int)((w1 >> 2) & 0xFFFFu);
+  const unsigned b = (unsigned)((w1 >> 18) & 0xFFu);
+  r.blast = b == 0 ? kNoBinade : (int)b - 128;
+  return r;
+}
+// wait until lanes < n of the wave see `tag` in the low bits of their word(s); bounded
+__device__ __forceinline__ void poll_tagged(const unsigned long long *p, int stride, int words, int n,
+                                            unsigned tag, unsigned long long (&v)[2], unsigned *err) {
+  const int lane = threadIdx.x & 63;
+  unsigned spins = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i < words) {
+        v[i] = lane < n ? ld_agent(p + (size_t)lane * stride + i) : (unsigned long long)tag;
+        ok = ok && (unsigned)(v[i] & 3u) == tag;
+      }
+    }
+    if (__all(ok)) return;
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > kResSpin) {
+      if (lane == 0) atomicOr(err, 1u);
+      return;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- DPP scans
+// A DPP move in which lanes whose source lies outside the pattern (or in a masked row) read 0.
+template <int CTRL, int RM>
+__device__ __forceinline__ int dpp0(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, RM, 0xF, false);
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ float dpp0(float v) {
+  return __builtin_bit_cast(float, dpp0<CTRL, RM>(__builtin_bit_cast(int, v)));
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp0(double v) {
+  const long long u = __builtin_bit_cast(long long, v);
+  const int lo = dpp0<CTRL, RM>((int)u), hi = dpp0<CTRL, RM>((int)(u >> 32));
+  return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+// inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 inside each row of 16 lanes, then
+// row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3)
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan_dpp(T v) {
+  v += dpp0<0x111, 0xF>(v);
+  v += dpp0<0x112, 0xF>(v);
+  v += dpp0<0x114, 0xF>(v);
+  v += dpp0<0x118, 0xF>(v);
+  v += dpp0<0x142, 0xA>(v);
+  v += dpp0<0x143, 0xC>(v);
+  return v;
+}
+// K exclusive prefix sums over the workgroup at once, totals in tot; sh: kResNW * K slots.
+// Exact for integer-valued doubles below 2^53; for floats the order of the additions is free.
+template <int K, typename T>
+__device__ __forceinline__ void block_excl_scan_dpp(const T (&v)[K], T (&ex)[K], T (&tot)[K], T *sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  T inc[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) inc[k] = wave_incl_scan_dpp(v[k]);
+  if (lane == 63)
+#pragma unroll
+    for (int k = 0; k < K; ++k) sh[wave * K + k] = inc[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    T base = 0, t = 0;
+#pragma unroll
+    for (int i = 0; i < kResNW; ++i) {
+      const T x = sh[i * K + k];
+      if (i < wave) base += x;
+      t += x;
+    }
+    ex[k] = base + inc[k] - v[k];
+    tot[k] = t;
+  }
+  __syncthreads();
+}
+
+// one query head's score of one key (the tail): as qk_row_dot, with qt[j] = q16[h][16j + lane%16]
+// for the head h of the lane's DPP row
+__device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
+  const uint4 scl = row[16];
+#pragma unroll
+  for (int b = 0; b < kHd / 32; ++b) {
+    const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
+    float x0[16], x1[16];
+    const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x0[i] = sbyte(u0[i >> 2], i & 3);
+      x1[i] = sbyte(u1[i >> 2], i & 3);
+    }
+    const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
+    const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+    float inner = 0.0f;
+    Dot16<16>::run(inner, qt[2 * b], x0);
+    Dot16<16>::run(inner, qt[2 * b + 1], x1);
+    acc = __fadd_rn(acc, __fmul_rn(sc, inner));
+  }
+}
+template <int CH>
+__device__ __forceinline__ void qk_f16_half1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+    Dot16<16>::run(acc, qt[CH * 8 + j], x);
+  }
+}
+// inclusive prefix sum inside each DPP row of 16 lanes
+template <typename T>
+__device__ __forceinline__ T row_incl_scan_dpp(T v) {
+  v += dpp0<0x111, 0xF>(v);
+  v += dpp0<0x112, 0xF>(v);
+  v += dpp0<0x114, 0xF>(v);
+  v += dpp0<0x118, 0xF>(v);
+  return v;
+}
+
+// classify (bkv_device.h) without branches, the increment as an exact double
+__device__ __forceinline__ void classify_d(double abefore, double aafter, float e, bool &special, int &bin,
+                                           double &inc) {
+  const int B = ilogb(aafter);
+  const double lo = ldexp(1.0, B);
+  const double t = ldexp((double)e, 23 - B);
+  const bool ok = aafter >= 0x1p-17 && aafter < 0x1p22 && !(aafter > 2.0 * lo * (1.0 - kMargin)) &&
+                  !(abefore < lo * (1.0 + kMargin)) && (t - floor(t) != 0.5);
+  special = !ok;
+  bin = ok ? B : kNoBinade;
+  inc = ok ? ldexp(rint(t), B + 17) : 0.0;
+}
+
+// the workgroup-wide max / sum of four values at once (every thread receives them)
+__device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_max(v[h]);
+  if (lane == 0)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float r = sh[h];
+#pragma unroll
+    for (int i = 1; i < kResNW; ++i) r = fmaxf(r, sh[i * kGqa + h]);
+    v[h] = r;
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ void block_sum4(float (&v)[kGqa], float *sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_sum(v[h]);
+  if (lane == 0)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float r = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kResNW; ++i) r += sh[i * kGqa + h];
+    v[h] = r;
+  }
+  __syncthreads();
+}
+
+template <typename T>
+__device__ __forceinline__ T pick4(const T (&v)[kGqa], int i) {
+  return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
+template <int KF, int VF, bool VRES, bool PG>
+__global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
+  constexpr int NT = kResNT, NW = kResNW;
+  // VRES: one pass of NT keys plus a tail of at most kResTail keys (wave 0, one lane per key and head)
+  constexpr int MP = VRES ? 1 : kResMaxPass;
+  constexpr bool TAIL = VRES;
+  constexpr int SB = MP * NT + (TAIL ? kResTail : 0);   // binade-map row per head
+  using VR = KRow<VF>;
+  static_assert(!VRES || VF == BKV_Q8_0, "registers hold q8_0 V rows only");
+  // T: per-wave K tiles (64 rows x kUPR uint4 each); after the scores, each wave's q8_0 V rows
+  // (68 rows x 256 B, the same bytes) and at the end the PV reduction and the merge.
+  // X: the binade map, then the walk scratch, then the fp16 probabilities.
+  using WS = WalkScratchT<kResMaxGroupWgs, 192>;
+  __shared__ uint4 lds[NW * 64 * kUPR];
+  __shared__ uint4 ldx[kResXBytes / 16];
+  static_assert(64 * kUPR * 16 == kResVTiles * 1024 + 64 * 16, "a wave's V rows and scales fill its K tile");
+  static_assert(kResTail <= 16 && NT == 32 * kResVTiles, "the tail rows are the streamed slot");
+  static_assert(kGqa * SB + kGqa * kMaxSpecial * sizeof(Special) <= sizeof(ldx), "binade map and staged specials must fit");
+  static_assert(kGqa * sizeof(WS) <= sizeof(ldx), "walk scratch must fit");
+  static_assert(SB * sizeof(uint2) <= sizeof(ldx), "p16 buffer must fit");
+  static_assert(NW * kGqa * kHd * sizeof(float) <= sizeof(lds), "PV reduction must fit");
+  __shared__ float shf4[NW * kGqa];
+  __shared__ float4 s_wf[NW];
+  __shared__ double s_wd[NW * kGqa];
+  __shared__ int s_wc[NW * kGqa];
+  __shared__ float s_M[kGqa], s_S[kGqa];
+  __shared__ double s_P0[kGqa];
+  __shared__ int s_ok[kGqa];
+  __shared__ long long s_tt[kGqa];
+  __shared__ int s_tc[kGqa];
+
+  const int w = blockIdx.x, nkv = a.nkv, g = w % nkv, wi = w / nkv, G = a.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t kb = (int64_t)wi * a.kpw;
+  const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
+  const int nk = (int)max((int64_t)0, ke - kb);
+  const LayerView &L = a.L;
+
+  // sync lines of group g: generation, then counters A, B, C, F of parity 0 and of parity 1
+  unsigned *gs = a.sync + (size_t)g * kResGroupLines * kCounterStride;
+  unsigned *err = a.sync + (size_t)nkv * kResGroupLines * kCounterStride;
+  const unsigned gen = ld_agent(gs) + 1u;
+  unsigned *cnt = gs + (1 + (gen & 1u) * 4) * kCounterStride;
+  if (wi == 0 && tid < 4) st_agent(gs + (1 + ((gen + 1u) & 1u) * 4 + tid) * kCounterStride, 0u);
+  const unsigned tag = 1u + (gen & 1u);
+  constexpr int GM = kResMaxGroupWgs;
+  unsigned long long *tstats = a.tstats + (size_t)g * kGqa * GM;        // [kGqa][GM]
+  unsigned long long *trec = a.trec + (size_t)g * kGqa * GM * 2;        // [kGqa][GM][2]
+  if (wi == 0)                                  // entries of workgroups this call does not run
+    for (int i = tid; i < kGqa * (GM - G); i += NT) {
+      const int h = i / (GM - G), c = G + i % (GM - G);
+      st_agent(tstats + h * GM + c, 0ull);
+      st_agent(trec + (h * GM + c) * 2, 0ull);
+      st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
+    }
+  RTS(0);
+
+  if (a.ap.k) {                                 // decode_step: append the new token first
+    if (wave == 0 && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke)
+      append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- QK
+  float qv[kGqa][kHd / 16];
+  load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
+  asm volatile("s_nop 4");
+
+  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
+  uint4 *kt = lds + wave * 64 * kUPR;
+  // VRES: this wave's V rows 32 s + 4 wave + vkk (s < kResVTiles) and their block-pair scale words,
+  // loaded right behind the first K tile so that they stream in during the scores
+  uint4 vd[VRES ? kResVTiles : 1];
+  uint32_t vsw[VRES ? kResVTiles : 1];
+  float sc[MP][kGqa];
+  float mloc[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) mloc[h] = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < MP; ++r) {
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) sc[r][h] = 0.0f;
+    const int64_t j0 = kb + (int64_t)r * NT + wave * 64;
+    const int n = (int)max((int64_t)0, min((int64_t)64, ke - j0));
+    if (n > 0) {
+      float acc[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) acc[h] = 0.0f;
+      stage_k_wave<KF, PG>(kt, L, nkv, g, j0, n, 0);
+      if (VRES && r == 0) {
+        if constexpr (VRES) load_v_regs<PG>(vd, vsw, L, nkv, g, kb, nk);
+        wait_vm<kVLoads>();                // the K tile has landed; the V rows stay in flight
+      } else {
+        wait_vm<0>();
+      }
+      if (KF == BKV_Q8_0) {
+        qk_row_dot<KF>(kt + lane * kUPR, qv, acc);
+      } else {
+        qk_f16_half<0>(kt + lane * kUPR, qv, acc);
+        wave_lds_sync();
+        stage_k_wave<KF, PG>(kt, L, nkv, g, j0, n, 1);
+        wait_vm<0>();
+        qk_f16_half<1>(kt + lane * kUPR, qv, acc);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        sc[r][h] = acc[h];
+        if (lane < n) mloc[h] = fmaxf(mloc[h], acc[h] * a.scale);
+      }
+    } else if (r == 0) {
+      if constexpr (VRES) load_v_regs<PG>(vd, vsw, L, nkv, g, kb, nk);
+    }
+  }
+  // the tail (keys NT .. nk-1, at most kResTail): wave 0, lane = 16 h + t scores key NT + t against
+  // head h, with its own head's q16 broadcast along the lane's DPP row
+  const int tn = TAIL ? max(0, nk - NT) : 0;
+  const int th = lane >> 4, tt = lane & 15;
+  float sct = 0.0f;
+  if (TAIL && tn > 0 && wave == 0) {
+    float qt[kHd / 16];
+    const float *qh = a.q + ((size_t)g * kGqa + th) * kHd + tt;
+#pragma unroll
+    for (int j = 0; j < kHd / 16; ++j) qt[j] = round_f16(qh[16 * j]);
+#pragma unroll
+    for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
+    stage_k_wave<KF, PG>(kt, L, nkv, g, kb + NT, tn, 0);
+    wait_vm<0>();
+    asm volatile("s_nop 4");
+    float acc1 = 0.0f;
+    if (KF == BKV_Q8_0) {
+      qk_row_dot1(kt + tt * kUPR, qt, acc1);
+    } else {
+      qk_f16_half1<0>(kt + tt * kUPR, qt, acc1);
+      wave_lds_sync();
+      stage_k_wave<KF, PG>(kt, L, nkv, g, kb + NT, tn, 1);
+      wait_vm<0>();
+      qk_f16_half1<1>(kt + tt * kUPR, qt, acc1);
+    }
+    wave_lds_sync();
+    sct = acc1;
+    if (tt < tn)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+        if (th == h) mloc[h] = fmaxf(mloc[h], sct * a.scale);
+  }
+  RTS(1);
+
+  // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
+  block_max4(mloc, shf4);                  // also: every wave is done with its K tile
+
+  float lsum[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < MP; ++r)
+      if (r * NT + tid < nk) l += __expf(sc[r][h] * a.scale - mloc[h]);
+    if (TAIL && wave == 0 && th == h && tt < tn) l += __expf(sct * a.scale - mloc[h]);
+    lsum[h] = l;
+  }
+  block_sum4(lsum, shf4);
+  if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
+
+  // ---------------------------------------------------------------- barrier A: global max
+  // wave h polls head h's statistics of every workgroup of the group: the global max and this
+  // workgroup's approximate position on the running sum come with them
+  if (wave < kGqa) {
+    unsigned long long v[2];
+    poll_tagged(tstats + wave * GM, 1, 1, G, tag, v, err);
+    const float mw = lane < G ? __uint_as_float((unsigned)(v[0] >> 32)) : -INFINITY;
+    const float lw = lane < G ? __uint_as_float((unsigned)v[0] & ~3u) : 0.0f;
+    const float m = wave_max(mw);
+    double p = lane < wi ? (double)lw * exp((double)mw - (double)m) : 0.0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) p += __shfl_xor(p, o);
+    if (lane == 0) {
+      s_M[wave] = m;
+      s_P0[wave] = p;
+    }
+  }
+  __syncthreads();
+  RTS(2);
+  RTS(9);
+  // ---------------------------------------------------------------- e, classification, records
+  int8_t *s_bin = reinterpret_cast<int8_t *>(ldx);   // [kGqa][SB] binade, kNoBin8: special
+  Special *s_spec = reinterpret_cast<Special *>(ldx + (kGqa * SB + 15) / 16);   // [kGqa][kMaxSpecial]
+  float ev[MP][kGqa];
+  long long itot[kGqa];
+  int nspc[kGqa];
+  double carry[kGqa];
+  float Mh[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) { itot[h] = 0; nspc[h] = 0; carry[h] = s_P0[h]; Mh[h] = s_M[h]; }
+  Special *spec_g = a.spec + (size_t)(g * kGqa) * G * kMaxSpecial;
+#pragma unroll
+  for (int r = 0; r < MP; ++r) {
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) ev[r][h] = 0.0f;
+    if (r * NT < nk) {
+      const int kl = r * NT + tid;
+      const bool valid = kl < nk;
+      const int64_t j = kb + kl;
+      // the key's position on the running sum: the fp64 start of this workgroup plus an fp32
+      // exclusive scan inside it (relative error ~1e-7, far inside the classification margin)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        ev[r][h] = valid ? exp_cr(sc[r][h] * a.scale - Mh[h]) : 0.0f;
+        if (valid && a.keep_e) a.e[(size_t)(g * kGqa + h) * a.ld + j] = ev[r][h];
+      }
+      float fin[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) fin[h] = wave_incl_scan_dpp(ev[r][h]);
+      if (lane == 63) s_wf[wave] = make_float4(fin[0], fin[1], fin[2], fin[3]);
+      __syncthreads();
+      float fb[kGqa] = {0.0f, 0.0f, 0.0f, 0.0f}, ft[kGqa] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const float4 x = s_wf[i];
+        const float xv[kGqa] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          fb[h] += i < wave ? xv[h] : 0.0f;
+          ft[h] += xv[h];
+        }
+      }
+      // per head: the step's exact increment (an integer below 2^40 in units of 2^-40: fp64 sums of
+      // a workgroup's increments stay exact) or a special
+      bool sp[kGqa];
+      double dinc[kGqa], din[kGqa];
+      unsigned long long msk[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        const double ab = carry[h] + (double)(fb[h] + fin[h] - ev[r][h]);
+        int bin;
+        classify_d(ab, ab + (double)ev[r][h], ev[r][h], sp[h], bin, dinc[h]);
+        sp[h] = sp[h] && valid;
+        if (!valid) dinc[h] = 0.0;
+        carry[h] += (double)ft[h];
+        s_bin[h * SB + kl] = (valid && !sp[h]) ? (int8_t)bin : kNoBin8;
+        msk[h] = __ballot(sp[h]);
+        din[h] = wave_incl_scan_dpp(dinc[h]);
+      }
+      if (lane == 63)
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          s_wd[wave * kGqa + h] = din[h];
+          s_wc[wave * kGqa + h] = __popcll(msk[h]);
+        }
+      __syncthreads();                     // also publishes s_bin
+      // (pass timestamp removed)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        double ib = 0.0, it = 0.0;
+        int cb = 0, ct = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          const double x = s_wd[i * kGqa + h];
+          const int c = s_wc[i * kGqa + h];
+          ib += i < wave ? x : 0.0;
+          it += x;
+          cb += i < wave ? c : 0;
+          ct += c;
+        }
+        if (sp[h]) {
+          const int id = nspc[h] + cb + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(msk[h] >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)msk[h], 0u));
+          if (id < kMaxSpecial) {
+            const int8_t bp8 = kl > 0 ? s_bin[h * SB + kl - 1] : (int8_t)0;
+            const int bprev = kl > 0 ? (bp8 == kNoBin8 ? kNoBinade : bp8) : 127;
+            Special x;
+            x.ipre = itot[h] + (long long)(ib + din[h] - dinc[h]);
+            x.e = ev[r][h];
+            x.meta = kl | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+            s_spec[h * kMaxSpecial + id] = x;
+          }
+        }
+        itot[h] += (long long)it;
+        nspc[h] += ct;
+      }
+    }
+  }
+  // the tail's steps come after every key of the passes: wave 0 places them with DPP-row scans
+  // (lane 16 h + t: key NT + t, head h) on the running sums carried so far
+  float evt = 0.0f;
+  if (TAIL) {
+    if (wave == 0) {
+      long long tot_l = 0;
+      int tot_c = 0;
+      if (tn > 0) {
+        const bool valid = tt < tn;
+        float Mt = Mh[0];
+        double ct = carry[0];
+        long long it = itot[0];
+        int ns = nspc[0];
+#pragma unroll
+        for (int h = 1; h < kGqa; ++h)
+          if (th == h) { Mt = Mh[h]; ct = carry[h]; it = itot[h]; ns = nspc[h]; }
+        evt = valid ? exp_cr(sct * a.scale - Mt) : 0.0f;
+        if (valid && a.keep_e) a.e[(size_t)(g * kGqa + th) * a.ld + kb + NT + tt] = evt;
+        const float fin = row_incl_scan_dpp(evt);
+        const double ab = ct + (double)(fin - evt);
+        bool sp;
+        int bin;
+        double dinc;
+        classify_d(ab, ab + (double)evt, evt, sp, bin, dinc);
+        sp = sp && valid;
+        if (!valid) dinc = 0.0;
+        s_bin[th * SB + NT + tt] = (valid && !sp) ? (int8_t)bin : kNoBin8;
+        wave_lds_sync();
+        const unsigned long long msk = __ballot(sp);
+        const unsigned rowm = (unsigned)(msk >> (16 * th)) & 0xFFFFu;
+        const double din = row_incl_scan_dpp(dinc);
+        if (sp) {
+          const int id = ns + __popc(rowm & ((1u << tt) - 1u));
+          if (id < kMaxSpecial) {
+            const int8_t bp8 = s_bin[th * SB + NT + tt - 1];
+            const int bprev = bp8 == kNoBin8 ? kNoBinade : bp8;
+            Special x;
+            x.ipre = it + (long long)(din - dinc);
+            x.e = evt;
+            x.meta = (NT + tt) | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+            s_spec[th * kMaxSpecial + id] = x;
+          }
+        }
+        tot_l = (long long)__shfl(din, 16 * th + 15);
+        tot_c = __popc(rowm);
+      }
+      if (tt == 0) {
+        s_tt[th] = tot_l;
+        s_tc[th] = tot_c;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      itot[h] += s_tt[h];
+      nspc[h] += s_tc[h];
+    }
+  }
+  __syncthreads();                         // s_spec complete
+  // (spec timestamp removed)
+  // wave h writes head h's specials (staged in LDS) and record: only waves 0..3 store anything
+  // barrier B waits for
+  if (wave < kGqa) {
+    const int h = wave, ns = min(pick4(nspc, h), kMaxSpecial);
+    if (lane < ns) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
+    if (ns > 0) __builtin_amdgcn_s_waitcnt(0);   // the specials are visible before the record is
+    if (lane == 0) {
+      ChunkRec rc;
+      rc.tot = pick4(itot, h);
+      rc.nsp = pick4(nspc, h);
+      rc.blast = (nk > 0 && s_bin[h * SB + nk - 1] != kNoBin8) ? s_bin[h * SB + nk - 1] : kNoBinade;
+      unsigned long long w0, w1;
+      pack_rec(rc, tag, w0, w1);
+      st_agent(trec + (h * GM + wi) * 2, w0);
+      st_agent(trec + (h * GM + wi) * 2 + 1, w1);
+    }
+  }
+  RTS(3);
+
+  // ---------------------------------------------------------------- barrier B: the exact sums
+  // wave h polls head h's records of every workgroup, then walks them (every workgroup of the
+  // group walks the same records to the same sums: no second hand-off)
+  if (wave < kGqa) {
+    const int hh = g * kGqa + wave;
+    unsigned long long v[2];
+    poll_tagged(trec + wave * GM * 2, 2, 2, G, tag, v, err);
+    RTS(4);
+    const ChunkRec x = unpack_rec(v[0], v[1]);
+    float sres;
+    bool gres;
+    walk_one<WS>(x, a.spec + (size_t)hh * G * kMaxSpecial, G, (int64_t)a.kpw, (int64_t)a.nfill,
+                 reinterpret_cast<WS *>(ldx)[wave], sres, gres);
+    if (lane == 0) {
+      s_S[wave] = sres;
+      s_ok[wave] = gres ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  if (!(s_ok[0] && s_ok[1] && s_ok[2] && s_ok[3])) {
+    // a classification assumption failed (the same in every workgroup of the group, since all
+    // walk the same records): publish e device-wide and run the serial loop itself
+    if (!a.keep_e) {
+#pragma unroll
+      for (int r = 0; r < MP; ++r)
+        if (r * NT + tid < nk)
+#pragma unroll
+          for (int h = 0; h < kGqa; ++h) a.e[(size_t)(g * kGqa + h) * a.ld + kb + r * NT + tid] = ev[r][h];
+      if (TAIL && wave == 0 && tt < tn) a.e[(size_t)(g * kGqa + th) * a.ld + kb + NT + tt] = evt;
+    }
+    __threadfence();
+    group_barrier(cnt + 3 * kCounterStride, (unsigned)G, err);
+    if (wave < kGqa && !s_ok[wave]) {
+      const int hh = g * kGqa + wave;
+      float ss = 0.0f;
+      for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
+        const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
+        const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
+        for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+      }
+      if (lane == 0) s_S[wave] = ss;
+    }
+    __syncthreads();
+  }
+  if (wi == 0 && tid < kGqa) {
+    a.sum[g * kGqa + tid] = s_S[tid];
+    a.status[g * kGqa + tid] = s_ok[tid] ? 0u : 1u;
+  }
+  RTS(5);
+
+  // ---------------------------------------------------------------- p16 and PV
+  // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296), the 4 heads of a
+  // key side by side in LDS; out += p16 * V over this workgroup's rows, 4 heads per V row read
+  uint2 *s_p16 = reinterpret_cast<uint2 *>(ldx);
+  {
+    float S[kGqa];
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) S[h] = s_S[h];
+#pragma unroll
+    for (int r = 0; r < MP; ++r) {
+      if (r * NT < nk) {
+        const int kl = r * NT + tid;
+        _Float16 pk[kGqa];
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) pk[h] = (_Float16)(kl < nk ? ev[r][h] / S[h] : 0.0f);
+        uint2 pw;
+        pw.x = (uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16);
+        pw.y = (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16);
+        s_p16[kl] = pw;
+      }
+    }
+    if (TAIL && wave == 0 && tt < tn) {
+      float St = S[0];
+#pragma unroll
+      for (int h = 1; h < kGqa; ++h)
+        if (th == h) St = S[h];
+      reinterpret_cast<_Float16 *>(s_p16 + NT + tt)[th] = (_Float16)(evt / St);
+    }
+  }
+  __syncthreads();
+  float acc[kGqa][VR::EPL];
+  RTS(12);
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) acc[h][i] = 0.0f;
+  auto probs = [&](int k, float (&p)[kGqa]) {
+    const uint2 pw = k < nk ? s_p16[k] : make_uint2(0u, 0u);
+    p[0] = f16_to_f32(pw.x & 0xFFFFu);
+    p[1] = f16_to_f32(pw.x >> 16);
+    p[2] = f16_to_f32(pw.y & 0xFFFFu);
+    p[3] = f16_to_f32(pw.y >> 16);
+  };
+  if constexpr (VRES) {
+    // rows 32*kResVTiles.. (at most one slot) are not resident: this wave's row of that slot
+    const int kx = kResVTiles * 32 + wave * 4 + vkk;
+    uint4 xw = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t xs = 0u;
+    if (kResVTiles * 32 < nk) {
+      const int64_t slot = slot_t<PG>(L, kb + min(kx, nk - 1));
+      xw = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+      xs = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+    }
+#pragma unroll
+    for (int s = 0; s < kResVTiles; ++s) {
+      if (s * 32 < nk) {
+        const int k = s * 32 + wave * 4 + vkk;
+        const uint2 pw = k < nk ? s_p16[k] : make_uint2(0u, 0u);
+        const float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
+                               f16_to_f32(pw.y >> 16)};
+        const float vsc = k < nk ? f16_to_f32(((vsub >> 1) & 1) ? (vsw[s] >> 16) : (vsw[s] & 0xFFFFu)) : 0.0f;
+        v_accum<BKV_Q8_0>(vd[s], vsc, p, acc);
+      }
+    }
+    if (kResVTiles * 32 < nk) {
+      float p[kGqa];
+      probs(kx, p);
+      const float vsc = kx < nk ? f16_to_f32(((vsub >> 1) & 1) ? (xs >> 16) : (xs & 0xFFFFu)) : 0.0f;
+      v_accum<BKV_Q8_0>(xw, vsc, p, acc);
+    }
+  } else {
+    constexpr int RS = NW * VR::KPW;        // rows per workgroup step
+    constexpr int U = 4;                    // row loads in flight per lane
+    constexpr int RB = row_bytes(VF);
+    for (int base = 0; base < nk; base += RS * U) {
+      uint4 wv[U];
+      uint32_t sw[U];
+      int kl[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        kl[u] = base + u * RS + wave * VR::KPW + vkk;
+        const int64_t slot = slot_t<PG>(L, kb + min(kl[u], nk - 1));
+        wv[u] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * RB + vsub * 16);
+        sw[u] = 0u;
+        if (VF == BKV_Q8_0)
+          sw[u] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float p[kGqa];
+        probs(kl[u], p);
+        float vsc = 1.0f;
+        if (VF == BKV_Q8_0) vsc = f16_to_f32(((vsub >> 1) & 1) ? (sw[u] >> 16) : (sw[u] & 0xFFFFu));
+        if (kl[u] >= nk) {
+          vsc = 0.0f;
+          wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        v_accum<VF>(wv[u], vsc, p, acc);
+      }
+    }
+  }
+  RTS(13);
+  RTSW(15, 7);
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) {
+      float v = acc[h][i];
+      if (VR::LPR == 16) v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[h][i] = v;
+    }
+  RTS(14);
+  RTSW(10, 7);
+  __syncthreads();                         // every wave is done with its V rows
+  RTSW(11, 7);
+  float *s_red = reinterpret_cast<float *>(lds);   // [NW][kGqa][kHd]
+  if (vkk == 0) {
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int i = 0; i < VR::EPL; ++i) s_red[(wave * kGqa + h) * kHd + vsub * VR::EPL + i] = acc[h][i];
+  }
+  __syncthreads();
+  float *part_g = a.part + (size_t)g * G * kGqa * kHd;
+  {
+    static_assert(kGqa * kHd == 2 * NT, "two partial elements per thread");
+    float2 v = make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) {
+      v.x += s_red[wv * kGqa * kHd + 2 * tid];
+      v.y += s_red[wv * kGqa * kHd + 2 * tid + 1];
+    }
+    st_f2(reinterpret_cast<float2 *>(part_g + (size_t)wi * kGqa * kHd) + tid, v);
+  }
+  RTS(6);
+
+  // ---------------------------------------------------------------- barrier C: merge + gate
+  group_barrier(cnt + 2 * kCounterStride, (unsigned)G, err);
+  RTS(7);
+  if (wi == 0 && tid == 0) st_agent(gs, gen);   // every workgroup of the group has read it
+  {
+    constexpr int E = kGqa * kHd;
+    const int sl = (E + G - 1) / G;                      // elements per workgroup
+    const int e0 = wi * sl, ecount = max(0, min(E, e0 + sl) - e0);
+    for (int c0 = 0; c0 < ecount; c0 += NT) {
+      const int ne = min(NT, ecount - c0);
+      const int ngrp = NT / ne;                          // threads per element
+      const int el = tid % ne, grp = tid / ne;
+      constexpr int B = 8;
+      float sacc = 0.0f;
+      if (grp < ngrp) {
+        for (int w0 = grp; w0 < G; w0 += ngrp * B) {
+          float t[B];
+#pragma unroll
+          for (int u = 0; u < B; ++u) {
+            const int ww = w0 + u * ngrp;
+            t[u] = ww < G ? ld_agent(&part_g[(size_t)ww * E + e0 + c0 + el]) : 0.0f;
+          }
+#pragma unroll
+          for (int u = 0; u < B; ++u) sacc += t[u];
+        }
+        s_red[grp * ne + el] = sacc;
+      }
+      __syncthreads();
+      if (tid < ne) {
+        float v = 0.0f;
+        for (int j = 0; j < ngrp; ++j) v += s_red[j * ne + tid];
+        const int eg = e0 + c0 + tid;
+        const size_t oi = (size_t)g * E + eg;           // out is [nh][hd], head g*kGqa + eg/hd
+        a.out[oi] = v;
+        if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+      }
+      __syncthreads();
+    }
+  }
+  RTS(8);
+}
+
+template <int KF, int VF>
+static int resident_capacity() {
+  static int cap = -1;
+  if (cap < 0) {
+    int dev = 0, per = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, resident_kernel<KF, VF, false, false>, kResNT, 0) != hipSuccess)
+      cap = 0;
+    else
+      cap = per * pr.multiProcessorCount;
+  }
+  return cap;
+}
+
+int resident_max_workgroups(int kf, int vf) {
+  BKV_FMT_SWITCH(kf, vf, { return resident_capacity<KF_, VF_>(); });
+  return 0;
+}
+
+template <int KF, int VF, bool VRES>
+static void launch_res(const ResArgs &a, hipStream_t st) {
+  const dim3 grid(a.G * a.nkv), block(kResNT);
+  if (a.L.page) hipLaunchKernelGGL((resident_kernel<KF, VF, VRES, true>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((resident_kernel<KF, VF, VRES, false>), grid, block, 0, st, a);
+}
+
+// The grid never exceeds what the occupancy query says is resident at once (one workgroup per CU),
+// so on a device not held by other long-running kernels every wait is reached by its producers.
+hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st) {
+  BKV_FMT_SWITCH(kf, vf, {
+    if constexpr (VF_ == BKV_Q8_0) {
+      if (vres) {
+        launch_res<KF_, VF_, true>(a, st);
+        return hipGetLastError();
+      }
+    }
+    launch_res<KF_, VF_, false>(a, st);
+  });
+  return hipGetLastError();
+}
+
+}  // namespace bkv

@@ -121,9 +121,10 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
  * workspace afterwards. */
 int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
 
-/* Which decode implementation a call with nfill keys takes on the current device: 1 = the fused
- * single cooperative launch, 0 = the four-launch split path (also forced by BKV_DECODE=split),
- * -1 = bad arguments. */
+/* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
+ * single launch (one workgroup per CU, the default), 1 = the older fused single launch, 0 = the
+ * four-launch split path; -1 = bad arguments. The environment variable BKV_DECODE = split | fused |
+ * resident forces one (read on every call). */
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill);
 
 /* Workspace needed by op (enum bkv_op) for contexts up to max_ctx positions (prefill: max_ctx is

@@ -13,13 +13,13 @@ TOL = 1e-4
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["fused", "split"])
+PATHS = {"resident": 2, "fused": 1, "split": 0}
+
+
+@pytest.fixture(params=list(PATHS))
 def path(request, monkeypatch):
-    """Run a test through both decode implementations (the library reads BKV_DECODE per call)."""
-    if request.param == "split":
-        monkeypatch.setenv("BKV_DECODE", "split")
-    else:
-        monkeypatch.delenv("BKV_DECODE", raising=False)
+    """Run a test through every decode implementation (the library reads BKV_DECODE per call)."""
+    monkeypatch.setenv("BKV_DECODE", request.param)
     return request.param
 FMTS = [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16), (BKV_F16, BKV_Q8_0), (BKV_Q8_0, BKV_F16)]
 
@@ -121,10 +121,11 @@ def test_deterministic_repeat(path):
 
 @pytest.mark.parametrize("kf,vf,n,seed", [(BKV_Q8_0, BKV_Q8_0, 4097, 1), (BKV_F16, BKV_F16, 3000, 7),
                                           (BKV_Q8_0, BKV_Q8_0, 40000, 2)])
-def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed, path):
+def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed, path, monkeypatch):
     """The intermediates the reference's bitwise gate (BONSAI_QCHECK stages A/B) compares: every score,
     every e_j = exp(s_j*scale - max) and the serial fp32 softmax sum match the oracle bit for bit, and
     so do the fp16 probabilities formed from them."""
+    monkeypatch.setenv("BKV_KEEP_INTERMEDIATES", "1")
     say(f"bit-exact intermediates kf={kf} n={n}")
     dev, host = pair(1, n, kf, vf)
     fill(dev, host, 0, n, seed=seed)
@@ -145,8 +146,9 @@ def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed, path):
     assert report("out", out.cpu().numpy(), want) <= TOL
 
 
-def test_identical_keys_uniform_attention(path):
+def test_identical_keys_uniform_attention(path, monkeypatch):
     """All scores equal: every e_j = 1 and the serial sum is exactly n; p = 1/n in fp16."""
+    monkeypatch.setenv("BKV_KEEP_INTERMEDIATES", "1")
     n = 5000
     dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
     k1, _ = oracle.synth_kv(1, 4, 256, 9, 0)
@@ -161,3 +163,61 @@ def test_identical_keys_uniform_attention(path):
     _, e, ssum, status = dev.debug_intermediates(n)
     assert torch.all(e == 1.0) and torch.all(ssum == float(n)) and int(status.sum()) == 0
     assert report("uniform", out.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("kf,vf", [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16)])
+def test_paged_matches_oracle_and_contiguous(kf, vf, path):
+    """Paged cache (64-token pages, a seeded random permutation of a 48-page pool as each layer's block
+    table): the oracle's paged decode matches, and the result equals the contiguous cache's bit for bit
+    (same keys in the same order, only their slots differ)."""
+    n, page, pool = 2900, 64, 48
+    rng = np.random.default_rng(3)
+    bt = np.stack([rng.permutation(pool)[:pool] for _ in range(2)]).astype(np.int32)
+    say(f"paged kf={kf} vf={vf} n={n} path={path}")
+    dev, host = pair(2, pool * page, kf, vf, page_tokens=page, max_pages=pool, block_table=bt)
+    flat, _ = pair(2, pool * page, kf, vf)
+    k, v = fill(dev, host, 1, n, seed=3)
+    flat.append(1, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    q, g = qg(3, 1)
+    want, wg = host.decode(1, n, q, g, nthreads=8)
+    out, og = dev.decode(1, n, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    o2, _ = flat.decode(1, n, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    assert same_bytes(dev, host) == [0] * len(same_bytes(dev, host))
+    assert report("paged", out.cpu().numpy(), want) <= TOL
+    assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
+    assert torch.equal(out, o2)
+
+
+def test_consecutive_decode_steps(path):
+    """BASELINE config 3's pattern at a smaller context: consecutive decode_steps on one workspace
+    (each call appends one token and attends over all of them), every step checked against the
+    oracle, across layers that share the workspace."""
+    n0, steps = 3000, 6
+    dev, host = pair(2, n0 + steps, BKV_Q8_0, BKV_Q8_0)
+    for layer in range(2):
+        fill(dev, host, layer, n0, seed=2)
+    kn, vn = oracle.synth_kv(steps * 2, 4, 256, 77, 0, outliers=3)
+    worst = 0.0
+    for i in range(steps):
+        for layer in range(2):
+            t = 2 * i + layer
+            host.append(layer, n0 + i, kn[t:t + 1], vn[t:t + 1])
+            q, _ = qg(20 + i, layer)
+            want, _ = host.decode(layer, n0 + i + 1, q, nthreads=8)
+            out, _ = dev.decode_step(layer, n0 + i, torch.from_numpy(kn[t:t + 1]).cuda(),
+                                     torch.from_numpy(vn[t:t + 1]).cuda(), torch.from_numpy(q).cuda())
+            torch.cuda.synchronize()
+            worst = max(worst, report(f"step {i} layer {layer}", out.cpu().numpy(), want))
+    assert same_bytes(dev, host) == [0, 0, 0, 0]
+    assert worst <= TOL
+
+
+def test_decode_path_selection(monkeypatch):
+    """The resident single launch is the default wherever it fits; BKV_DECODE forces the others."""
+    dev, _ = pair(1, 70000, BKV_Q8_0, BKV_Q8_0)
+    monkeypatch.delenv("BKV_DECODE", raising=False)
+    assert dev.decode_path(1) == 2 and dev.decode_path(32769) == 2 and dev.decode_path(65537) == 2
+    for name, code in PATHS.items():
+        monkeypatch.setenv("BKV_DECODE", name)
+        assert dev.decode_path(32769) == code
