@@ -129,23 +129,25 @@ __device__ __forceinline__ void qk_row_dot(const uint4 *row, const float (&qv)[k
     const uint4 scl = row[16];
 #pragma unroll
     for (int b = 0; b < kHd / 32; ++b) {
-      const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
-      float x0[16], x1[16];
-      const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
+      // the block's two 16-element halves in turn, each head's inner chain continuing across them
+      float inner[kGqa];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        x0[i] = sbyte(u0[i >> 2], i & 3);
-        x1[i] = sbyte(u1[i >> 2], i & 3);
+      for (int half = 0; half < 2; ++half) {
+        const uint4 w = row[2 * b + half];
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = sbyte(u[i >> 2], i & 3);
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          if (half == 0) inner[h] = 0.0f;
+          Dot16<16>::run(inner[h], qv[h][2 * b + half], x);
+        }
       }
       const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
       const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
 #pragma unroll
-      for (int h = 0; h < kGqa; ++h) {
-        float inner = 0.0f;
-        Dot16<16>::run(inner, qv[h][2 * b], x0);
-        Dot16<16>::run(inner, qv[h][2 * b + 1], x1);
-        acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner));
-      }
+      for (int h = 0; h < kGqa; ++h) acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner[h]));
     }
   } else {
 #pragma unroll

@@ -435,6 +435,14 @@ __device__ __forceinline__ T row_incl_scan_dpp(T v) {
   return v;
 }
 
+// the sum over the four DPP rows (lanes l, l^16, l^32, l^48) in every lane
+__device__ __forceinline__ float sum4rows(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // classify (bkv_device.h) without branches, the increment as an exact double
 __device__ __forceinline__ void classify_d(double abefore, double aafter, float e, bool &special, int &bin,
                                            double &inc) {
@@ -1008,8 +1016,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 #pragma unroll
     for (int i = 0; i < VR::EPL; ++i) {
       float v = acc[h][i];
-      if (VR::LPR == 16) v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      if (VR::LPR == 16) {
+        v = sum4rows(v);
+      } else {
+        const auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(a2[0]) + __uint_as_float(a2[1]);
+      }
       acc[h][i] = v;
     }
   RTS(14);
