@@ -113,7 +113,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
       p.r_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
       p.r_sum = f;    f += align256((size_t)nh * sizeof(float));
       p.r_status = f; f += align256((size_t)nh * sizeof(unsigned));
-      p.r_part = f;   f += align256((size_t)nkv * gmax * kGqa * kHd * sizeof(float));
+      p.r_part = f;   f += align256((size_t)nkv * gmax * kGqa * kHd * sizeof(unsigned long long));
       p.r_total = f;
       total = std::max(total, f);
     }
@@ -232,7 +232,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
     ra.keep_e = keep_intermediates() ? 1 : 0;
     ra.sum = (float *)(w + p.r_sum);
     ra.status = (unsigned *)(w + p.r_status);
-    ra.part = (float *)(w + p.r_part);
+    ra.part = (unsigned long long *)(w + p.r_part);
     ra.sync = (unsigned *)(w + kResSyncOffset);
 #ifdef BKV_EXPERIMENT_TS
     ra.ts = (unsigned *)w + 32768;
@@ -410,7 +410,10 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
   if (!workspace) return BKV_EWORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return BKV_EALIGN;
   if (ws_bytes < kSyncBytes) return BKV_EWORKSPACE;
-  return hip_fail(launch_workspace_init((unsigned *)workspace, (int)(kSyncBytes / sizeof(unsigned)), stream));
+  // the whole workspace: the sync words, and the tagged partials of the resident path (a tag is
+  // the call generation, which starts at 1)
+  if (ws_bytes / sizeof(unsigned) > 0x7FFFFFFFull) return BKV_EINVAL;
+  return hip_fail(launch_workspace_init((unsigned *)workspace, (int)(ws_bytes / sizeof(unsigned)), stream));
 }
 
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill) {

@@ -9,6 +9,7 @@
 // itself. The grid is sized so that all workgroups are resident at once, so every wait is reached by
 // its producers; each wait is also bounded and records an error word instead of hanging.
 // While the walk runs, the other workgroups stage their first V pass into LDS.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -530,7 +531,8 @@ __global__ void workspace_init_kernel(unsigned *sync, int n) {
 }
 
 hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st) {
-  hipLaunchKernelGGL(workspace_init_kernel, dim3(1), dim3(256), 0, st, sync, nwords);
+  const int blocks = (int)std::min<long long>(1024, ((long long)nwords + 255) / 256);
+  hipLaunchKernelGGL(workspace_init_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, sync, nwords);
   return hipGetLastError();
 }
 

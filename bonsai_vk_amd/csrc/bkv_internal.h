@@ -153,7 +153,7 @@ struct ResArgs {
   int keep_e;
   float *sum;                    // [nh]
   unsigned *status;              // [nh]
-  float *part;                   // [nkv][G][kGqa][hd]
+  unsigned long long *part;      // [nkv][G][kGqa][hd] {float bits, call generation}
   unsigned *sync;                // the resident kernel's sync lines
   unsigned *ts;                  // phase timestamps (experiment builds), or null
 };

@@ -1036,7 +1036,10 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int i = 0; i < VR::EPL; ++i) s_red[(wave * kGqa + h) * kHd + vsub * VR::EPL + i] = acc[h][i];
   }
   __syncthreads();
-  float *part_g = a.part + (size_t)g * G * kGqa * kHd;
+  // the partial, each element tagged with the call's generation: {float bits, gen} in one 64-bit
+  // store, so the merge below polls the data itself (no arrival counter, no stale match: the
+  // generation only grows)
+  unsigned long long *part_g = a.part + (size_t)g * G * kGqa * kHd;
   {
     static_assert(kGqa * kHd == 2 * NT, "two partial elements per thread");
     float2 v = make_float2(0.0f, 0.0f);
@@ -1045,14 +1048,15 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       v.x += s_red[wv * kGqa * kHd + 2 * tid];
       v.y += s_red[wv * kGqa * kHd + 2 * tid + 1];
     }
-    st_f2(reinterpret_cast<float2 *>(part_g + (size_t)wi * kGqa * kHd) + tid, v);
+    unsigned long long *dst = part_g + (size_t)wi * kGqa * kHd + 2 * tid;
+    st_agent(dst, (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)gen << 32));
+    st_agent(dst + 1, (unsigned long long)__float_as_uint(v.y) | ((unsigned long long)gen << 32));
   }
   RTS(6);
 
-  // ---------------------------------------------------------------- barrier C: merge + gate
-  group_barrier(cnt + 2 * kCounterStride, (unsigned)G, err);
-  RTS(7);
-  if (wi == 0 && tid == 0) st_agent(gs, gen);   // every workgroup of the group has read it
+  // ---------------------------------------------------------------- merge + gate
+  // workgroup wi sums slice wi of the group's partials in workgroup order, polling each element
+  // until it carries this call's generation
   {
     constexpr int E = kGqa * kHd;
     const int sl = (E + G - 1) / G;                      // elements per workgroup
@@ -1065,14 +1069,25 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       float sacc = 0.0f;
       if (grp < ngrp) {
         for (int w0 = grp; w0 < G; w0 += ngrp * B) {
-          float t[B];
+          unsigned long long t[B];
+          unsigned spins = 0;
+          for (;;) {
+            bool ok = true;
 #pragma unroll
-          for (int u = 0; u < B; ++u) {
-            const int ww = w0 + u * ngrp;
-            t[u] = ww < G ? ld_agent(&part_g[(size_t)ww * E + e0 + c0 + el]) : 0.0f;
+            for (int u = 0; u < B; ++u) {
+              const int ww = w0 + u * ngrp;
+              t[u] = ww < G ? ld_agent(&part_g[(size_t)ww * E + e0 + c0 + el]) : ((unsigned long long)gen << 32);
+              ok = ok && (unsigned)(t[u] >> 32) == gen;
+            }
+            if (ok) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kResSpin) {
+              atomicOr(err, 1u);
+              break;
+            }
           }
 #pragma unroll
-          for (int u = 0; u < B; ++u) sacc += t[u];
+          for (int u = 0; u < B; ++u) sacc += __uint_as_float((unsigned)t[u]);
         }
         s_red[grp * ne + el] = sacc;
       }
@@ -1088,6 +1103,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       __syncthreads();
     }
   }
+  RTS(7);
+  // every workgroup of the group has written its partial, so all have read the generation
+  if (wi == 0 && tid == 0) st_agent(gs, gen);
   RTS(8);
 }
 

@@ -116,9 +116,8 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
                            const float *q, const float *gate, float *out, float *out_gated,
                            void *workspace, size_t ws_bytes, hipStream_t stream);
 
-/* Prepare a workspace for its first use: zeroes the synchronisation words at its start (a small
- * kernel on `stream`, no memset). Call once after allocating it; the caller must not write into the
- * workspace afterwards. */
+/* Prepare a workspace for its first use: zeroes it (a small kernel on `stream`, no memset). Call
+ * once after allocating it; the caller must not write into the workspace afterwards. */
 int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
 
 /* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
