@@ -46,6 +46,58 @@ static int forced_path() {
   return -1;
 }
 
+// Chunked prefill: 16 queries x 4 heads per workgroup; when that gives fewer than kPfFill
+// workgroups the key range of every query block is split so that the chip fills (never into more
+// splits than the first query block has 64-key tiles).
+static int prefill_splits(int nkv, int nqb, int64_t first_keys) {
+  const int64_t want = std::max<int64_t>(1, cdiv(kPfFill, (int64_t)nkv * nqb));
+  return (int)std::min<int64_t>(want, std::max<int64_t>(1, cdiv(first_keys, kPfTile)));
+}
+
+// BKV_PREFILL=mfma selects the matrix-core prefill (scores and sums in MFMA order: within
+// tolerance of the serial reference on long rows, not bit-identical probabilities); the default
+// is the exact path, one decode row per query.
+static bool prefill_mfma_requested() {
+  const char *e = std::getenv("BKV_PREFILL");
+  return e && std::strcmp(e, "mfma") == 0;
+}
+
+PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q) {
+  PrefillPlan p{};
+  p.nqb = (int)cdiv(n_q, kPfQ);
+  p.nsplit = prefill_splits(nkv, p.nqb, (int64_t)pos0 + std::min(n_q, kPfQ));
+  const size_t rows = (size_t)n_q * nh;
+  size_t o = kSyncBytes;
+  p.off_stats = o;
+  o = align256(o + (size_t)p.nsplit * rows * sizeof(float2));
+  p.off_part = o;
+  if (p.nsplit > 1) o = align256(o + (size_t)p.nsplit * rows * kHd * sizeof(float));
+  p.total = o;
+  return p;
+}
+
+// the exact prefill's workspace for chunks ending at or before max_ctx: fp16-rounded Q of one slice,
+// then per workgroup of a slice the [keys][rows] score / exp scratch
+size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx) {
+  const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile;
+  const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
+  return kSyncBytes + align256((size_t)kPxSlice * nh * kHd * sizeof(float)) +
+         align256(wgs * (size_t)ld * kPxRows * sizeof(float));
+}
+
+// the largest plan_prefill(...).total over every chunk length and start position
+size_t prefill_workspace_bound(int nh, int nkv) {
+  size_t worst = 0;
+  for (int nqb = 1; nqb <= BKV_PREFILL_MAX_Q / kPfQ; ++nqb) {
+    const int nsplit = (int)std::max<int64_t>(1, cdiv(kPfFill, (int64_t)nkv * nqb));
+    const size_t rows = (size_t)nqb * kPfQ * nh;
+    size_t o = align256(kSyncBytes + (size_t)nsplit * rows * sizeof(float2));
+    if (nsplit > 1) o = align256(o + (size_t)nsplit * rows * kHd * sizeof(float));
+    worst = std::max(worst, o);
+  }
+  return worst;
+}
+
 DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
   DecodePlan p;
   p.qk_chunk = qk_keys_per_wg(kfmt);
@@ -356,22 +408,81 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
   int rc = check(d);
   if (rc) return rc;
   if ((rc = check_kernels(d))) return rc;
+  if (layer < 0 || layer >= d->n_layers) return BKV_EINVAL;
   if (n_q < 0 || n_q > BKV_PREFILL_MAX_Q) return BKV_EINVAL;
   if (n_q == 0) return BKV_OK;
   if ((int64_t)pos0 + n_q > max_positions(d)) return BKV_ECAP;
-  const size_t rs = (size_t)d->nh * d->hd;
-  for (int i = 0; i < n_q; ++i) {
-    rc = decode_common(d, layer, pos0 + (uint32_t)i + 1u, q + i * rs, gate ? gate + i * rs : nullptr,
-                       out + i * rs, out_gated ? out_gated + i * rs : nullptr, workspace, ws_bytes,
-                       stream, nullptr);
-    if (rc) return rc;
+  if (!aligned16(q) || !aligned16(out)) return q && out ? BKV_EALIGN : BKV_EINVAL;
+  if ((gate == nullptr) != (out_gated == nullptr)) return BKV_EINVAL;
+  if (gate && (!aligned16(gate) || !aligned16(out_gated))) return BKV_EALIGN;
+  if (!workspace) return BKV_EWORKSPACE;
+  if (((uintptr_t)workspace & 255u) != 0) return BKV_EALIGN;
+  if (!prefill_mfma_requested() && n_q >= kPxMinQ) {
+    // the exact kernel, in slices of at most kPxSlice queries
+    const int64_t ld = cdiv((int64_t)pos0 + n_q, kPxTile) * kPxTile;
+    if (ws_bytes < prefill_exact_workspace(d->nh, d->nkv, (int64_t)pos0 + n_q)) return BKV_EWORKSPACE;
+    char *w = (char *)workspace;
+    PrefillXArgs a{};
+    a.L = view(d, layer);
+    a.nkv = d->nkv;
+    a.nh = d->nh;
+    a.pos0 = pos0;
+    a.chunk_q = n_q;
+    a.scale = d->scale;
+    a.ld = ld;
+    a.q16 = (const float *)(w + kSyncBytes);
+    a.sc = (float *)(w + kSyncBytes + align256((size_t)kPxSlice * d->nh * kHd * sizeof(float)));
+    a.gate = gate;
+    a.out = out;
+    a.out_gated = out_gated;
+    for (int qb = 0; qb < n_q; qb += kPxSlice) {
+      a.q_base = qb;
+      a.n_q = std::min(kPxSlice, n_q - qb);
+      a.nqb = (int)cdiv(a.n_q, kPxQ);
+      if ((rc = hip_fail(launch_prefill_exact(a, d->k_fmt, d->v_fmt, q, stream)))) return rc;
+    }
+    return BKV_OK;
   }
-  return BKV_OK;
+  if (!prefill_mfma_requested()) {
+    // short chunks: every row is the decode row at nfill = pos0 + i + 1
+    const size_t rs = (size_t)d->nh * d->hd;
+    for (int i = 0; i < n_q; ++i) {
+      rc = decode_common(d, layer, pos0 + (uint32_t)i + 1u, q + i * rs,
+                         gate ? gate + i * rs : nullptr, out + i * rs,
+                         out_gated ? out_gated + i * rs : nullptr, workspace, ws_bytes, stream,
+                         nullptr);
+      if (rc) return rc;
+    }
+    return BKV_OK;
+  }
+  const PrefillPlan p = plan_prefill(d->nh, d->nkv, pos0, n_q);
+  if (ws_bytes < p.total) return BKV_EWORKSPACE;
+  char *w = (char *)workspace;
+  PrefillArgs a{};
+  a.L = view(d, layer);
+  a.nkv = d->nkv;
+  a.nh = d->nh;
+  a.pos0 = pos0;
+  a.n_q = n_q;
+  a.scale = d->scale;
+  a.nqb = p.nqb;
+  a.nsplit = p.nsplit;
+  a.q = q;
+  a.gate = gate;
+  a.out = out;
+  a.out_gated = out_gated;
+  a.stats = (float2 *)(w + p.off_stats);
+  a.part = p.nsplit > 1 ? (float *)(w + p.off_part) : nullptr;
+  return hip_fail(launch_prefill(a, d->k_fmt, d->v_fmt, stream));
 }
 
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
   if (check(d) || max_ctx == 0) return 0;
-  if (op != BKV_OP_DECODE && op != BKV_OP_PREFILL) return 0;
+  if (op == BKV_OP_PREFILL)
+    return std::max({prefill_workspace_bound(d->nh, d->nkv),
+                     plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total,
+                     prefill_exact_workspace(d->nh, d->nkv, max_ctx)});
+  if (op != BKV_OP_DECODE) return 0;
   return plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total;
 }
 

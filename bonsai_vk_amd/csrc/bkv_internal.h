@@ -158,6 +158,56 @@ struct ResArgs {
   unsigned *ts;                  // phase timestamps (experiment builds), or null
 };
 
+// ------------------------------------------------------------------ chunked prefill (MFMA)
+constexpr int kPfQ = 16;       // queries per workgroup (x 4 heads = 64 rows)
+constexpr int kPfTile = 64;    // keys per tile
+constexpr int kPfFill = 256;   // workgroups the split count aims for (one per CU)
+
+struct PrefillArgs {
+  LayerView L;
+  int nkv, nh;
+  uint32_t pos0;
+  int n_q;
+  float scale;
+  int nqb, nsplit;               // query blocks, key splits per query block
+  const float *q, *gate;         // [n_q][nh][hd]
+  float *out, *out_gated;
+  float2 *stats;                 // [nsplit][n_q][nh] (max, sum exp) of the split's keys
+  float *part;                   // [nsplit][n_q][nh][hd] normalised partial outputs (nsplit > 1)
+};
+
+struct PrefillPlan {
+  int nqb, nsplit;
+  size_t off_stats, off_part, total;
+};
+PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q);
+size_t prefill_workspace_bound(int nh, int nkv);
+hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st);
+
+// ------------------------------------------------------------------ exact chunked prefill
+constexpr int kPxQ = 8;          // queries per workgroup (x 4 heads = 32 rows)
+constexpr int kPxRows = kPxQ * kGqa;
+constexpr int kPxTile = 256;     // keys per score / exp tile (one per lane of the workgroup)
+constexpr int kPxSlice = 512;    // queries per launch (bounds the score scratch)
+constexpr int kPxMinQ = 16;      // shorter chunks run as decode rows
+
+struct PrefillXArgs {
+  LayerView L;
+  int nkv, nh;
+  uint32_t pos0;
+  int q_base, n_q;               // this slice: queries q_base .. q_base + n_q - 1 of the chunk
+  int chunk_q;                   // queries in the whole chunk (row stride of q / out)
+  float scale;
+  int nqb;
+  int64_t ld;                    // keys per workgroup scratch region (multiple of kPxTile)
+  const float *q16;              // [n_q][nh][hd] this slice's Q rounded through fp16, as fp32
+  const float *gate;
+  float *out, *out_gated;
+  float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp
+};
+hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, const float *q, hipStream_t st);
+size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx);
+
 #define BKV_FMT_SWITCH(KF, VF, ...)                                                    \
   do {                                                                                \
     if ((KF) == BKV_Q8_0 && (VF) == BKV_Q8_0) { constexpr int KF_ = 1, VF_ = 1; __VA_ARGS__; } \

@@ -1,0 +1,717 @@
+// bkv_prefill.hip - chunked prefill attention on the gfx950 matrix cores (bkv_attn_prefill_chunk).
+//
+// Query i of the chunk (position pos0 + i) attends causally to keys 0 .. pos0 + i, exactly the row
+// bkv_attn_decode computes with nfill = pos0 + i + 1 (the reference's prefill is that decode row
+// repeated, runtime_vk/attn_vk.h:261-311 per token; bonsai_forward.h:2752-2759). Rows are (query,
+// head) pairs; the 4 query heads of one KV head share every K/V tile read.
+//
+// Work split: a workgroup owns 16 queries x 4 heads = 64 rows of one KV group and one contiguous
+// range of 64-key tiles (a "split"); splits exist only to fill the chip when the chunk is short.
+// Two passes over the same tiles:
+//   stats  S^T = K . Q^T per tile on MFMA, masked causally; online (max, sum exp) per row,
+//          written per split;
+//   pv     the splits' statistics give the row max M and sum S; scores recomputed bit-identically,
+//          p16 = f16(exp(s*scale - M) / S) (the reference rounds the normalised probability to
+//          fp16 before PV, attn_vk.h:184-189), then out^T = V^T . P^T on MFMA;
+//   merge  (more than one split) the normalised partial outputs are summed in split order, and the
+//          gate applied.
+//
+// Exactness of the matrix-core operands: Q is rounded to fp16 as the reference does; a q8_0 K or V
+// element d*b (fp16 scale d, int8 b) has up to 18 significant bits, so it enters the MFMA as the
+// exact fp16 pair hi = f16(d*b), lo = d*b - hi (the rounding error of an fp16 product is an fp16
+// number, computed by one fp16 fma), and fp16 x fp16 products are exact in the fp32 accumulator.
+// What differs from the serial reference is only the order of the fp32 sums (dot products, the
+// softmax sum and PV), hence a tolerance rather than bit-exact parity for prefill.
+
+#include "bkv_internal.h"
+
+namespace bkv {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfNT = 256;      // 4 waves
+constexpr int kPfRS = 144;      // LDS row stride in bytes of the P and V^T tiles (64 fp16 + pad)
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t w) { return __builtin_bit_cast(h2, w); }
+__device__ __forceinline__ uint32_t as_u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// two signed bytes of w (already biased by 0x80 per byte), selected by SEL, as an exact fp16 pair:
+// 0x64XX is the fp16 number 1024 + XX, so subtracting 1152 leaves the signed byte value.
+template <uint32_t SEL>
+__device__ __forceinline__ h2 bytes_h2(uint32_t wb) {
+  const h2 x = as_h2(__builtin_amdgcn_perm(0x64646464u, wb, SEL));
+  return x - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+
+// exact fp16 split of s*b: hi = f16(s*b) (rounded fp16 product), lo = the product's rounding error
+__device__ __forceinline__ void split_prod(h2 b, h2 s, h2 &hi, h2 &lo) {
+  hi = b * s;
+  lo = __builtin_elementwise_fma(b, s, -hi);
+}
+
+// exp(x) for x <= 0 (or -inf) in fp32 to about 2 ulp: 2^(x log2 e) on the hardware exp2 with the
+// rounding error of the product x*log2(e) carried as a first-order correction
+__device__ __forceinline__ float fexp(float x) {
+  x = fmaxf(x, -150.0f);
+  constexpr float L = 0x1.715476p0f;          // log2(e) rounded to float
+  constexpr float Llo = 1.925963033e-8f;      // log2(e) - L
+  const float t = x * L;
+  const float err = fmaf(x, L, -t) + x * Llo;
+  const float y = __builtin_amdgcn_exp2f(t);
+  return fmaf(y, err * 0.6931471806f, y);
+}
+
+struct PfGeo {
+  int g, s, qb, q0, nqv, t0, t1;
+  uint32_t kend;
+};
+
+// blockIdx -> (KV group, split, query block). Workgroups are dealt to the 8 XCDs round-robin; when
+// the grid is a multiple of 8 the index is permuted so that one XCD runs consecutive query blocks
+// of one (group, split), which read the same K/V tiles through that XCD's L2.
+__device__ __forceinline__ PfGeo pf_geo(const PrefillArgs &a) {
+  const int n = gridDim.x, b = blockIdx.x;
+  const int i = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
+  PfGeo p;
+  p.qb = i % a.nqb;
+  p.s = (i / a.nqb) % a.nsplit;
+  p.g = i / (a.nqb * a.nsplit);
+  p.q0 = p.qb * kPfQ;
+  p.nqv = min(kPfQ, a.n_q - p.q0);
+  p.kend = a.pos0 + (uint32_t)(p.q0 + p.nqv);
+  const int nt = (int)((p.kend + kPfTile - 1) / kPfTile);
+  p.t0 = (int)((int64_t)p.s * nt / a.nsplit);
+  p.t1 = (int)((int64_t)(p.s + 1) * nt / a.nsplit);
+  return p;
+}
+
+// Q fragments (MFMA B operand of S^T = K.Q^T): row-tile nt, k-step s, lane l holds Q[row 16nt +
+// l%16][dims 64(l/16) + 8s .. + 8] in fp16 (rounded to nearest even)
+__device__ __forceinline__ void load_q(const PrefillArgs &a, const PfGeo &p, int lane, h8 (&qf)[4][8]) {
+  const int lr = lane & 15, lq = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int r = 16 * nt + lr;
+    const int qi = min(p.q0 + (r >> 2), a.n_q - 1);
+    const float *qp = a.q + ((size_t)qi * a.nh + (size_t)(p.g * kGqa + (r & 3))) * kHd + 64 * lq;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(qp + 8 * s);
+      const float4 x1 = *reinterpret_cast<const float4 *>(qp + 8 * s + 4);
+      h8 h;
+      h[0] = (_Float16)x0.x; h[1] = (_Float16)x0.y; h[2] = (_Float16)x0.z; h[3] = (_Float16)x0.w;
+      h[4] = (_Float16)x1.x; h[5] = (_Float16)x1.y; h[6] = (_Float16)x1.z; h[7] = (_Float16)x1.w;
+      qf[nt][s] = h;
+    }
+  }
+}
+
+// the raw K bytes one lane feeds to the MFMA for a tile: key kb + l%16, dims 64(l/16) .. + 64
+template <int KF>
+struct KRaw {
+  uint4 d[KF ? 4 : 8];
+  uint32_t sc;                  // q8_0: the scales of blocks 2(l/16), 2(l/16)+1
+};
+
+template <int KF, bool PG>
+__device__ __forceinline__ void load_k(const LayerView &L, int nkv, int g, uint32_t key, int lq,
+                                       KRaw<KF> &r) {
+  const int64_t sl = slot_t<PG>(L, key);
+  constexpr int RB = row_bytes(KF ? BKV_Q8_0 : BKV_F16);
+  const uint4 *src = reinterpret_cast<const uint4 *>(L.kd + (sl * nkv + g) * RB + (RB / 4) * lq);
+#pragma unroll
+  for (int c = 0; c < (KF ? 4 : 8); ++c) r.d[c] = src[c];
+  if constexpr (KF)
+    r.sc = *reinterpret_cast<const uint32_t *>(L.ks + (sl * nkv + g) * kScaleRowBytes + 4 * lq);
+}
+
+// S^T tile (16 keys of this wave x 64 rows): acc[nt][i] = dot(K[key 4(l/16)+i], Q[row 16nt + l%16])
+template <int KF>
+__device__ __forceinline__ void qk_tile(const KRaw<KF> &r, const h8 (&qf)[4][8], f4 (&acc)[4]) {
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if constexpr (KF) {
+      const uint32_t w0 = r.d[s >> 1][(s & 1) * 2] ^ 0x80808080u;
+      const uint32_t w1 = r.d[s >> 1][(s & 1) * 2 + 1] ^ 0x80808080u;
+      const uint32_t sw = s < 4 ? (r.sc & 0xFFFFu) * 0x10001u : (r.sc >> 16) * 0x10001u;
+      const h2 sc = as_h2(sw);
+      h2 hi[4], lo[4];
+      split_prod(bytes_h2<0x04010400u>(w0), sc, hi[0], lo[0]);
+      split_prod(bytes_h2<0x04030402u>(w0), sc, hi[1], lo[1]);
+      split_prod(bytes_h2<0x04010400u>(w1), sc, hi[2], lo[2]);
+      split_prod(bytes_h2<0x04030402u>(w1), sc, hi[3], lo[3]);
+      const h8 ah = {hi[0][0], hi[0][1], hi[1][0], hi[1][1], hi[2][0], hi[2][1], hi[3][0], hi[3][1]};
+      const h8 al = {lo[0][0], lo[0][1], lo[1][0], lo[1][1], lo[2][0], lo[2][1], lo[3][0], lo[3][1]};
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        acc[nt] = mfma16(ah, qf[nt][s], acc[nt]);
+        acc[nt] = mfma16(al, qf[nt][s], acc[nt]);
+      }
+    } else {
+      const h8 ak = __builtin_bit_cast(h8, r.d[s]);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma16(ak, qf[nt][s], acc[nt]);
+    }
+  }
+}
+
+// causal limit of the lane's rows: the last key row 16nt + l%16 may see (-1: no such query)
+__device__ __forceinline__ void row_limits(const PrefillArgs &a, const PfGeo &p, int lr, int (&lim)[4]) {
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int r = 16 * nt + lr;
+    lim[nt] = (r >> 2) < p.nqv ? (int)(a.pos0 + (uint32_t)(p.q0 + (r >> 2))) : -1;
+  }
+}
+
+// ------------------------------------------------------------------ pass 1: row statistics
+template <int KF, bool PG>
+__global__ __launch_bounds__(kPfNT) void prefill_stats_kernel(PrefillArgs a) {
+  const PfGeo p = pf_geo(a);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lq = lane >> 4;
+  __shared__ float2 s_st[4][4][64];
+
+  h8 qf[4][8];
+  load_q(a, p, lane, qf);
+  int lim[4];
+  row_limits(a, p, lr, lim);
+  float m[4], l[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) { m[nt] = -3.0e38f; l[nt] = 0.f; }
+
+  const uint32_t klast = p.kend - 1;
+  KRaw<KF> cur, nxt;
+  if (p.t0 < p.t1) load_k<KF, PG>(a.L, a.nkv, p.g, min((uint32_t)(p.t0 * kPfTile + 16 * w + lr), klast), lq, cur);
+  for (int t = p.t0; t < p.t1; ++t) {
+    const int tn = min(t + 1, p.t1 - 1);
+    load_k<KF, PG>(a.L, a.nkv, p.g, min((uint32_t)(tn * kPfTile + 16 * w + lr), klast), lq, nxt);
+    f4 acc[4];
+    qk_tile<KF>(cur, qf, acc);
+    const int kb = t * kPfTile + 16 * w + 4 * lq;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      float v[4], mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = kb + i <= lim[nt] ? acc[nt][i] * a.scale : -INFINITY;
+        mx = fmaxf(mx, v[i]);
+      }
+      const float mn = fmaxf(m[nt], mx);
+      float sum = l[nt] * fexp(m[nt] - mn);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum += fexp(v[i] - mn);
+      m[nt] = mn;
+      l[nt] = sum;
+    }
+    cur = nxt;
+  }
+  // the four lanes holding one row (l%16 equal), then the four waves
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) s_st[w][lq][16 * nt + lr] = make_float2(m[nt], l[nt]);
+  __syncthreads();
+  if (tid < 64) {
+    float mm = -3.0e38f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) mm = fmaxf(mm, s_st[k >> 2][k & 3][tid].x);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float2 e = s_st[k >> 2][k & 3][tid];
+      ss += e.y * fexp(e.x - mm);
+    }
+    if ((tid >> 2) < p.nqv) {
+      const size_t row = (size_t)(p.q0 + (tid >> 2)) * a.nh + p.g * kGqa + (tid & 3);
+      a.stats[(size_t)p.s * a.n_q * a.nh + row] = make_float2(mm, ss);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ pass 2: probabilities and PV
+template <int VF>
+struct VRaw {
+  uint4 a[VF ? 2 : 4], b[VF ? 2 : 4];   // keys 2kp, 2kp+1: dims 64w + 32h .. + 32
+  uint32_t sa, sb;                       // q8_0: their scales (fp16 bits in the low half)
+};
+
+template <int VF, bool PG>
+__device__ __forceinline__ void load_v(const LayerView &L, int nkv, int g, uint32_t ka, uint32_t kb,
+                                       int w, int h, VRaw<VF> &r) {
+  const int64_t sa = slot_t<PG>(L, ka), sb = slot_t<PG>(L, kb);
+  constexpr int RB = row_bytes(VF ? BKV_Q8_0 : BKV_F16);
+  constexpr int DB = VF ? 1 : 2;   // bytes per element
+  const int off = (64 * w + 32 * h) * DB;
+  const uint4 *pa = reinterpret_cast<const uint4 *>(L.vd + (sa * nkv + g) * RB + off);
+  const uint4 *pb = reinterpret_cast<const uint4 *>(L.vd + (sb * nkv + g) * RB + off);
+#pragma unroll
+  for (int c = 0; c < (VF ? 2 : 4); ++c) { r.a[c] = pa[c]; r.b[c] = pb[c]; }
+  if constexpr (VF) {
+    const int blk = 2 * w + h;
+    r.sa = *reinterpret_cast<const uint16_t *>(L.vs + (sa * nkv + g) * kScaleRowBytes + 2 * blk);
+    r.sb = *reinterpret_cast<const uint16_t *>(L.vs + (sb * nkv + g) * kScaleRowBytes + 2 * blk);
+  }
+}
+
+// V^T into the wave's LDS tiles: vt_hi/vt_lo[dim 0..63][key 0..63] (row stride kPfRS), the lane
+// writing keys 2kp, 2kp+1 of dims 32h .. + 32
+template <int VF>
+__device__ __forceinline__ void put_vt(const VRaw<VF> &r, int kp, int h, char *vt_hi, char *vt_lo) {
+  char *bh = vt_hi + (32 * h) * kPfRS + 4 * kp;
+  if constexpr (VF) {
+    char *bl = vt_lo + (32 * h) * kPfRS + 4 * kp;
+    const h2 sc = as_h2((r.sa & 0xFFFFu) | (r.sb << 16));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t wa = r.a[c >> 2][c & 3] ^ 0x80808080u, wb = r.b[c >> 2][c & 3] ^ 0x80808080u;
+      const uint32_t t0 = __builtin_amdgcn_perm(wb, wa, 0x05010400u);   // a0 b0 a1 b1
+      const uint32_t t1 = __builtin_amdgcn_perm(wb, wa, 0x07030602u);   // a2 b2 a3 b3
+      const h2 x[4] = {bytes_h2<0x04010400u>(t0), bytes_h2<0x04030402u>(t0),
+                       bytes_h2<0x04010400u>(t1), bytes_h2<0x04030402u>(t1)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h2 hi, lo;
+        split_prod(x[i], sc, hi, lo);
+        *reinterpret_cast<uint32_t *>(bh + (4 * c + i) * kPfRS) = as_u(hi);
+        *reinterpret_cast<uint32_t *>(bl + (4 * c + i) * kPfRS) = as_u(lo);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const uint32_t wa = r.a[c >> 2][c & 3], wb = r.b[c >> 2][c & 3];
+      *reinterpret_cast<uint32_t *>(bh + (2 * c) * kPfRS) = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
+      *reinterpret_cast<uint32_t *>(bh + (2 * c + 1) * kPfRS) = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
+    }
+  }
+}
+
+template <int KF, int VF, bool PG>
+__global__ __launch_bounds__(kPfNT) void prefill_pv_kernel(PrefillArgs a) {
+  const PfGeo p = pf_geo(a);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lq = lane >> 4;
+  const int kp = lane & 31, vh = lane >> 5;
+  __shared__ __attribute__((aligned(16))) char s_p[2][64 * kPfRS];
+  __shared__ __attribute__((aligned(16))) char s_vt[4][VF ? 2 : 1][64 * kPfRS];
+  __shared__ float2 s_ms[64];
+
+  // row max and 1/sum from the splits' statistics
+  if (tid < 64) {
+    float mm = -3.0e38f, ss = 0.f;
+    if ((tid >> 2) < p.nqv) {
+      const size_t row = (size_t)(p.q0 + (tid >> 2)) * a.nh + p.g * kGqa + (tid & 3);
+      const size_t rs = (size_t)a.n_q * a.nh;
+      for (int s = 0; s < a.nsplit; ++s) mm = fmaxf(mm, a.stats[s * rs + row].x);
+      for (int s = 0; s < a.nsplit; ++s) {
+        const float2 e = a.stats[s * rs + row];
+        ss += e.y * fexp(e.x - mm);
+      }
+    }
+    s_ms[tid] = make_float2(mm, ss > 0.f ? 1.0f / ss : 0.f);
+  }
+  h8 qf[4][8];
+  load_q(a, p, lane, qf);
+  int lim[4];
+  row_limits(a, p, lr, lim);
+  __syncthreads();
+  float M[4], iS[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const float2 e = s_ms[16 * nt + lr];
+    M[nt] = e.x;
+    iS[nt] = e.y;
+  }
+
+  f4 o[4][4];   // [dim tile][row tile]: out^T[dim 64w + 16mt + 4(l/16) + i][row 16nt + l%16]
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) o[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+  char *vt_hi = s_vt[w][0];
+  char *vt_lo = s_vt[w][VF ? 1 : 0];
+  const uint32_t klast = p.kend - 1;
+  KRaw<KF> kc, kn;
+  VRaw<VF> vc, vn;
+  auto vkeys = [&](int t, uint32_t &ka, uint32_t &kb) {
+    ka = min((uint32_t)(t * kPfTile + 2 * kp), klast);
+    kb = min((uint32_t)(t * kPfTile + 2 * kp + 1), klast);
+  };
+  if (p.t0 < p.t1) {
+    load_k<KF, PG>(a.L, a.nkv, p.g, min((uint32_t)(p.t0 * kPfTile + 16 * w + lr), klast), lq, kc);
+    uint32_t ka, kb;
+    vkeys(p.t0, ka, kb);
+    load_v<VF, PG>(a.L, a.nkv, p.g, ka, kb, w, vh, vc);
+  }
+  int buf = 0;
+  for (int t = p.t0; t < p.t1; ++t) {
+    const int tn = min(t + 1, p.t1 - 1);
+    load_k<KF, PG>(a.L, a.nkv, p.g, min((uint32_t)(tn * kPfTile + 16 * w + lr), klast), lq, kn);
+    {
+      uint32_t ka, kb;
+      vkeys(tn, ka, kb);
+      load_v<VF, PG>(a.L, a.nkv, p.g, ka, kb, w, vh, vn);
+    }
+    f4 acc[4];
+    qk_tile<KF>(kc, qf, acc);
+    const int kb0 = t * kPfTile + 16 * w + 4 * lq;
+    char *pb = s_p[buf];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      h2 pp[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = fexp(acc[nt][i] * a.scale - M[nt]) * iS[nt];
+        pp[i >> 1][i & 1] = (_Float16)(kb0 + i <= lim[nt] ? e : 0.f);
+      }
+      *reinterpret_cast<uint2 *>(pb + (16 * nt + lr) * kPfRS + 2 * (16 * w + 4 * lq)) =
+          make_uint2(as_u(pp[0]), as_u(pp[1]));
+    }
+    put_vt<VF>(vc, kp, vh, vt_hi, vt_lo);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      h8 bp[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+        bp[nt] = *reinterpret_cast<const h8 *>(pb + (16 * nt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const h8 ah = *reinterpret_cast<const h8 *>(vt_hi + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) o[mt][nt] = mfma16(ah, bp[nt], o[mt][nt]);
+        if constexpr (VF) {
+          const h8 al = *reinterpret_cast<const h8 *>(vt_lo + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) o[mt][nt] = mfma16(al, bp[nt], o[mt][nt]);
+        }
+      }
+    }
+    buf ^= 1;
+    kc = kn;
+    vc = vn;
+  }
+
+  // rows' outputs: the final result (one split) or the split's normalised partial
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int r = 16 * nt + lr;
+    if ((r >> 2) >= p.nqv) continue;
+    const size_t row = (size_t)(p.q0 + (r >> 2)) * a.nh + p.g * kGqa + (r & 3);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int d = 64 * w + 16 * mt + 4 * lq;
+      const float4 v = make_float4(o[mt][nt][0], o[mt][nt][1], o[mt][nt][2], o[mt][nt][3]);
+      if (a.nsplit > 1) {
+        *reinterpret_cast<float4 *>(a.part + ((size_t)p.s * a.n_q * a.nh + row) * kHd + d) = v;
+      } else {
+        *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
+        if (a.gate) {
+          const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * kHd + d);
+          float4 og;
+          og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
+          og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
+          og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
+          og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
+          *reinterpret_cast<float4 *>(a.out_gated + row * kHd + d) = og;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ merge of the splits + gate
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
+  const size_t rs4 = n4;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    const float4 *pp = reinterpret_cast<const float4 *>(a.part);
+    float4 v = pp[i];
+    for (int s = 1; s < a.nsplit; ++s) {
+      const float4 x = pp[s * rs4 + i];
+      v.x += x.x; v.y += x.y; v.z += x.z; v.w += x.w;
+    }
+    reinterpret_cast<float4 *>(a.out)[i] = v;
+    if (a.gate) {
+      const float4 gt = reinterpret_cast<const float4 *>(a.gate)[i];
+      float4 og;
+      og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
+      og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
+      og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
+      og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
+      reinterpret_cast<float4 *>(a.out_gated)[i] = og;
+    }
+  }
+}
+
+hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) {
+  const int grid = a.nkv * a.nqb * a.nsplit;
+  const bool pg = a.L.page != 0;
+  BKV_FMT_SWITCH(kf, vf, {
+    if (pg) {
+      hipLaunchKernelGGL((prefill_stats_kernel<KF_, true>), dim3(grid), dim3(kPfNT), 0, st, a);
+      hipLaunchKernelGGL((prefill_pv_kernel<KF_, VF_, true>), dim3(grid), dim3(kPfNT), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((prefill_stats_kernel<KF_, false>), dim3(grid), dim3(kPfNT), 0, st, a);
+      hipLaunchKernelGGL((prefill_pv_kernel<KF_, VF_, false>), dim3(grid), dim3(kPfNT), 0, st, a);
+    }
+  });
+  if (a.nsplit > 1) {
+    const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
+    const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 2048);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(blocks), dim3(256), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+// ================================================================== exact prefill
+// The default prefill: every (query, head) row reproduces the serial reference bit for bit up to
+// the PV contraction. A workgroup owns 8 queries x 4 heads = 32 rows of one KV group and all of
+// their keys, in three sweeps:
+//   1  scores on the vector ALUs in the reference's order (fp16 K: acc = acc + q16*k ascending;
+//      q8_0 K: inner = sum of q16*int8 over a block ascending, acc = acc + f16(scale)*inner; every
+//      product is exact, so each step is one fma), times the softmax scale, masked causally; the
+//      row max. Scores go to a scratch region [key][row].
+//   2  e = exp(v - max) correctly rounded, written back over the scores; one lane per row adds
+//      them in key order (the reference's serial fp32 sum, attn_vk.h:175-189).
+//   3  p16 = f16(e / sum) (correctly rounded division, then round to nearest even), and
+//      out = sum p16 * v on the matrix cores with V as its exact fp16 hi/lo pair.
+// Only the PV sum runs in another order than the reference (fp32 accumulation of exact products).
+
+typedef const __attribute__((address_space(4))) float *cfloat_p;
+
+__global__ __launch_bounds__(256) void q16_kernel(const float *q, float *q16, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    q16[i] = round_f16(q[i]);
+}
+
+template <int KF, int VF, bool PG>
+__global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
+  const int n = gridDim.x, b = blockIdx.x;
+  const int wi = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
+  const int qb = wi % a.nqb, g = wi / a.nqb;
+  const int q0 = a.q_base + qb * kPxQ;                   // first query (chunk index)
+  const int nqv = min(kPxQ, a.q_base + a.n_q - q0);
+  const uint32_t kend = a.pos0 + (uint32_t)(q0 + nqv);  // keys 0 .. kend-1
+  const int ntile = (int)((kend + kPxTile - 1) / kPxTile);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float *sc = a.sc + (size_t)wi * a.ld * kPxRows;
+  // the causal limit of row r is pos0 + q0 + r/4 (rows of queries past the chunk see nothing)
+  const int lim0 = (int)(a.pos0 + (uint32_t)q0);
+
+  __shared__ float s_red[4][kPxRows];
+  __shared__ float s_m[kPxRows], s_sum[kPxRows];
+  __shared__ __attribute__((aligned(16))) char s_big[2 * 256 * 33 * 4 > 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS
+                                                        ? 2 * 256 * 33 * 4
+                                                        : 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS];
+
+  // ---------------------------------------------------------------- sweep 1: exact scores
+  cfloat_p qc = (cfloat_p)(a.q16 + ((size_t)(q0 - a.q_base) * a.nh + (size_t)g * kGqa) * kHd);
+  // row r = 4*qi + hh reads q16 row (q0 + qi, head 4g + hh); rows past the chunk reuse a valid row
+  const int qlast = a.q_base + a.n_q - 1 - q0;
+  float mx[kPxRows];
+#pragma unroll
+  for (int r = 0; r < kPxRows; ++r) mx[r] = -INFINITY;
+  constexpr int RB = row_bytes(KF ? BKV_Q8_0 : BKV_F16);
+  for (int t = 0; t < ntile; ++t) {
+    const uint32_t j = (uint32_t)(t * kPxTile + tid);
+    const int64_t sl = slot_t<PG>(a.L, min(j, kend - 1));
+    const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + (sl * a.nkv + g) * RB);
+    float acc[kPxRows];
+#pragma unroll
+    for (int r = 0; r < kPxRows; ++r) acc[r] = 0.f;
+    uint4 sw4 = make_uint4(0, 0, 0, 0);
+    if constexpr (KF) sw4 = *reinterpret_cast<const uint4 *>(a.L.ks + (sl * a.nkv + g) * kScaleRowBytes);
+#pragma unroll 1
+    for (int blk = 0; blk < 8; ++blk) {
+      float kf[32];
+      if constexpr (KF) {
+        const uint4 k0 = kp[2 * blk], k1 = kp[2 * blk + 1];
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+        for (int e = 0; e < 32; ++e) kf[e] = sbyte(kw[e >> 2], e & 3);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint4 kk = kp[4 * blk + c];
+          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            kf[8 * c + 2 * i] = f16_to_f32(kw[i] & 0xFFFFu);
+            kf[8 * c + 2 * i + 1] = f16_to_f32(kw[i] >> 16);
+          }
+        }
+      }
+      float scl = 0.f;
+      if constexpr (KF) {
+        const uint32_t sw = (&sw4.x)[blk >> 1];
+        scl = f16_to_f32((blk & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+      }
+#pragma unroll
+      for (int r = 0; r < kPxRows; ++r) {
+        const int qi = min(r >> 2, qlast);
+        cfloat_p qr = qc + ((size_t)qi * a.nh + (r & 3)) * kHd + 32 * blk;
+        if constexpr (KF) {
+          float inner = 0.f;
+#pragma unroll
+          for (int e = 0; e < 32; ++e) inner = __builtin_fmaf(qr[e], kf[e], inner);
+          acc[r] = acc[r] + scl * inner;
+        } else {
+          float x = acc[r];
+#pragma unroll
+          for (int e = 0; e < 32; ++e) x = __builtin_fmaf(qr[e], kf[e], x);
+          acc[r] = x;
+        }
+      }
+    }
+    float *dst = sc + (size_t)j * kPxRows;
+#pragma unroll
+    for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * r4 + i;
+        v[i] = (int)j <= lim0 + (r >> 2) && (r >> 2) < nqv ? acc[r] * a.scale : -INFINITY;
+        mx[r] = v[i] > mx[r] ? v[i] : mx[r];
+      }
+      *reinterpret_cast<float4 *>(dst + 4 * r4) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kPxRows; ++r) {
+    const float m = wave_max(mx[r]);
+    if (lane == 0) s_red[w][r] = m;
+  }
+  __syncthreads();
+  if (tid < kPxRows) {
+    float m = fmaxf(fmaxf(s_red[0][tid], s_red[1][tid]), fmaxf(s_red[2][tid], s_red[3][tid]));
+    s_m[tid] = (tid >> 2) < nqv ? m : 0.f;
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- sweep 2: exp and serial sum
+  float *et = reinterpret_cast<float *>(s_big);   // [2][256][33]
+  float sum = 0.f;
+  for (int t = 0; t < ntile; ++t) {
+    const uint32_t j = (uint32_t)(t * kPxTile + tid);
+    float *src = sc + (size_t)j * kPxRows;
+    float *eb = et + (t & 1) * 256 * 33 + tid * 33;
+#pragma unroll
+    for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
+      const float4 v = *reinterpret_cast<const float4 *>(src + 4 * r4);
+      float4 e;
+      e.x = exp_cr(v.x - s_m[4 * r4]);
+      e.y = exp_cr(v.y - s_m[4 * r4 + 1]);
+      e.z = exp_cr(v.z - s_m[4 * r4 + 2]);
+      e.w = exp_cr(v.w - s_m[4 * r4 + 3]);
+      *reinterpret_cast<float4 *>(src + 4 * r4) = e;
+      eb[4 * r4] = e.x;
+      eb[4 * r4 + 1] = e.y;
+      eb[4 * r4 + 2] = e.z;
+      eb[4 * r4 + 3] = e.w;
+    }
+    __syncthreads();
+    if (tid < kPxRows) {
+      const float *col = et + (t & 1) * 256 * 33 + tid;
+#pragma unroll 16
+      for (int k = 0; k < kPxTile; ++k) sum = sum + col[k * 33];
+    }
+  }
+  if (tid < kPxRows) s_sum[tid] = (tid >> 2) < nqv ? sum : 1.0f;
+  __syncthreads();
+
+  // ---------------------------------------------------------------- sweep 3: p16 and PV
+  const int lr = lane & 15, lq = lane >> 4, kp = lane & 31, vh = lane >> 5;
+  char *s_p = s_big;                                              // [2][32 rows][kPfRS]
+  char *vt_hi = s_big + 2 * kPxRows * kPfRS + w * (VF ? 2 : 1) * 64 * kPfRS;
+  char *vt_lo = vt_hi + (VF ? 64 * kPfRS : 0);
+  f4 o[4][2];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) o[mt][0] = o[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+  const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
+  for (int t = 0; t < nt64; ++t) {
+    char *pb = s_p + (t & 1) * kPxRows * kPfRS;
+    {
+      const int k = tid >> 2, r0 = 8 * (tid & 3);
+      const float *src = sc + ((size_t)t * kPfTile + k) * kPxRows + r0;
+      const float4 e0 = *reinterpret_cast<const float4 *>(src);
+      const float4 e1 = *reinterpret_cast<const float4 *>(src + 4);
+      const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const _Float16 h = (_Float16)(ev[i] / s_sum[r0 + i]);
+        *reinterpret_cast<_Float16 *>(pb + (r0 + i) * kPfRS + 2 * k) = h;
+      }
+    }
+    {
+      VRaw<VF> vr;
+      const uint32_t ka = min((uint32_t)(t * kPfTile + 2 * kp), kend - 1);
+      const uint32_t kb = min((uint32_t)(t * kPfTile + 2 * kp + 1), kend - 1);
+      load_v<VF, PG>(a.L, a.nkv, g, ka, kb, w, vh, vr);
+      put_vt<VF>(vr, kp, vh, vt_hi, vt_lo);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      h8 bp[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        bp[nt] = *reinterpret_cast<const h8 *>(pb + (16 * nt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const h8 ah = *reinterpret_cast<const h8 *>(vt_hi + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) o[mt][nt] = mfma16(ah, bp[nt], o[mt][nt]);
+        if constexpr (VF) {
+          const h8 al = *reinterpret_cast<const h8 *>(vt_lo + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) o[mt][nt] = mfma16(al, bp[nt], o[mt][nt]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int r = 16 * nt + lr;
+    if ((r >> 2) >= nqv) continue;
+    const size_t row = (size_t)(q0 + (r >> 2)) * a.nh + g * kGqa + (r & 3);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int d = 64 * w + 16 * mt + 4 * lq;
+      const float4 v = make_float4(o[mt][nt][0], o[mt][nt][1], o[mt][nt][2], o[mt][nt][3]);
+      *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
+      if (a.gate) {
+        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * kHd + d);
+        float4 og;
+        og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
+        og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
+        og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
+        og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
+        *reinterpret_cast<float4 *>(a.out_gated + row * kHd + d) = og;
+      }
+    }
+  }
+}
+
+hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, const float *q, hipStream_t st) {
+  const int grid = a.nkv * a.nqb;
+  const bool pg = a.L.page != 0;
+  {
+    const size_t nq = (size_t)a.n_q * a.nh * kHd;
+    hipLaunchKernelGGL(q16_kernel, dim3((int)std::min<size_t>((nq + 255) / 256, 4096)), dim3(256), 0, st,
+                       q + (size_t)a.q_base * a.nh * kHd, const_cast<float *>(a.q16), nq);
+  }
+  BKV_FMT_SWITCH(kf, vf, {
+    if (pg) hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, true>), dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, false>), dim3(grid), dim3(256), 0, st, a);
+  });
+  return hipGetLastError();
+}
+
+}  // namespace bkv

@@ -1,0 +1,126 @@
+"""GPU parity of the MFMA chunked prefill (bkv_attn_prefill_chunk through the C ABI) against the CPU
+oracle, whose prefill is the decode row repeated per query (the reference's own prefill,
+runtime_vk/attn_vk.h:261-311 once per token). Bar: max relative error 1e-4 per head row
+(max |gpu - oracle| / max |oracle|); the matrix cores sum dot products, the softmax sum and PV in
+another order than the serial reference, so prefill is held to the tolerance, not to bit-exactness."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from bonsai_vk_amd import BKV_F16, BKV_Q8_0
+from tests.gpu_util import fill, pair, qg, report, say
+
+TOL = 1e-4
+pytestmark = pytest.mark.gpu
+FMTS = [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16), (BKV_F16, BKV_Q8_0), (BKV_Q8_0, BKV_F16)]
+
+
+def run_pair(dev, host, layer, pos0, n_q, seed, gate=True):
+    q, g = qg(seed, layer, n=n_q)
+    if not gate:
+        g = None
+    want, wg = host.prefill(layer, pos0, q, g, nthreads=8)
+    out, og = dev.prefill_chunk(layer, pos0, torch.from_numpy(q).cuda(),
+                                None if g is None else torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    r = report(f"prefill pos0={pos0} n_q={n_q}", out.cpu().numpy(), want)
+    if gate:
+        r = max(r, report("gated", og.cpu().numpy(), wg))
+    return r
+
+
+@pytest.mark.parametrize("kf,vf", FMTS)
+@pytest.mark.parametrize("pos0,n_q", [(0, 1), (0, 37), (5, 16), (200, 70), (1000, 130), (3000, 300)])
+def test_prefill_matches_oracle(kf, vf, pos0, n_q):
+    say(f"prefill kf={kf} vf={vf} pos0={pos0} n_q={n_q}")
+    n = pos0 + n_q
+    dev, host = pair(1, n, kf, vf)
+    fill(dev, host, 0, n, seed=n_q)
+    assert run_pair(dev, host, 0, pos0, n_q, seed=pos0 + 1) <= TOL
+
+
+def test_prefill_without_gate_and_layer_offset():
+    dev, host = pair(3, 700, BKV_Q8_0, BKV_Q8_0)
+    for layer in range(3):
+        fill(dev, host, layer, 700, seed=9)
+    assert run_pair(dev, host, 2, 600, 100, seed=4, gate=False) <= TOL
+
+
+@pytest.mark.parametrize("kf,vf", [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16)])
+def test_prefill_paged(kf, vf):
+    """64-token pages, a seeded permutation of a 48-page pool as the block table: matches the oracle,
+    and equals the contiguous cache's result bit for bit."""
+    page, pool, pos0, n_q = 64, 48, 2500, 170
+    rng = np.random.default_rng(5)
+    bt = np.stack([rng.permutation(pool) for _ in range(2)]).astype(np.int32)
+    say(f"prefill paged kf={kf} vf={vf}")
+    dev, host = pair(2, pool * page, kf, vf, page_tokens=page, max_pages=pool, block_table=bt)
+    flat, _ = pair(2, pool * page, kf, vf)
+    k, v = fill(dev, host, 1, pos0 + n_q, seed=6)
+    flat.append(1, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    q, g = qg(6, 1, n=n_q)
+    want, _ = host.prefill(1, pos0, q, g, nthreads=8)
+    out, _ = dev.prefill_chunk(1, pos0, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    o2, _ = flat.prefill_chunk(1, pos0, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    assert report("paged prefill", out.cpu().numpy(), want) <= TOL
+    assert torch.equal(out, o2)
+
+
+def test_prefill_equals_decode_rows():
+    """Each prefill row against the device decode of the same query at nfill = pos0 + i + 1 (the
+    reference's prefill-vs-decode equality leg, align_attn.cpp:1330-1385), to the tolerance."""
+    pos0, n_q = 1500, 40
+    dev, host = pair(1, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, pos0 + n_q, seed=12)
+    q, _ = qg(12, 0, n=n_q)
+    qd = torch.from_numpy(q).cuda()
+    out, _ = dev.prefill_chunk(0, pos0, qd)
+    worst = 0.0
+    for i in range(0, n_q, 7):
+        o, _ = dev.decode(0, pos0 + i + 1, qd[i].contiguous())
+        torch.cuda.synchronize()
+        worst = max(worst, oracle.rel_err(out[i].cpu().numpy(), o.cpu().numpy()))
+    say(f"prefill vs decode rows: max rel err {worst:.3e}")
+    assert worst <= TOL
+
+
+def test_prefill_deterministic():
+    pos0, n_q = 900, 50
+    dev, host = pair(1, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, pos0 + n_q, seed=13)
+    q, g = qg(13, 0, n=n_q)
+    qd, gd = torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda()
+    a, ag = dev.prefill_chunk(0, pos0, qd, gd)
+    b, bg = dev.prefill_chunk(0, pos0, qd, gd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(ag, bg)
+
+
+def test_config5_sampled_rows():
+    """BASELINE config 5 at its true shape for one layer: 512 queries appended onto 8192 cached
+    tokens, q8_0 K+V, seed 4; sampled query rows checked against the oracle's decode row."""
+    pos0, n_q = 8192, 512
+    dev, host = pair(1, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, pos0 + n_q, seed=4, outliers=0)
+    q, g = qg(4, 0, n=n_q)
+    out, og = dev.prefill_chunk(0, pos0, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    out, og = out.cpu().numpy(), og.cpu().numpy()
+    worst = 0.0
+    for i in [0, 1, 15, 16, 17, 100, 255, 256, 400, 510, 511]:
+        want, wg = host.decode(0, pos0 + i + 1, q[i], g[i], nthreads=8)
+        worst = max(worst, oracle.rel_err(out[i], want), oracle.rel_err(og[i], wg))
+    say(f"config5 sampled rows: max rel err {worst:.3e}")
+    assert worst <= TOL
+
+
+def test_prefill_errors():
+    from bonsai_vk_amd import BkvError
+    dev, _ = pair(1, 100, BKV_Q8_0, BKV_Q8_0)
+    q = torch.zeros((10, 16, 256), device="cuda")
+    with pytest.raises(BkvError):
+        dev.prefill_chunk(0, 95, q)          # pos0 + n_q beyond the cache
+    with pytest.raises(BkvError):
+        dev.prefill_chunk(1, 0, q)           # no such layer
