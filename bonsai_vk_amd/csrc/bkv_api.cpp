@@ -76,13 +76,13 @@ PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q) {
   return p;
 }
 
-// the exact prefill's workspace for chunks ending at or before max_ctx: fp16-rounded Q of one slice,
-// then per workgroup of a slice the [keys][rows] score / exp scratch
+// the exact prefill's workspace for chunks ending at or before max_ctx: per workgroup of one slice,
+// the [keys][rows] score / exp scratch
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx) {
+  (void)nh;
   const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile;
   const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
-  return kSyncBytes + align256((size_t)kPxSlice * nh * kHd * sizeof(float)) +
-         align256(wgs * (size_t)ld * kPxRows * sizeof(float));
+  return kSyncBytes + align256(wgs * (size_t)ld * kPxRows * sizeof(float));
 }
 
 // the largest plan_prefill(...).total over every chunk length and start position
@@ -430,16 +430,19 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
     a.chunk_q = n_q;
     a.scale = d->scale;
     a.ld = ld;
-    a.q16 = (const float *)(w + kSyncBytes);
-    a.sc = (float *)(w + kSyncBytes + align256((size_t)kPxSlice * d->nh * kHd * sizeof(float)));
+    a.q = q;
+    a.sc = (float *)(w + kSyncBytes);
     a.gate = gate;
     a.out = out;
     a.out_gated = out_gated;
+#ifdef BKV_EXPERIMENT_TS
+    a.ts = (unsigned *)w + 32768;
+#endif
     for (int qb = 0; qb < n_q; qb += kPxSlice) {
       a.q_base = qb;
       a.n_q = std::min(kPxSlice, n_q - qb);
       a.nqb = (int)cdiv(a.n_q, kPxQ);
-      if ((rc = hip_fail(launch_prefill_exact(a, d->k_fmt, d->v_fmt, q, stream)))) return rc;
+      if ((rc = hip_fail(launch_prefill_exact(a, d->k_fmt, d->v_fmt, stream)))) return rc;
     }
     return BKV_OK;
   }

@@ -185,7 +185,7 @@ size_t prefill_workspace_bound(int nh, int nkv);
 hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st);
 
 // ------------------------------------------------------------------ exact chunked prefill
-constexpr int kPxQ = 8;          // queries per workgroup (x 4 heads = 32 rows)
+constexpr int kPxQ = 4;          // queries per workgroup (x 4 heads = 16 rows)
 constexpr int kPxRows = kPxQ * kGqa;
 constexpr int kPxTile = 256;     // keys per score / exp tile (one per lane of the workgroup)
 constexpr int kPxSlice = 512;    // queries per launch (bounds the score scratch)
@@ -200,12 +200,13 @@ struct PrefillXArgs {
   float scale;
   int nqb;
   int64_t ld;                    // keys per workgroup scratch region (multiple of kPxTile)
-  const float *q16;              // [n_q][nh][hd] this slice's Q rounded through fp16, as fp32
+  const float *q;                // [chunk_q][nh][hd] fp32
   const float *gate;
   float *out, *out_gated;
-  float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp
+  float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp (the slice's workgroups)
+  unsigned *ts;                  // sweep timestamps (experiment builds), or null
 };
-hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, const float *q, hipStream_t st);
+hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st);
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx);
 
 #define BKV_FMT_SWITCH(KF, VF, ...)                                                    \

@@ -23,6 +23,7 @@
 // What differs from the serial reference is only the order of the fp32 sums (dot products, the
 // softmax sum and PV), hence a tolerance rather than bit-exact parity for prefill.
 
+#include "bkv_device.h"
 #include "bkv_internal.h"
 
 namespace bkv {
@@ -472,7 +473,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 
 // ================================================================== exact prefill
 // The default prefill: every (query, head) row reproduces the serial reference bit for bit up to
-// the PV contraction. A workgroup owns 8 queries x 4 heads = 32 rows of one KV group and all of
+// the PV contraction. A workgroup owns 4 queries x 4 heads = 16 rows of one KV group and all of
 // their keys, in three sweeps:
 //   1  scores on the vector ALUs in the reference's order (fp16 K: acc = acc + q16*k ascending;
 //      q8_0 K: inner = sum of q16*int8 over a block ascending, acc = acc + f16(scale)*inner; every
@@ -484,15 +485,54 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 //      out = sum p16 * v on the matrix cores with V as its exact fp16 hi/lo pair.
 // Only the PV sum runs in another order than the reference (fp32 accumulation of exact products).
 
-typedef const __attribute__((address_space(4))) float *cfloat_p;
 
-__global__ __launch_bounds__(256) void q16_kernel(const float *q, float *q16, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
-    q16[i] = round_f16(q[i]);
+#ifdef BKV_EXPERIMENT_TS
+#define PXTS(i) do { if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+#else
+#define PXTS(i) do { } while (0)
+#endif
+
+// one q8_0 K block (32 elements, blk) of the lane's key against every row: the reference's
+// block-factored order, inner = sum of q16*int8 ascending, acc = acc + f16(scale)*inner
+template <int BLK>
+__device__ __forceinline__ void score_block_q8(const uint4 (&rc)[8], const uint4 &sw4, const float *qlane,
+                                               float (&acc)[kPxRows]) {
+  constexpr int H = BLK & 3;   // block within the half row held in rc
+  const uint32_t kw[8] = {rc[2 * H].x, rc[2 * H].y, rc[2 * H].z, rc[2 * H].w,
+                          rc[2 * H + 1].x, rc[2 * H + 1].y, rc[2 * H + 1].z, rc[2 * H + 1].w};
+  float k0[16], k1[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    k0[e] = sbyte(kw[e >> 2], e & 3);
+    k1[e] = sbyte(kw[4 + (e >> 2)], e & 3);
+  }
+  const uint32_t sw = BLK < 2 ? sw4.x : BLK < 4 ? sw4.y : BLK < 6 ? sw4.z : sw4.w;
+  const float scl = f16_to_f32((BLK & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+  const float *qb = qlane + 32 * BLK;
+#pragma unroll
+  for (int r = 0; r < kPxRows; ++r) {
+    float inner = 0.f;
+    Dot16<16>::run(inner, qb[r * kHd], k0);
+    Dot16<16>::run(inner, qb[r * kHd + 16], k1);
+    acc[r] = acc[r] + scl * inner;
+  }
 }
+// blocks B0 .. B0+N-1 (all in one half row)
+template <int B0, int N>
+struct ScoreBlocksQ8 {
+  static __device__ __forceinline__ void run(const uint4 (&rc)[8], const uint4 &sw4, const float *qlane,
+                                             float (&acc)[kPxRows]) {
+    ScoreBlocksQ8<B0, N - 1>::run(rc, sw4, qlane, acc);
+    score_block_q8<B0 + N - 1>(rc, sw4, qlane, acc);
+  }
+};
+template <int B0>
+struct ScoreBlocksQ8<B0, 0> {
+  static __device__ __forceinline__ void run(const uint4 (&)[8], const uint4 &, const float *, float (&)[kPxRows]) {}
+};
 
 template <int KF, int VF, bool PG>
-__global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   const int n = gridDim.x, b = blockIdx.x;
   const int wi = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
   const int qb = wi % a.nqb, g = wi / a.nqb;
@@ -507,67 +547,98 @@ __global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
 
   __shared__ float s_red[4][kPxRows];
   __shared__ float s_m[kPxRows], s_sum[kPxRows];
-  __shared__ __attribute__((aligned(16))) char s_big[2 * 256 * 33 * 4 > 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS
-                                                        ? 2 * 256 * 33 * 4
-                                                        : 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS];
+  constexpr int ES = kPxRows + 1;          // LDS row stride (floats) of the exp tile
+  constexpr int NT = kPxRows / 16;         // MFMA row tiles
+  constexpr int PR = kPxRows / 4;          // probabilities per thread per 64-key tile
+  constexpr int kBig2 = 2 * 256 * ES * 4, kBig3 = 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS;
+  __shared__ __attribute__((aligned(16))) char s_big[kBig2 > kBig3 ? kBig2 : kBig3];
 
+  PXTS(0);
+#ifdef BKV_EXPERIMENT_TS
+  if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + 8] = (unsigned)__smid();
+#endif
   // ---------------------------------------------------------------- sweep 1: exact scores
-  cfloat_p qc = (cfloat_p)(a.q16 + ((size_t)(q0 - a.q_base) * a.nh + (size_t)g * kGqa) * kHd);
-  // row r = 4*qi + hh reads q16 row (q0 + qi, head 4g + hh); rows past the chunk reuse a valid row
-  const int qlast = a.q_base + a.n_q - 1 - q0;
+  // the rows' q16 in LDS: s_q[r][d], row r = query q0 + r/4 (clamped into the chunk), head 4g + r%4
+  float *s_q = reinterpret_cast<float *>(s_big);
+  {
+    const int qlast = a.q_base + a.n_q - 1;
+    for (int i = tid; i < kPxRows * kHd / 4; i += 256) {
+      const int r = i / (kHd / 4), d4 = i % (kHd / 4);
+      const int qi = min(q0 + (r >> 2), qlast);
+      const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * kHd + 4 * d4);
+      *reinterpret_cast<float4 *>(s_q + r * kHd + 4 * d4) =
+          make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
+    }
+  }
+  __syncthreads();
+  const int l16 = lane & 15;
   float mx[kPxRows];
 #pragma unroll
   for (int r = 0; r < kPxRows; ++r) mx[r] = -INFINITY;
   constexpr int RB = row_bytes(KF ? BKV_Q8_0 : BKV_F16);
+  const float *qlane = s_q + l16;
+  auto kaddr = [&](int t) -> int64_t {
+    return slot_t<PG>(a.L, min((uint32_t)(t * kPxTile + tid), kend - 1)) * a.nkv + g;
+  };
+  // q8_0: each half of the K row (128 B) is fetched for the next tile as soon as this tile has
+  // used it, so a load has half a tile to land; fp16: two 64 B blocks ahead
+  uint4 ra[8], rb[8];
+  uint4 swn = make_uint4(0, 0, 0, 0);
+  if constexpr (KF) {
+    const int64_t ro = kaddr(0);
+    const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) { ra[c] = kp[c]; rb[c] = kp[8 + c]; }
+    swn = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
+  }
   for (int t = 0; t < ntile; ++t) {
     const uint32_t j = (uint32_t)(t * kPxTile + tid);
-    const int64_t sl = slot_t<PG>(a.L, min(j, kend - 1));
-    const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + (sl * a.nkv + g) * RB);
     float acc[kPxRows];
 #pragma unroll
     for (int r = 0; r < kPxRows; ++r) acc[r] = 0.f;
-    uint4 sw4 = make_uint4(0, 0, 0, 0);
-    if constexpr (KF) sw4 = *reinterpret_cast<const uint4 *>(a.L.ks + (sl * a.nkv + g) * kScaleRowBytes);
-#pragma unroll 1
-    for (int blk = 0; blk < 8; ++blk) {
-      float kf[32];
-      if constexpr (KF) {
-        const uint4 k0 = kp[2 * blk], k1 = kp[2 * blk + 1];
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    if constexpr (KF) {
+      const uint4 sw4 = swn;
+      const int64_t ro = kaddr(min(t + 1, ntile - 1));
+      const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB);
+      ScoreBlocksQ8<0, 4>::run(ra, sw4, qlane, acc);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) kf[e] = sbyte(kw[e >> 2], e & 3);
-      } else {
+      for (int c = 0; c < 8; ++c) ra[c] = kp[c];
+      swn = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
+      ScoreBlocksQ8<4, 4>::run(rb, sw4, qlane, acc);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) rb[c] = kp[8 + c];
+    } else {
+      const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + kaddr(t) * RB);
+      uint4 b0[4], b1[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) { b0[c] = kp[c]; b1[c] = kp[4 + c]; }
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        uint4 b2[4];
+        const int bn = min(blk + 2, 7);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) b2[c] = kp[4 * bn + c];
+        float k0[16], k1[16];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const uint4 kk = kp[4 * blk + c];
-          const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+          const uint32_t kw[4] = {b0[c].x, b0[c].y, b0[c].z, b0[c].w};
+          float *kk = c < 2 ? k0 : k1;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            kf[8 * c + 2 * i] = f16_to_f32(kw[i] & 0xFFFFu);
-            kf[8 * c + 2 * i + 1] = f16_to_f32(kw[i] >> 16);
+            kk[8 * (c & 1) + 2 * i] = f16_to_f32(kw[i] & 0xFFFFu);
+            kk[8 * (c & 1) + 2 * i + 1] = f16_to_f32(kw[i] >> 16);
           }
         }
-      }
-      float scl = 0.f;
-      if constexpr (KF) {
-        const uint32_t sw = (&sw4.x)[blk >> 1];
-        scl = f16_to_f32((blk & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-      }
+        const float *qb = qlane + 32 * blk;
 #pragma unroll
-      for (int r = 0; r < kPxRows; ++r) {
-        const int qi = min(r >> 2, qlast);
-        cfloat_p qr = qc + ((size_t)qi * a.nh + (r & 3)) * kHd + 32 * blk;
-        if constexpr (KF) {
-          float inner = 0.f;
-#pragma unroll
-          for (int e = 0; e < 32; ++e) inner = __builtin_fmaf(qr[e], kf[e], inner);
-          acc[r] = acc[r] + scl * inner;
-        } else {
+        for (int r = 0; r < kPxRows; ++r) {
           float x = acc[r];
-#pragma unroll
-          for (int e = 0; e < 32; ++e) x = __builtin_fmaf(qr[e], kf[e], x);
+          Dot16<16>::run(x, qb[r * kHd], k0);
+          Dot16<16>::run(x, qb[r * kHd + 16], k1);
           acc[r] = x;
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) { b0[c] = b1[c]; b1[c] = b2[c]; }
       }
     }
     float *dst = sc + (size_t)j * kPxRows;
@@ -595,16 +666,32 @@ __global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
   }
   __syncthreads();
 
+  PXTS(1);
   // ---------------------------------------------------------------- sweep 2: exp and serial sum
-  float *et = reinterpret_cast<float *>(s_big);   // [2][256][33]
+  float *et = reinterpret_cast<float *>(s_big);   // [2][256][ES]
   float sum = 0.f;
+  float4 vn[kPxRows / 4];
+  {
+    const float *src = sc + (size_t)tid * kPxRows;
+#pragma unroll
+    for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = *reinterpret_cast<const float4 *>(src + 4 * r4);
+  }
   for (int t = 0; t < ntile; ++t) {
     const uint32_t j = (uint32_t)(t * kPxTile + tid);
     float *src = sc + (size_t)j * kPxRows;
-    float *eb = et + (t & 1) * 256 * 33 + tid * 33;
+    float *eb = et + (t & 1) * 256 * ES + tid * ES;
+    float4 vc[kPxRows / 4];
+#pragma unroll
+    for (int r4 = 0; r4 < kPxRows / 4; ++r4) vc[r4] = vn[r4];
+    {
+      // the next tile's scores are in flight while this tile's exp runs
+      const float *nx = sc + (size_t)(min(t + 1, ntile - 1) * kPxTile + tid) * kPxRows;
+#pragma unroll
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = *reinterpret_cast<const float4 *>(nx + 4 * r4);
+    }
 #pragma unroll
     for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
-      const float4 v = *reinterpret_cast<const float4 *>(src + 4 * r4);
+      const float4 v = vc[r4];
       float4 e;
       e.x = exp_cr(v.x - s_m[4 * r4]);
       e.y = exp_cr(v.y - s_m[4 * r4 + 1]);
@@ -618,66 +705,76 @@ __global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
     }
     __syncthreads();
     if (tid < kPxRows) {
-      const float *col = et + (t & 1) * 256 * 33 + tid;
+      const float *col = et + (t & 1) * 256 * ES + tid;
 #pragma unroll 16
-      for (int k = 0; k < kPxTile; ++k) sum = sum + col[k * 33];
+      for (int k = 0; k < kPxTile; ++k) sum = sum + col[k * ES];
     }
   }
   if (tid < kPxRows) s_sum[tid] = (tid >> 2) < nqv ? sum : 1.0f;
   __syncthreads();
 
+  PXTS(2);
   // ---------------------------------------------------------------- sweep 3: p16 and PV
   const int lr = lane & 15, lq = lane >> 4, kp = lane & 31, vh = lane >> 5;
-  char *s_p = s_big;                                              // [2][32 rows][kPfRS]
+  char *s_p = s_big;                                              // [2][kPxRows][kPfRS]
   char *vt_hi = s_big + 2 * kPxRows * kPfRS + w * (VF ? 2 : 1) * 64 * kPfRS;
   char *vt_lo = vt_hi + (VF ? 64 * kPfRS : 0);
-  f4 o[4][2];
+  f4 o[4][NT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) o[mt][0] = o[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
   const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
+  const int pk = tid >> 2, pr0 = PR * (tid & 3);   // this thread's probabilities: key pk, rows pr0..+PR
+  float4 en[PR / 4];
+  VRaw<VF> vrn;
+  auto load_tile = [&](int t) {
+    const float *src = sc + ((size_t)t * kPfTile + pk) * kPxRows + pr0;
+#pragma unroll
+    for (int i = 0; i < PR / 4; ++i) en[i] = *reinterpret_cast<const float4 *>(src + 4 * i);
+    const uint32_t ka = min((uint32_t)(t * kPfTile + 2 * kp), kend - 1);
+    const uint32_t kb = min((uint32_t)(t * kPfTile + 2 * kp + 1), kend - 1);
+    load_v<VF, PG>(a.L, a.nkv, g, ka, kb, w, vh, vrn);
+  };
+  load_tile(0);
   for (int t = 0; t < nt64; ++t) {
     char *pb = s_p + (t & 1) * kPxRows * kPfRS;
-    {
-      const int k = tid >> 2, r0 = 8 * (tid & 3);
-      const float *src = sc + ((size_t)t * kPfTile + k) * kPxRows + r0;
-      const float4 e0 = *reinterpret_cast<const float4 *>(src);
-      const float4 e1 = *reinterpret_cast<const float4 *>(src + 4);
-      const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    float ev[PR];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const _Float16 h = (_Float16)(ev[i] / s_sum[r0 + i]);
-        *reinterpret_cast<_Float16 *>(pb + (r0 + i) * kPfRS + 2 * k) = h;
-      }
+    for (int i = 0; i < PR / 4; ++i) {
+      ev[4 * i] = en[i].x; ev[4 * i + 1] = en[i].y; ev[4 * i + 2] = en[i].z; ev[4 * i + 3] = en[i].w;
     }
-    {
-      VRaw<VF> vr;
-      const uint32_t ka = min((uint32_t)(t * kPfTile + 2 * kp), kend - 1);
-      const uint32_t kb = min((uint32_t)(t * kPfTile + 2 * kp + 1), kend - 1);
-      load_v<VF, PG>(a.L, a.nkv, g, ka, kb, w, vh, vr);
-      put_vt<VF>(vr, kp, vh, vt_hi, vt_lo);
+    const VRaw<VF> vr = vrn;
+    load_tile(min(t + 1, nt64 - 1));   // in flight during this tile
+#pragma unroll
+    for (int i = 0; i < PR; ++i) {
+      const _Float16 h = (_Float16)(ev[i] / s_sum[pr0 + i]);
+      *reinterpret_cast<_Float16 *>(pb + (pr0 + i) * kPfRS + 2 * pk) = h;
     }
+    put_vt<VF>(vr, kp, vh, vt_hi, vt_lo);
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      h8 bp[2];
+      h8 bp[NT];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NT; ++nt)
         bp[nt] = *reinterpret_cast<const h8 *>(pb + (16 * nt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const h8 ah = *reinterpret_cast<const h8 *>(vt_hi + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) o[mt][nt] = mfma16(ah, bp[nt], o[mt][nt]);
+        for (int nt = 0; nt < NT; ++nt) o[mt][nt] = mfma16(ah, bp[nt], o[mt][nt]);
         if constexpr (VF) {
           const h8 al = *reinterpret_cast<const h8 *>(vt_lo + (16 * mt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) o[mt][nt] = mfma16(al, bp[nt], o[mt][nt]);
+          for (int nt = 0; nt < NT; ++nt) o[mt][nt] = mfma16(al, bp[nt], o[mt][nt]);
         }
       }
     }
   }
+  PXTS(3);
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int r = 16 * nt + lr;
     if ((r >> 2) >= nqv) continue;
     const size_t row = (size_t)(q0 + (r >> 2)) * a.nh + g * kGqa + (r & 3);
@@ -699,14 +796,9 @@ __global__ __launch_bounds__(256) void prefill_exact_kernel(PrefillXArgs a) {
   }
 }
 
-hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, const float *q, hipStream_t st) {
+hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st) {
   const int grid = a.nkv * a.nqb;
   const bool pg = a.L.page != 0;
-  {
-    const size_t nq = (size_t)a.n_q * a.nh * kHd;
-    hipLaunchKernelGGL(q16_kernel, dim3((int)std::min<size_t>((nq + 255) / 256, 4096)), dim3(256), 0, st,
-                       q + (size_t)a.q_base * a.nh * kHd, const_cast<float *>(a.q16), nq);
-  }
   BKV_FMT_SWITCH(kf, vf, {
     if (pg) hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, true>), dim3(grid), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, false>), dim3(grid), dim3(256), 0, st, a);
