@@ -6,7 +6,11 @@ The cache is prefilled with seeded synthetic K/V (K ~ N(0,1) with 3 channels per
 scaled x8, V ~ N(0, 0.5) std, Q ~ N(0,1)) so that the timed steps attend over 32769..32768+K keys
 Inputs are resident in HBM before the timed region.
 
-    python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu]
+A second object on the same line, "prefill", times BASELINE config 5: 512 new q8_0 tokens appended
+onto an 8192-token cache, then causal GQA attention for the 512 queries over 8 layers
+(bkv_attn_prefill_chunk), on the exact path (the default) and on the MFMA-order variant.
+
+    python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu] [--no-prefill]
 """
 import argparse
 import ctypes
@@ -94,6 +98,82 @@ def cpu_baseline(ctx, seed=2):
             "host_gbs": algorithmic_bytes(n) / per_layer / 1e9}
 
 
+VALU_FMA_PEAK = 256 * 64 * 2.4e9     # fp32 FMA lane-ops/s without packed math (256 CUs, 64 lanes, 2.4 GHz)
+
+
+def prefill_flops(pos0, n_q, nh=16, hd=256):
+    """QK^T + PV flops of one layer's causal chunk: 2*2*hd per (row, visible key)."""
+    return 4 * hd * nh * sum(pos0 + i + 1 for i in range(n_q))
+
+
+def prefill_leg(cpu=True, reps=5):
+    """BASELINE config 5 on the GPU (exact path and the MFMA-order variant) and the CPU oracle on
+    a bounded sample (a few query rows, scaled to the chunk)."""
+    import torch
+    from bonsai_vk_amd import BKV_Q8_0, KvCache
+    pos0, n_q, L = 8192, 512, 8
+    n = pos0 + n_q
+    cache = KvCache(n_layers=L, cap=n, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    for layer in range(L):
+        k = torch.randn(n, 4, 256, generator=g, device="cuda")
+        v = torch.randn(n, 4, 256, generator=g, device="cuda") * 0.5
+        cache.append(layer, 0, k, v)
+    q = torch.randn(L, n_q, 16, 256, generator=g, device="cuda")
+
+    def run():
+        for layer in range(L):
+            cache.prefill_chunk(layer, pos0, q[layer])
+
+    res = {}
+    for mode in ("exact", "mfma"):
+        if mode == "mfma":
+            os.environ["BKV_PREFILL"] = "mfma"
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        res[mode] = e0.elapsed_time(e1) / reps * 1e3   # us per 8-layer chunk
+        os.environ.pop("BKV_PREFILL", None)
+    fl = L * prefill_flops(pos0, n_q)
+    # the exact path's score sweep: 16 rows x 34 tiles x 256 keys per workgroup, 272 lane-ops per
+    # (row, key) (256 serial fma, 8 scale mul + 8 add), over 512 workgroups per layer
+    score_ops = L * 512 * 16 * (34 * 256) * 272
+    out = {"workload": "bkv_attn_prefill_chunk x 8 layers: 512 q8_0 queries onto 8192 cached keys "
+                       "(BASELINE config 5)",
+           "unit": "us/chunk", "value": round(res["exact"], 1),
+           "us_per_layer": round(res["exact"] / L, 1),
+           "algorithmic_tflops": round(fl / (res["exact"] * 1e-6) / 1e12, 2),
+           "bound": "valu (serial fp32 fma chains of the exact scores)",
+           "score_fma_frac_of_valu_peak": round(score_ops / (res["exact"] * 1e-6) / VALU_FMA_PEAK, 3),
+           "mfma_variant": {"value": round(res["mfma"], 1), "unit": "us/chunk",
+                            "algorithmic_tflops": round(fl / (res["mfma"] * 1e-6) / 1e12, 1),
+                            "peak_tflops": 2500.0,
+                            "note": "scores and sums in MFMA order: not bit-identical probabilities"}}
+    if cpu:
+        import numpy as np
+        import oracle
+        cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+        host = oracle.HostCache(n_layers=1, cap=n, k_fmt=oracle.Q8_0, v_fmt=oracle.Q8_0)
+        kk, vv = oracle.synth_kv(n, 4, 256, 4, 0, outliers=0)
+        host.append(0, 0, kk, vv)
+        qh = oracle.normal(16 * 256, 4, 5).reshape(16, 256)
+        rows = [0, 255, 511]
+        t0 = time.perf_counter()
+        for i in rows:
+            host.decode(0, pos0 + i + 1, qh, nthreads=cores)
+        per_row = (time.perf_counter() - t0) / len(rows)
+        out["cpu_baseline"] = {"value": round(per_row * n_q * L * 1e6, 1), "unit": "us/chunk",
+                               "cores": cores, "kind": "port",
+                               "sample": f"oracle rows {rows} of one layer (16 heads each), x512 rows x8 layers"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +182,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill leg")
     ap.add_argument("--gate", action="store_true", help="also read the gate and write GOUT")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="after the timed region, copy a MIB MiB buffer once (a reference kernel for "
@@ -192,6 +273,10 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctx)
+    if not args.no_prefill:
+        del cache
+        torch.cuda.empty_cache()
+        line["prefill"] = prefill_leg(cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 
