@@ -62,12 +62,15 @@ static bool prefill_mfma_requested() {
   return e && std::strcmp(e, "mfma") == 0;
 }
 
-PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q) {
+// Prefill arrays start past every array a decode on the same workspace can use (the decode plan
+// at the cache's full capacity): the resident decode polls its partials for generation tags, so no
+// other path may leave bytes in that region.
+PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q, size_t base) {
   PrefillPlan p{};
   p.nqb = (int)cdiv(n_q, kPfQ);
   p.nsplit = prefill_splits(nkv, p.nqb, (int64_t)pos0 + std::min(n_q, kPfQ));
   const size_t rows = (size_t)n_q * nh;
-  size_t o = kSyncBytes;
+  size_t o = base;
   p.off_stats = o;
   o = align256(o + (size_t)p.nsplit * rows * sizeof(float2));
   p.off_part = o;
@@ -78,20 +81,20 @@ PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q) {
 
 // the exact prefill's workspace for chunks ending at or before max_ctx: per workgroup of one slice,
 // the [keys][rows] score / exp scratch
-size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx) {
+size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base) {
   (void)nh;
   const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile;
   const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
-  return kSyncBytes + align256(wgs * (size_t)ld * kPxRows * sizeof(float));
+  return base + align256(wgs * (size_t)ld * kPxRows * sizeof(float));
 }
 
 // the largest plan_prefill(...).total over every chunk length and start position
-size_t prefill_workspace_bound(int nh, int nkv) {
+size_t prefill_workspace_bound(int nh, int nkv, size_t base) {
   size_t worst = 0;
   for (int nqb = 1; nqb <= BKV_PREFILL_MAX_Q / kPfQ; ++nqb) {
     const int nsplit = (int)std::max<int64_t>(1, cdiv(kPfFill, (int64_t)nkv * nqb));
     const size_t rows = (size_t)nqb * kPfQ * nh;
-    size_t o = align256(kSyncBytes + (size_t)nsplit * rows * sizeof(float2));
+    size_t o = align256(base + (size_t)nsplit * rows * sizeof(float2));
     if (nsplit > 1) o = align256(o + (size_t)nsplit * rows * kHd * sizeof(float));
     worst = std::max(worst, o);
   }
@@ -236,6 +239,11 @@ static int check_kernels(const bkv_cache_desc *d) {
 
 static int64_t max_positions(const bkv_cache_desc *d) {
   return d->page_tokens > 0 ? (int64_t)d->max_pages * d->page_tokens : (int64_t)d->cap;
+}
+
+// where a prefill's own arrays begin: past the largest decode plan this cache allows
+static size_t prefill_base(const bkv_cache_desc *d) {
+  return align256(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_positions(d)).total);
 }
 
 static LayerView view(const bkv_cache_desc *d, int layer) {
@@ -417,10 +425,11 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
   if (gate && (!aligned16(gate) || !aligned16(out_gated))) return BKV_EALIGN;
   if (!workspace) return BKV_EWORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return BKV_EALIGN;
+  const size_t base = prefill_base(d);
   if (!prefill_mfma_requested() && n_q >= kPxMinQ) {
     // the exact kernel, in slices of at most kPxSlice queries
     const int64_t ld = cdiv((int64_t)pos0 + n_q, kPxTile) * kPxTile;
-    if (ws_bytes < prefill_exact_workspace(d->nh, d->nkv, (int64_t)pos0 + n_q)) return BKV_EWORKSPACE;
+    if (ws_bytes < prefill_exact_workspace(d->nh, d->nkv, (int64_t)pos0 + n_q, base)) return BKV_EWORKSPACE;
     char *w = (char *)workspace;
     PrefillXArgs a{};
     a.L = view(d, layer);
@@ -431,7 +440,7 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
     a.scale = d->scale;
     a.ld = ld;
     a.q = q;
-    a.sc = (float *)(w + kSyncBytes);
+    a.sc = (float *)(w + base);
     a.gate = gate;
     a.out = out;
     a.out_gated = out_gated;
@@ -458,7 +467,7 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
     }
     return BKV_OK;
   }
-  const PrefillPlan p = plan_prefill(d->nh, d->nkv, pos0, n_q);
+  const PrefillPlan p = plan_prefill(d->nh, d->nkv, pos0, n_q, base);
   if (ws_bytes < p.total) return BKV_EWORKSPACE;
   char *w = (char *)workspace;
   PrefillArgs a{};
@@ -482,9 +491,8 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
   if (check(d) || max_ctx == 0) return 0;
   if (op == BKV_OP_PREFILL)
-    return std::max({prefill_workspace_bound(d->nh, d->nkv),
-                     plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total,
-                     prefill_exact_workspace(d->nh, d->nkv, max_ctx)});
+    return std::max(prefill_workspace_bound(d->nh, d->nkv, prefill_base(d)),
+                    prefill_exact_workspace(d->nh, d->nkv, max_ctx, prefill_base(d)));
   if (op != BKV_OP_DECODE) return 0;
   return plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total;
 }

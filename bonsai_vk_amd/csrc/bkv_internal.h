@@ -180,8 +180,8 @@ struct PrefillPlan {
   int nqb, nsplit;
   size_t off_stats, off_part, total;
 };
-PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q);
-size_t prefill_workspace_bound(int nh, int nkv);
+PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q, size_t base);
+size_t prefill_workspace_bound(int nh, int nkv, size_t base);
 hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st);
 
 // ------------------------------------------------------------------ exact chunked prefill
@@ -207,7 +207,7 @@ struct PrefillXArgs {
   unsigned *ts;                  // sweep timestamps (experiment builds), or null
 };
 hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st);
-size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx);
+size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base);
 
 #define BKV_FMT_SWITCH(KF, VF, ...)                                                    \
   do {                                                                                \

@@ -1,8 +1,8 @@
-"""GPU parity of the MFMA chunked prefill (bkv_attn_prefill_chunk through the C ABI) against the CPU
+"""GPU parity of the chunked prefill (bkv_attn_prefill_chunk through the C ABI) against the CPU
 oracle, whose prefill is the decode row repeated per query (the reference's own prefill,
-runtime_vk/attn_vk.h:261-311 once per token). Bar: max relative error 1e-4 per head row
-(max |gpu - oracle| / max |oracle|); the matrix cores sum dot products, the softmax sum and PV in
-another order than the serial reference, so prefill is held to the tolerance, not to bit-exactness."""
+runtime_vk/attn_vk.h:261-311 once per token). The default path reproduces the serial scores, row
+max, softmax sum and fp16 probabilities bit for bit and sums PV on the matrix cores. Bar: max
+relative error 1e-4 per head row (max |gpu - oracle| / max |oracle|), bit-diff counts printed."""
 import numpy as np
 import pytest
 import torch
@@ -124,3 +124,31 @@ def test_prefill_errors():
         dev.prefill_chunk(0, 95, q)          # pos0 + n_q beyond the cache
     with pytest.raises(BkvError):
         dev.prefill_chunk(1, 0, q)           # no such layer
+
+
+def test_prefill_and_decode_share_a_workspace():
+    """The exact prefill's scratch lies past every array a decode can use, so decode calls (the
+    resident kernel polls its partials for generation tags) and short prefill chunks (decode rows)
+    on the same workspace stay correct after a prefill has filled its scratch."""
+    import ctypes
+    from bonsai_vk_amd import lib
+    from bonsai_vk_amd._lib import check
+    pos0, n_q = 700, 40
+    n = pos0 + n_q
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n, seed=21)
+    q, _ = qg(21, 0, n=n_q)
+    qd = torch.from_numpy(q).cuda()
+    ws = dev.prefill_workspace(n)
+    want, _ = host.prefill(0, pos0, q, None, nthreads=8)
+    for rep in range(3):
+        out, _ = dev.prefill_chunk(0, pos0, qd)
+        o = torch.empty((16, 256), device="cuda")
+        check(lib().bkv_attn_decode(ctypes.byref(dev.desc), 0, n, qd[-1].data_ptr(), None,
+                                    o.data_ptr(), None, ws.data_ptr(), ws.numel(), dev._stream()),
+              "bkv_attn_decode")
+        short, _ = dev.prefill_chunk(0, pos0 + 30, qd[30:35].contiguous())
+        torch.cuda.synchronize()
+        assert report(f"shared ws prefill rep {rep}", out.cpu().numpy(), want) <= TOL
+        assert report(f"shared ws decode rep {rep}", o.cpu().numpy(), want[-1]) <= TOL
+        assert report(f"shared ws short chunk rep {rep}", short.cpu().numpy(), want[30:35]) <= TOL
