@@ -200,6 +200,11 @@ class KvCache:
                                            self._stream()), "bkv_workspace_init")
         return self._pws
 
+    def fill_synthetic(self):
+        """bkv_kv_fill_synthetic: every slot of every layer holds the word 0x3C003C00 (the reference's
+        kv_fill_synthetic timing fixture, runtime_vk/bonsai_forward.h:1355-1370)."""
+        check(lib().bkv_kv_fill_synthetic(ctypes.byref(self.desc), self._stream()), "bkv_kv_fill_synthetic")
+
     def decode_path(self, nfill):
         """1: fused single launch, 0: split path"""
         return lib().bkv_decode_path(ctypes.byref(self.desc), nfill)

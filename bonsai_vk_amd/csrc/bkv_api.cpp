@@ -538,6 +538,24 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
   return hip_fail(launch_workspace_init((unsigned *)workspace, (int)(ws_bytes / sizeof(unsigned)), stream));
 }
 
+int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream) {
+  const int rc = check(d);
+  if (rc) return rc;
+  const size_t slots = (size_t)d->cap * d->nkv;
+  const size_t rows[4] = {slots * (size_t)row_bytes(d->k_fmt), slots * kScaleRowBytes,
+                          slots * (size_t)row_bytes(d->v_fmt), slots * kScaleRowBytes};
+  void *bases[4] = {d->k_data, d->k_scales, d->v_data, d->v_scales};
+  for (int i = 0; i < 4; ++i) {
+    if (!bases[i]) continue;
+    for (int l = 0; l < d->n_layers; ++l) {
+      unsigned *p = (unsigned *)((char *)bases[i] + (uint64_t)l * d->layer_stride_bytes[i]);
+      const hipError_t e = launch_fill_words(p, rows[i] / 4, 0x3C003C00u, stream);
+      if (e != hipSuccess) return hip_fail(e);
+    }
+  }
+  return BKV_OK;
+}
+
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill) {
   if (check(d) || nfill == 0) return -1;
   return choose_path(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill));

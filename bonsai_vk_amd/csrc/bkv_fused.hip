@@ -536,6 +536,17 @@ hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st) {
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void fill_words_kernel(unsigned *p, size_t n, unsigned value) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = value;
+}
+
+hipError_t launch_fill_words(unsigned *p, size_t nwords, unsigned value, hipStream_t st) {
+  if (nwords == 0) return hipSuccess;
+  const int blocks = (int)std::min<size_t>(4096, (nwords + 255) / 256);
+  hipLaunchKernelGGL(fill_words_kernel, dim3(blocks), dim3(256), 0, st, p, nwords, value);
+  return hipGetLastError();
+}
+
 template <int KF, int VF, bool FUSE>
 static int fused_capacity() {
   static int cap = -1;

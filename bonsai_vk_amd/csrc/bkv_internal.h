@@ -241,6 +241,7 @@ hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream
 int resident_max_workgroups(int kf, int vf);
 hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st);
 hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st);
+hipError_t launch_fill_words(unsigned *p, size_t nwords, unsigned value, hipStream_t st);
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);
 hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, const RedArgs &ra,
                          int kf, int vf, bool fuse, hipStream_t st);

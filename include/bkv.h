@@ -120,6 +120,13 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
  * once after allocating it; the caller must not write into the workspace afterwards. */
 int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
 
+/* Timing fixture: fill every slot of every layer's K data, K scales, V data and V scales with the
+ * 32-bit word 0x3C003C00 (fp16 1.0 in both halves: fp16 K/V = 1.0, q8_0 bytes 0 / 60 with scale
+ * 1.0), so that attention can be timed at any context without a prompt. Replaces kv_fill_synthetic
+ * (runtime_vk/bonsai_forward.h:1355-1370), which fills the whole KV arena with that word. A kernel,
+ * not a memset; stream-ordered. */
+int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream);
+
 /* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
  * single launch (one workgroup per CU, the default), 1 = the older fused single launch, 0 = the
  * four-launch split path; -1 = bad arguments. The environment variable BKV_DECODE = split | fused |

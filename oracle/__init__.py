@@ -167,6 +167,7 @@ class HostCache:
                  page_tokens=0, max_pages=0, block_table=None, scale=None, rhaz=0):
         self.n_layers, self.nh, self.nkv, self.hd, self.cap = n_layers, nh, nkv, hd, cap
         self.k_fmt, self.v_fmt, self.rhaz = k_fmt, v_fmt, rhaz
+        self.page_tokens, self.max_pages = page_tokens, max_pages
         rowb = lambda f: nkv * hd * (2 if f == F16 else 1)
         srow = nkv * (hd // 32) * 2
         self.k_data = np.zeros((n_layers, cap, rowb(k_fmt)), np.uint8)
@@ -193,6 +194,13 @@ class HostCache:
         for mine, theirs in zip(self.arrays(), arrs):
             if mine is not None:
                 mine[...] = np.asarray(theirs)
+
+    def fill_synthetic(self):
+        """The reference's timing fixture (runtime_vk/bonsai_forward.h:1355-1370): the whole KV arena
+        filled with the word 0x3C003C00 (fp16 1.0 pairs; q8_0 bytes 0/60 with fp16 scale 1.0)."""
+        for a in self.arrays():
+            if a is not None:
+                a.view(np.uint32)[...] = 0x3C003C00
 
     def slot(self, layer, pos):
         return lib().bko_slot(ctypes.byref(self.desc), layer, pos)

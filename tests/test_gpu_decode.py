@@ -221,3 +221,26 @@ def test_decode_path_selection(monkeypatch):
     for name, code in PATHS.items():
         monkeypatch.setenv("BKV_DECODE", name)
         assert dev.decode_path(32769) == code
+
+
+def test_fill_synthetic_and_dump(path):
+    """bkv_kv_fill_synthetic leaves the reference's fixture bytes (0x3C003C00 everywhere) in every
+    layer, decode over them matches the oracle's decode of the same fixture, and the TSV dump of the
+    device cache equals the host cache's dump (kv_dump format) after real appends on top."""
+    from bonsai_vk_amd import kvdump
+    n = 600
+    dev, host = pair(2, n, BKV_Q8_0, BKV_Q8_0)
+    dev.fill_synthetic()
+    host.fill_synthetic()
+    torch.cuda.synchronize()
+    assert same_bytes(dev, host) == [0] * len(same_bytes(dev, host))
+    q, g = qg(31, 1)
+    want, _ = host.decode(1, n, q, nthreads=8)
+    out, _ = dev.decode(1, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    assert report("synthetic fill", out.cpu().numpy(), want) <= TOL
+    k, v = oracle.synth_kv(40, 4, 256, 32, 0, outliers=3)
+    host.append(0, 5, k, v)
+    dev.append(0, 5, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    torch.cuda.synchronize()
+    assert kvdump.dump_cache(dev, 0, 60) == kvdump.dump_cache(host, 0, 60)
