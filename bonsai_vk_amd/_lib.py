@@ -22,7 +22,7 @@ EXPORTS = [
     "bkv_geom_check", "bkv_slot_bytes", "bkv_max_positions", "bkv_kv_append", "bkv_attn_decode",
     "bkv_decode_step", "bkv_attn_prefill_chunk", "bkv_workspace_bytes", "bkv_strerror",
     "bkv_last_hip_error", "bkv_version", "bkv_debug_layout", "bkv_workspace_init", "bkv_decode_path",
-    "bkv_kv_fill_synthetic",
+    "bkv_kv_fill_synthetic", "bkv_attn_decode_qg", "bkv_decode_step_qg", "bkv_attn_prefill_chunk_qg",
 ]
 
 
@@ -78,6 +78,9 @@ def lib():
         "bkv_workspace_init": (i32, [D, P, sz, P]),
         "bkv_decode_path": (i32, [D, u32]),
         "bkv_kv_fill_synthetic": (i32, [D, P]),
+        "bkv_attn_decode_qg": (i32, [D, i32, u32, P, P, P, P, sz, P]),
+        "bkv_decode_step_qg": (i32, [D, i32, u32, P, P, P, P, P, P, sz, P]),
+        "bkv_attn_prefill_chunk_qg": (i32, [D, i32, u32, i32, P, P, P, P, sz, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -200,6 +200,41 @@ class KvCache:
                                            self._stream()), "bkv_workspace_init")
         return self._pws
 
+    def decode_qg(self, layer, nfill, qg, gated=True):
+        """bkv_attn_decode_qg: q and gate from the interleaved attn_q output [nh][2*hd]."""
+        qg = self._f32(qg, (self.nh, 2 * self.hd))
+        out = torch.empty((self.nh, self.hd), dtype=torch.float32, device=self.device)
+        og = torch.empty_like(out) if gated else None
+        check(lib().bkv_attn_decode_qg(ctypes.byref(self.desc), layer, nfill, qg.data_ptr(), out.data_ptr(),
+                                       self._ptr(og), self.workspace.data_ptr(), self.workspace.numel(),
+                                       self._stream()), "bkv_attn_decode_qg")
+        return out, og
+
+    def decode_step_qg(self, layer, pos, k, v, qg, gated=True):
+        """bkv_decode_step_qg: append the token, then attention with the interleaved q/gate rows."""
+        k = self._f32(k, (1, self.nkv, self.hd))
+        v = self._f32(v, (1, self.nkv, self.hd))
+        qg = self._f32(qg, (self.nh, 2 * self.hd))
+        out = torch.empty((self.nh, self.hd), dtype=torch.float32, device=self.device)
+        og = torch.empty_like(out) if gated else None
+        check(lib().bkv_decode_step_qg(ctypes.byref(self.desc), layer, pos, k.data_ptr(), v.data_ptr(),
+                                       qg.data_ptr(), out.data_ptr(), self._ptr(og),
+                                       self.workspace.data_ptr(), self.workspace.numel(), self._stream()),
+              "bkv_decode_step_qg")
+        return out, og
+
+    def prefill_chunk_qg(self, layer, pos0, qg, gated=True):
+        """bkv_attn_prefill_chunk_qg: qg [n][nh][2*hd]."""
+        n = qg.shape[0]
+        qg = self._f32(qg, (n, self.nh, 2 * self.hd))
+        out = torch.empty((n, self.nh, self.hd), dtype=torch.float32, device=self.device)
+        og = torch.empty_like(out) if gated else None
+        ws = self.prefill_workspace(pos0 + n)
+        check(lib().bkv_attn_prefill_chunk_qg(ctypes.byref(self.desc), layer, pos0, n, qg.data_ptr(),
+                                              out.data_ptr(), self._ptr(og), ws.data_ptr(), ws.numel(),
+                                              self._stream()), "bkv_attn_prefill_chunk_qg")
+        return out, og
+
     def fill_synthetic(self):
         """bkv_kv_fill_synthetic: every slot of every layer holds the word 0x3C003C00 (the reference's
         kv_fill_synthetic timing fixture, runtime_vk/bonsai_forward.h:1355-1370)."""

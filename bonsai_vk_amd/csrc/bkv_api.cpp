@@ -260,9 +260,11 @@ static LayerView view(const bkv_cache_desc *d, int layer) {
   return L;
 }
 
+// q / gate: head rows qs / gs floats apart (hd for [nh][hd]; 2*hd for the engine's interleaved
+// attn_q output, q then gate per head)
 static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
                          const float *gate, float *out, float *out_gated, void *ws, size_t ws_bytes,
-                         hipStream_t st, const AppendArgs *fused) {
+                         hipStream_t st, const AppendArgs *fused, int qs = kHd, int gs = kHd) {
   int rc = check(d);
   if (rc) return rc;
   if ((rc = check_kernels(d))) return rc;
@@ -282,7 +284,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if (path == kPathResident) {
     ResArgs ra{};
     ra.L = L; ra.nkv = d->nkv; ra.nh = d->nh; ra.nfill = nfill; ra.scale = d->scale;
-    ra.G = p.rG; ra.kpw = p.rkpw; ra.ld = p.ld; ra.q = q;
+    ra.G = p.rG; ra.kpw = p.rkpw; ra.ld = p.ld; ra.q = q; ra.qs = qs; ra.gs = gs;
     if (fused) ra.ap = *fused;
     ra.gate = gate; ra.out = out; ra.out_gated = out_gated;
     ra.tstats = (unsigned long long *)(w + kResTagOffset);
@@ -302,7 +304,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if (path == kPathFused) {
     FusedArgs fa{};
     fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub; fa.kpw = p.kpw;
-    fa.ld = p.ld; fa.q = q;
+    fa.ld = p.ld; fa.q = q; fa.qs = qs; fa.gs = gs;
     if (fused) fa.ap = *fused;
     fa.gate = gate; fa.out = out; fa.out_gated = out_gated;
     fa.stats = (float2 *)(w + p.f_stats);
@@ -324,6 +326,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   QkArgs qa{};
   qa.L = L; qa.nkv = d->nkv; qa.nfill = nfill; qa.nch = p.nch_qk; qa.ld = p.ld; qa.scale = d->scale;
   qa.q = q;
+  qa.qs = qs;
   qa.score = (float *)(w + p.off_score);
   qa.stats = (float2 *)(w + p.off_stats);
   qa.counters = (unsigned *)(w + p.off_cnt);
@@ -343,7 +346,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   pa.nch = p.nch_pv; pa.ld = p.ld; pa.e = ea.e; pa.sum = ea.sum;
   pa.part = (float *)(w + p.off_part);
   RedArgs ra{};
-  ra.nh = d->nh; ra.nch = p.nch_pv; ra.part = pa.part; ra.gate = gate; ra.out = out;
+  ra.nh = d->nh; ra.nch = p.nch_pv; ra.part = pa.part; ra.gate = gate; ra.gs = gs; ra.out = out;
   ra.out_gated = out_gated;
   return hip_fail(launch_decode(qa, ea, pa, ra, d->k_fmt, d->v_fmt, fused != nullptr, st));
 }
@@ -392,9 +395,10 @@ int bkv_attn_decode(const bkv_cache_desc *d, int layer, uint32_t nfill, const fl
                        nullptr);
 }
 
-int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
-                    const float *v, const float *q, const float *gate, float *out,
-                    float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream) {
+static int decode_step_common(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
+                              const float *v, const float *q, const float *gate, float *out,
+                              float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream,
+                              int qs, int gs) {
   int rc = check(d);
   if (rc) return rc;
   if (layer < 0 || layer >= d->n_layers) return BKV_EINVAL;
@@ -407,12 +411,38 @@ int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos, const floa
   a.pos = pos;
   a.k = k;
   a.v = v;
-  return decode_common(d, layer, pos + 1, q, gate, out, out_gated, workspace, ws_bytes, stream, &a);
+  return decode_common(d, layer, pos + 1, q, gate, out, out_gated, workspace, ws_bytes, stream, &a,
+                       qs, gs);
 }
 
-int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
-                           const float *q, const float *gate, float *out, float *out_gated,
-                           void *workspace, size_t ws_bytes, hipStream_t stream) {
+int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
+                    const float *v, const float *q, const float *gate, float *out,
+                    float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  return decode_step_common(d, layer, pos, k, v, q, gate, out, out_gated, workspace, ws_bytes,
+                            stream, kHd, kHd);
+}
+
+// the _qg variants read Q and the gate from the engine's attn_q output: per head, hd values of q
+// then hd values of the gate (the layout deint_qg splits, runtime_vk/shaders/deint_qg.comp)
+int bkv_attn_decode_qg(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *qg,
+                       float *out, float *out_gated, void *workspace, size_t ws_bytes,
+                       hipStream_t stream) {
+  if (!qg) return BKV_EINVAL;
+  return decode_common(d, layer, nfill, qg, out_gated ? qg + kHd : nullptr, out, out_gated,
+                       workspace, ws_bytes, stream, nullptr, 2 * kHd, 2 * kHd);
+}
+
+int bkv_decode_step_qg(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
+                       const float *v, const float *qg, float *out, float *out_gated,
+                       void *workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!qg) return BKV_EINVAL;
+  return decode_step_common(d, layer, pos, k, v, qg, out_gated ? qg + kHd : nullptr, out, out_gated,
+                            workspace, ws_bytes, stream, 2 * kHd, 2 * kHd);
+}
+
+static int prefill_common(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                          const float *q, const float *gate, float *out, float *out_gated,
+                          void *workspace, size_t ws_bytes, hipStream_t stream, int qs, int gs) {
   int rc = check(d);
   if (rc) return rc;
   if ((rc = check_kernels(d))) return rc;
@@ -440,6 +470,8 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
     a.scale = d->scale;
     a.ld = ld;
     a.q = q;
+    a.qs = qs;
+    a.gs = gs;
     a.sc = (float *)(w + base);
     a.gate = gate;
     a.out = out;
@@ -459,10 +491,10 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
     // short chunks: every row is the decode row at nfill = pos0 + i + 1
     const size_t rs = (size_t)d->nh * d->hd;
     for (int i = 0; i < n_q; ++i) {
-      rc = decode_common(d, layer, pos0 + (uint32_t)i + 1u, q + i * rs,
-                         gate ? gate + i * rs : nullptr, out + i * rs,
+      rc = decode_common(d, layer, pos0 + (uint32_t)i + 1u, q + i * (size_t)d->nh * qs,
+                         gate ? gate + i * (size_t)d->nh * gs : nullptr, out + i * rs,
                          out_gated ? out_gated + i * rs : nullptr, workspace, ws_bytes, stream,
-                         nullptr);
+                         nullptr, qs, gs);
       if (rc) return rc;
     }
     return BKV_OK;
@@ -485,7 +517,24 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
   a.out_gated = out_gated;
   a.stats = (float2 *)(w + p.off_stats);
   a.part = p.nsplit > 1 ? (float *)(w + p.off_part) : nullptr;
+  a.qs = qs;
+  a.gs = gs;
   return hip_fail(launch_prefill(a, d->k_fmt, d->v_fmt, stream));
+}
+
+int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                           const float *q, const float *gate, float *out, float *out_gated,
+                           void *workspace, size_t ws_bytes, hipStream_t stream) {
+  return prefill_common(d, layer, pos0, n_q, q, gate, out, out_gated, workspace, ws_bytes, stream,
+                        kHd, kHd);
+}
+
+int bkv_attn_prefill_chunk_qg(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                              const float *qg, float *out, float *out_gated, void *workspace,
+                              size_t ws_bytes, hipStream_t stream) {
+  if (!qg) return BKV_EINVAL;
+  return prefill_common(d, layer, pos0, n_q, qg, out_gated ? qg + kHd : nullptr, out, out_gated,
+                        workspace, ws_bytes, stream, 2 * kHd, 2 * kHd);
 }
 
 size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {

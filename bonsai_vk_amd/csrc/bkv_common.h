@@ -111,6 +111,12 @@ __device__ __forceinline__ int64_t slot_t(const LayerView &L, int64_t pos) {
   }
 }
 
+// element oi = head*hd + d of an [nh][hd] output, in a gate array whose head rows are gs floats
+// apart (hd: contiguous; 2*hd: the q/gate interleave of the engine's attn_q output)
+__host__ __device__ __forceinline__ size_t gate_index(size_t oi, int gs) {
+  return oi + (oi / kHd) * (size_t)(gs - kHd);
+}
+
 // bytes of one head row of the data array, per format
 __host__ __device__ constexpr int row_bytes(int fmt) { return fmt == BKV_F16 ? kHd * 2 : kHd; }
 // bytes of one head row of the scale array (q8_0 only)

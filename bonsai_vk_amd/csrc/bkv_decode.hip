@@ -50,7 +50,7 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
   stage_rows<NT, T::KEYS, T::DPR, T::UPR>(tile, L.kd, RB, L, a.nkv, g, j0, n);
   if (KF == BKV_Q8_0) stage_rows<NT, T::KEYS, 1, T::UPR>(tile + 16, L.ks, kScaleRowBytes, L, a.nkv, g, j0, n);
   float qv[kGqa][kHd / 16];
-  load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
+  load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
   __syncthreads();
   asm volatile("s_nop 4");      // DPP source registers written above: VALU-write -> DPP-read gap
 
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256) void merge_kernel(RedArgs a) {
     const float v = (s[0][tid] + s[1][tid]) + (s[2][tid] + s[3][tid]);
     const size_t o = (size_t)h * kHd + d;
     a.out[o] = v;
-    if (a.gate) a.out_gated[o] = v * (1.0f / (1.0f + exp_cr(-a.gate[o])));
+    if (a.gate) a.out_gated[o] = v * (1.0f / (1.0f + exp_cr(-a.gate[gate_index(o, a.gs)])));
   }
 }
 

@@ -103,13 +103,14 @@ struct Dot16<0> {
 };
 
 // The group's 4 query rows rounded to fp16 (the reference's Q16 operand), laid out for fmac_bc:
-// qv[h][j] holds q16[h][16j + lane%16] in every DPP row. q: the group's first row, [4][hd] fp32.
-__device__ __forceinline__ void load_q16_rows(const float *q, float (&qv)[kGqa][kHd / 16]) {
+// qv[h][j] holds q16[h][16j + lane%16] in every DPP row. q: the group's first row, rows qs floats
+// apart (hd for [nh][hd], 2*hd for the engine's interleaved q/gate rows).
+__device__ __forceinline__ void load_q16_rows(const float *q, float (&qv)[kGqa][kHd / 16], int qs = kHd) {
   const float *qg = q + (threadIdx.x & 15);
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
-    for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qg[h * kHd + 16 * j]);
+    for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qg[(size_t)h * qs + 16 * j]);
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll

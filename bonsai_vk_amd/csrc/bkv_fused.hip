@@ -145,7 +145,7 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
 
   // ---------------------------------------------------------------- QK
   float qv[kGqa][kHd / 16];
-  load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
+  load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
   float sc[kRMax][kGqa];
   float mloc[kGqa];
 #pragma unroll
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(FusedCfg<KF>::NT, FusedCfg<KF>::MINB) void fused_ke
             const float2 v = acc2[i];
             *reinterpret_cast<float2 *>(a.out + oi) = v;
             if (a.gate) {
-              const float2 gt = *reinterpret_cast<const float2 *>(a.gate + oi);
+              const float2 gt = *reinterpret_cast<const float2 *>(a.gate + gate_index(oi, a.gs));
               *reinterpret_cast<float2 *>(a.out_gated + oi) =
                   make_float2(v.x * (1.0f / (1.0f + exp_cr(-gt.x))), v.y * (1.0f / (1.0f + exp_cr(-gt.y))));
             }

@@ -46,7 +46,8 @@ struct QkArgs {
   int nch;                       // QK partitions
   int64_t ld;                    // row stride of score / e (floats)
   float scale;
-  const float *q;                // [nh][hd] fp32
+  const float *q;                // [nh][hd] fp32, head rows qs floats apart
+  int qs;
   float *score;                  // [nh][ld]
   float2 *stats;                 // [nh][nch] (partition max of s*scale, sum exp(s*scale - max))
   unsigned *counters;            // [nh] arrivals of the probability kernel (zeroed here)
@@ -84,7 +85,8 @@ struct PvArgs {
 struct RedArgs {
   int nh, nch;
   const float *part;
-  const float *gate;
+  const float *gate;             // head rows gs floats apart
+  int gs;
   float *out, *out_gated;
 };
 
@@ -106,9 +108,10 @@ struct FusedArgs {
   int gg, rsub;                  // workgroups per KV group, 256-key sub-chunks per workgroup
   int kpw;                       // keys per workgroup (the last one may hold fewer)
   int64_t ld;
-  const float *q;                // [nh][hd]
+  const float *q;                // [nh][hd], head rows qs floats apart
   AppendArgs ap;
-  const float *gate;
+  const float *gate;             // head rows gs floats apart
+  int qs, gs;
   float *out, *out_gated;
   float2 *stats;                 // [nh][gg]
   unsigned *mxenc;               // [2][nh] running max (order-preserving bits), by call parity
@@ -142,9 +145,10 @@ struct ResArgs {
   float scale;
   int G, kpw;                    // workgroups per KV group, keys per workgroup
   int64_t ld;
-  const float *q;                // [nh][hd]
+  const float *q;                // [nh][hd], head rows qs floats apart
   AppendArgs ap;                 // decode_step: the token to append first (ap.k null: none)
-  const float *gate;
+  const float *gate;             // head rows gs floats apart
+  int qs, gs;
   float *out, *out_gated;
   unsigned long long *tstats;    // [nh][kResMaxGroupWgs] tagged (max, sum exp) per workgroup
   unsigned long long *trec;      // [nh][kResMaxGroupWgs][2] tagged chunk records
@@ -170,7 +174,8 @@ struct PrefillArgs {
   int n_q;
   float scale;
   int nqb, nsplit;               // query blocks, key splits per query block
-  const float *q, *gate;         // [n_q][nh][hd]
+  const float *q, *gate;         // [n_q][nh] rows, qs / gs floats apart
+  int qs, gs;
   float *out, *out_gated;
   float2 *stats;                 // [nsplit][n_q][nh] (max, sum exp) of the split's keys
   float *part;                   // [nsplit][n_q][nh][hd] normalised partial outputs (nsplit > 1)
@@ -200,8 +205,9 @@ struct PrefillXArgs {
   float scale;
   int nqb;
   int64_t ld;                    // keys per workgroup scratch region (multiple of kPxTile)
-  const float *q;                // [chunk_q][nh][hd] fp32
-  const float *gate;
+  const float *q;                // [chunk_q][nh] rows of hd fp32, qs floats apart
+  const float *gate;             // rows gs floats apart
+  int qs, gs;
   float *out, *out_gated;
   float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp (the slice's workgroups)
   unsigned *ts;                  // sweep timestamps (experiment builds), or null

@@ -100,7 +100,7 @@ __device__ __forceinline__ void load_q(const PrefillArgs &a, const PfGeo &p, int
   for (int nt = 0; nt < 4; ++nt) {
     const int r = 16 * nt + lr;
     const int qi = min(p.q0 + (r >> 2), a.n_q - 1);
-    const float *qp = a.q + ((size_t)qi * a.nh + (size_t)(p.g * kGqa + (r & 3))) * kHd + 64 * lq;
+    const float *qp = a.q + ((size_t)qi * a.nh + (size_t)(p.g * kGqa + (r & 3))) * a.qs + 64 * lq;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const float4 x0 = *reinterpret_cast<const float4 *>(qp + 8 * s);
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(kPfNT) void prefill_pv_kernel(PrefillArgs a) {
       } else {
         *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
         if (a.gate) {
-          const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * kHd + d);
+          const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * a.gs + d);
           float4 og;
           og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
           og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
@@ -440,7 +440,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     }
     reinterpret_cast<float4 *>(a.out)[i] = v;
     if (a.gate) {
-      const float4 gt = reinterpret_cast<const float4 *>(a.gate)[i];
+      const float4 gt = *reinterpret_cast<const float4 *>(a.gate + gate_index(4 * i, a.gs));
       float4 og;
       og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
       og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     for (int i = tid; i < kPxRows * kHd / 4; i += 256) {
       const int r = i / (kHd / 4), d4 = i % (kHd / 4);
       const int qi = min(q0 + (r >> 2), qlast);
-      const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * kHd + 4 * d4);
+      const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * a.qs + 4 * d4);
       *reinterpret_cast<float4 *>(s_q + r * kHd + 4 * d4) =
           make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
     }
@@ -784,7 +784,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       const float4 v = make_float4(o[mt][nt][0], o[mt][nt][1], o[mt][nt][2], o[mt][nt][3]);
       *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
       if (a.gate) {
-        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * kHd + d);
+        const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * a.gs + d);
         float4 og;
         og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
         og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));

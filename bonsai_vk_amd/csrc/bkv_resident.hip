@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 
   // ---------------------------------------------------------------- QK
   float qv[kGqa][kHd / 16];
-  load_q16_rows(a.q + (size_t)g * kGqa * kHd, qv);
+  load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
   asm volatile("s_nop 4");
 
   const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   float sct = 0.0f;
   if (TAIL && tn > 0 && wave == 0) {
     float qt[kHd / 16];
-    const float *qh = a.q + ((size_t)g * kGqa + th) * kHd + tt;
+    const float *qh = a.q + ((size_t)g * kGqa + th) * a.qs + tt;
 #pragma unroll
     for (int j = 0; j < kHd / 16; ++j) qt[j] = round_f16(qh[16 * j]);
 #pragma unroll
@@ -1098,7 +1098,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         const int eg = e0 + c0 + tid;
         const size_t oi = (size_t)g * E + eg;           // out is [nh][hd], head g*kGqa + eg/hd
         a.out[oi] = v;
-        if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[oi])));
+        if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[gate_index(oi, a.gs)])));
       }
       __syncthreads();
     }

@@ -127,6 +127,22 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
  * not a memset; stream-ordered. */
 int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream);
 
+/* Q and the gate straight from the engine's attn_q output, qg = [nh][2*hd] per query: head h's
+ * hd query values, then its hd gate values (the per-head interleave that deint_qg splits,
+ * runtime_vk/shaders/deint_qg.comp:1-45, before attn_qk_softmax and attn_pv_q8v read q and the gate,
+ * attn_pv_q8v.comp:112). Same results as bkv_attn_decode / bkv_decode_step /
+ * bkv_attn_prefill_chunk given the de-interleaved q and gate; out_gated may be NULL (then the gate
+ * is not read). For the prefill, qg is [n_q][nh][2*hd]. */
+int bkv_attn_decode_qg(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *qg,
+                       float *out, float *out_gated, void *workspace, size_t ws_bytes,
+                       hipStream_t stream);
+int bkv_decode_step_qg(const bkv_cache_desc *d, int layer, uint32_t pos, const float *k,
+                       const float *v, const float *qg, float *out, float *out_gated,
+                       void *workspace, size_t ws_bytes, hipStream_t stream);
+int bkv_attn_prefill_chunk_qg(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
+                              const float *qg, float *out, float *out_gated, void *workspace,
+                              size_t ws_bytes, hipStream_t stream);
+
 /* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
  * single launch (one workgroup per CU, the default), 1 = the older fused single launch, 0 = the
  * four-launch split path; -1 = bad arguments. The environment variable BKV_DECODE = split | fused |

@@ -244,3 +244,40 @@ def test_fill_synthetic_and_dump(path):
     dev.append(0, 5, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
     torch.cuda.synchronize()
     assert kvdump.dump_cache(dev, 0, 60) == kvdump.dump_cache(host, 0, 60)
+
+
+def test_interleaved_qg_entry_points(path, monkeypatch):
+    """bkv_attn_decode_qg / bkv_decode_step_qg read q and the gate from the engine's interleaved
+    attn_q output (per head: 256 q then 256 gate, the layout deint_qg splits); results equal the
+    de-interleaved calls bit for bit, gated output included."""
+    monkeypatch.setenv("BKV_KEEP_INTERMEDIATES", "0")
+    n = 2000
+    dev, host = pair(1, n + 2, BKV_Q8_0, BKV_Q8_0)
+    twin, _ = pair(1, n + 2, BKV_Q8_0, BKV_Q8_0)
+    k, v = fill(dev, host, 0, n, seed=41)
+    twin.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    q, g = qg(41, 0)
+    qd, gd = torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda()
+    inter = torch.cat([qd, gd], dim=1).contiguous()          # [16][512]: q then gate per head
+    a, ag = dev.decode(0, n, qd, gd)
+    b, bg = dev.decode_qg(0, n, inter)
+    c, cg = dev.decode_qg(0, n, inter, gated=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(ag, bg) and torch.equal(a, c) and cg is None
+    kn, vn = oracle.synth_kv(1, 4, 256, 42, 0, outliers=3)
+    kd, vd = torch.from_numpy(kn).cuda(), torch.from_numpy(vn).cuda()
+    s1, s1g = dev.decode_step(0, n, kd, vd, qd, gd)
+    s2, s2g = twin.decode_step_qg(0, n, kd, vd, inter)
+    torch.cuda.synchronize()
+    assert torch.equal(s1, s2) and torch.equal(s1g, s2g)
+    assert not any(same_bytes(dev, oracle_like(twin)))
+    want, wg = host.decode(0, n, q, g, nthreads=8)
+    assert report("qg", b.cpu().numpy(), want) <= TOL
+
+
+def oracle_like(cache):
+    """the device arrays of another device cache, shaped like an oracle HostCache for same_bytes"""
+    class _H:
+        def arrays(self):
+            return [None if a is None else a.numpy() for a in cache.host_arrays()]
+    return _H()

@@ -152,3 +152,23 @@ def test_prefill_and_decode_share_a_workspace():
         assert report(f"shared ws prefill rep {rep}", out.cpu().numpy(), want) <= TOL
         assert report(f"shared ws decode rep {rep}", o.cpu().numpy(), want[-1]) <= TOL
         assert report(f"shared ws short chunk rep {rep}", short.cpu().numpy(), want[30:35]) <= TOL
+
+
+@pytest.mark.parametrize("mode", ["exact", "mfma"])
+@pytest.mark.parametrize("n_q", [5, 40])
+def test_prefill_interleaved_qg(mode, n_q, monkeypatch):
+    """bkv_attn_prefill_chunk_qg reads q and the gate from [n][nh][2*hd] rows (q then gate per head)
+    and equals the de-interleaved call bit for bit, on the exact path (and its decode-row path for
+    short chunks) and on the MFMA-order variant."""
+    if mode == "mfma":
+        monkeypatch.setenv("BKV_PREFILL", "mfma")
+    pos0 = 300
+    dev, host = pair(1, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, pos0 + n_q, seed=43)
+    q, g = qg(43, 0, n=n_q)
+    qd, gd = torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda()
+    inter = torch.cat([qd, gd], dim=2).contiguous()
+    a, ag = dev.prefill_chunk(0, pos0, qd, gd)
+    b, bg = dev.prefill_chunk_qg(0, pos0, inter)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(ag, bg)
