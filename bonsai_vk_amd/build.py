@@ -9,7 +9,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbkv.so")
-SOURCES = ["bkv_api.cpp", "bkv_decode.hip", "bkv_fused.hip", "bkv_resident.hip", "bkv_prefill.hip"]
+SOURCES = ["bkv_api.cpp", "bkv_decode.hip", "bkv_fused.hip", "bkv_resident.hip", "bkv_prefill.hip", "bkv_norm_rope.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -192,6 +192,39 @@ class KvCache:
               "bkv_attn_prefill_chunk")
         return out, out_gated
 
+    def norm_rope_append(self, layer, pos0, q_in, k_in, v_in, qn_w, kn_w, nrot=64, eps=1e-6,
+                         freq_base=1e7):
+        """bkv_qk_norm_rope_append: K normed + roped and V appended at pos0..; returns the roped Q."""
+        n = q_in.shape[0]
+        q_in = self._f32(q_in, (n, self.nh, self.hd))
+        k_in = self._f32(k_in, (n, self.nkv, self.hd))
+        v_in = self._f32(v_in, (n, self.nkv, self.hd))
+        qn_w = self._f32(qn_w, (self.hd,))
+        kn_w = self._f32(kn_w, (self.hd,))
+        q_out = torch.empty_like(q_in)
+        check(lib().bkv_qk_norm_rope_append(ctypes.byref(self.desc), layer, pos0, n, q_in.data_ptr(),
+                                            k_in.data_ptr(), v_in.data_ptr(), qn_w.data_ptr(),
+                                            kn_w.data_ptr(), nrot, eps, freq_base, q_out.data_ptr(),
+                                            self._stream()), "bkv_qk_norm_rope_append")
+        return q_out
+
+    def prefill_step(self, layer, pos0, k, v, q, gate=None):
+        """bkv_prefill_step: append the chunk's K/V (q8_0 / fp16 on write), then its causal attention."""
+        n = q.shape[0]
+        k = self._f32(k, (n, self.nkv, self.hd))
+        v = self._f32(v, (n, self.nkv, self.hd))
+        q = self._f32(q, (n, self.nh, self.hd))
+        out = torch.empty((n, self.nh, self.hd), dtype=torch.float32, device=self.device)
+        out_gated = None
+        if gate is not None:
+            gate = self._f32(gate, (n, self.nh, self.hd))
+            out_gated = torch.empty_like(out)
+        ws = self.prefill_workspace(pos0 + n)
+        check(lib().bkv_prefill_step(ctypes.byref(self.desc), layer, pos0, n, k.data_ptr(), v.data_ptr(),
+                                     q.data_ptr(), self._ptr(gate), out.data_ptr(), self._ptr(out_gated),
+                                     ws.data_ptr(), ws.numel(), self._stream()), "bkv_prefill_step")
+        return out, out_gated
+
     def prefill_workspace(self, max_ctx):
         need = lib().bkv_workspace_bytes(ctypes.byref(self.desc), BKV_OP_PREFILL, max_ctx)
         if getattr(self, "_pws", None) is None or self._pws.numel() < need:

@@ -388,6 +388,37 @@ int bkv_kv_append(const bkv_cache_desc *d, int layer, uint32_t pos, int n_tok, c
   return hip_fail(launch_append(a, d->k_fmt, d->v_fmt, n_tok, stream));
 }
 
+int bkv_qk_norm_rope_append(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_tok,
+                            const float *q_in, const float *k_in, const float *v_in,
+                            const float *qn_w, const float *kn_w, int nrot, float eps,
+                            float freq_base, float *q_out, hipStream_t stream) {
+  int rc = check(d);
+  if (rc) return rc;
+  if ((rc = check_kernels(d))) return rc;
+  if (layer < 0 || layer >= d->n_layers || n_tok < 0) return BKV_EINVAL;
+  if (nrot < 0 || nrot > d->hd || (nrot & 1)) return BKV_EINVAL;
+  if (!(eps >= 0.0f) || !std::isfinite(freq_base) || freq_base <= 0.0f) return BKV_EINVAL;
+  if (n_tok == 0) return BKV_OK;
+  if ((int64_t)pos0 + n_tok > max_positions(d)) return BKV_ECAP;
+  const void *ptrs[6] = {q_in, k_in, v_in, qn_w, kn_w, q_out};
+  for (const void *p : ptrs) {
+    if (!p) return BKV_EINVAL;
+    if (!aligned16(p)) return BKV_EALIGN;
+  }
+  NormRopeArgs a{};
+  a.L = view(d, layer);
+  a.nkv = d->nkv;
+  a.nh = d->nh;
+  a.nrot = nrot;
+  a.pos0 = pos0;
+  a.eps = eps;
+  a.freq_base = freq_base;
+  a.q_in = q_in; a.k_in = k_in; a.v_in = v_in;
+  a.qn_w = qn_w; a.kn_w = kn_w;
+  a.q_out = q_out;
+  return hip_fail(launch_norm_rope_append(a, d->k_fmt, d->v_fmt, n_tok, stream));
+}
+
 int bkv_attn_decode(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
                     const float *gate, float *out, float *out_gated, void *workspace,
                     size_t ws_bytes, hipStream_t stream) {
@@ -527,6 +558,22 @@ int bkv_attn_prefill_chunk(const bkv_cache_desc *d, int layer, uint32_t pos0, in
                            void *workspace, size_t ws_bytes, hipStream_t stream) {
   return prefill_common(d, layer, pos0, n_q, q, gate, out, out_gated, workspace, ws_bytes, stream,
                         kHd, kHd);
+}
+
+int bkv_prefill_step(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q, const float *k,
+                     const float *v, const float *q, const float *gate, float *out,
+                     float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  int rc = check(d);
+  if (rc) return rc;
+  if (n_q < 0 || n_q > BKV_PREFILL_MAX_Q) return BKV_EINVAL;
+  if (layer < 0 || layer >= d->n_layers) return BKV_EINVAL;
+  if ((int64_t)pos0 + n_q > max_positions(d)) return BKV_ECAP;
+  if (!workspace) return BKV_EWORKSPACE;
+  if (((uintptr_t)workspace & 255u) != 0) return BKV_EALIGN;
+  if (!q || !out) return BKV_EINVAL;
+  if ((rc = bkv_kv_append(d, layer, pos0, n_q, k, v, stream))) return rc;
+  return bkv_attn_prefill_chunk(d, layer, pos0, n_q, q, gate, out, out_gated, workspace, ws_bytes,
+                                stream);
 }
 
 int bkv_attn_prefill_chunk_qg(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,

@@ -215,6 +215,18 @@ struct PrefillXArgs {
 hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st);
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base);
 
+// ------------------------------------------------------------------ QK norm + rope + append
+struct NormRopeArgs {
+  LayerView L;
+  int nkv, nh, nrot;
+  uint32_t pos0;
+  float eps, freq_base;
+  const float *q_in, *k_in, *v_in;   // [n_tok][nh][hd], [n_tok][nkv][hd], [n_tok][nkv][hd]
+  const float *qn_w, *kn_w;          // [hd] norm weights
+  float *q_out;                      // [n_tok][nh][hd]
+};
+hipError_t launch_norm_rope_append(const NormRopeArgs &a, int kf, int vf, int n_tok, hipStream_t st);
+
 #define BKV_FMT_SWITCH(KF, VF, ...)                                                    \
   do {                                                                                \
     if ((KF) == BKV_Q8_0 && (VF) == BKV_Q8_0) { constexpr int KF_ = 1, VF_ = 1; __VA_ARGS__; } \

@@ -127,6 +127,29 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
  * not a memset; stream-ordered. */
 int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream);
 
+/* The reference's fused append front end (attn_norm_rope2.comp:138-217, dispatched by attn_block at
+ * runtime_vk/bonsai_forward.h:609-612; CPU mirror attn_vk.h:102-122, :266-281): for n_tok tokens at
+ * positions pos0.., the projected Q and K rows get the per-head RMS norm (eps), the norm weight
+ * (qn_w / kn_w, [hd]) and the half-split rope over the first nrot dims (freq_base); K is then
+ * appended like bkv_kv_append, V (no norm, no rope) too, and the roped Q rows go to
+ * q_out [n_tok][nh][hd] (fp32; bkv_attn_decode rounds them to the fp16 operand, as the reference's
+ * Q16 pack does). pow / cos / sin are correctly rounded (the reference's mirror uses powf / cosf /
+ * sinf, one fp32 ulp apart where those are not). q_out may alias q_in. */
+int bkv_qk_norm_rope_append(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_tok,
+                            const float *q_in, const float *k_in, const float *v_in,
+                            const float *qn_w, const float *kn_w, int nrot, float eps,
+                            float freq_base, float *q_out, hipStream_t stream);
+
+/* One chunk of a prompt for one layer: bkv_kv_append of the chunk's n_q tokens at pos0 .. pos0+n_q-1
+ * (k, v: [n_q][nkv][hd] post-RoPE K and raw V), then bkv_attn_prefill_chunk over them. The chunked
+ * form of the engine's prompt loop, which runs one decode step per prompt token
+ * (runtime_vk/bonsai_forward.h:2752-2759); row i equals bkv_decode_step at pos0 + i. The workspace
+ * is the prefill one (bkv_workspace_bytes(d, BKV_OP_PREFILL, ...)). Argument errors are reported
+ * before anything is launched. */
+int bkv_prefill_step(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q, const float *k,
+                     const float *v, const float *q, const float *gate, float *out,
+                     float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream);
+
 /* Q and the gate straight from the engine's attn_q output, qg = [nh][2*hd] per query: head h's
  * hd query values, then its hd gate values (the per-head interleave that deint_qg splits,
  * runtime_vk/shaders/deint_qg.comp:1-45, before attn_qk_softmax and attn_pv_q8v read q and the gate,

@@ -68,6 +68,9 @@ def lib():
             "bko_now": (ctypes.c_double, []),
             "bko_set_exp_mode": (None, [i32]),
             "bko_max_threads": (i32, []),
+            "bko_norm_rope_row": (None, [i32, i32, ctypes.c_float, ctypes.c_float, P, P, u32, i32, P]),
+            "bko_norm_rope_append": (None, [D, i32, u32, i32, P, P, P, P, P, i32, ctypes.c_float,
+                                            ctypes.c_float, i32, P]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -87,12 +90,40 @@ def ref():
         L.ref_decode_row.restype = None
         L.ref_decode_row.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, P, P, P,
                                      ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]
+        L.ref_norm_rope_row.restype = None
+        L.ref_norm_rope_row.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, P, P,
+                                        ctypes.c_int, P]
         _ref = L
     return _ref
 
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# the reference model's rope geometry (attn_vk.h:65-77: n_rot 64, eps 1e-6, freq_base 1e7)
+NROT, EPS, FREQ_BASE = 64, 1.0e-6, 10000000.0
+
+
+def norm_rope_row(x, w, pos, nrot=NROT, eps=EPS, base=FREQ_BASE, libm_float=False):
+    """bko_norm_rope_row: one row's RMS norm, weight and rope (fp32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().bko_norm_rope_row(x.size, nrot, eps, base, _p(x), _p(w), pos, int(libm_float), _p(y))
+    return y
+
+
+def ref_norm_rope_row(x, w, pos, nrot=NROT, eps=EPS, base=FREQ_BASE):
+    """The reference's attn_rms_norm + attn_rope compiled from attn_vk.h, or None when not built."""
+    R = ref()
+    if R is None:
+        return None
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    R.ref_norm_rope_row(x.size, nrot, eps, base, _p(x), _p(w), pos, _p(y))
+    return y
 
 
 class exp_mode:
@@ -194,6 +225,17 @@ class HostCache:
         for mine, theirs in zip(self.arrays(), arrs):
             if mine is not None:
                 mine[...] = np.asarray(theirs)
+
+    def norm_rope_append(self, layer, pos0, q_in, k_in, v_in, qn_w, kn_w, nrot=NROT, eps=EPS,
+                         base=FREQ_BASE):
+        """bko_norm_rope_append: returns the normed + roped Q [n][nh][hd]; K (normed + roped) and V go
+        into the cache at pos0.."""
+        q_in, k_in, v_in, qn_w, kn_w = (np.ascontiguousarray(a, np.float32) for a in (q_in, k_in, v_in, qn_w, kn_w))
+        n = q_in.shape[0]
+        q_out = np.empty_like(q_in)
+        lib().bko_norm_rope_append(ctypes.byref(self.desc), layer, pos0, n, _p(q_in), _p(k_in), _p(v_in),
+                                   _p(qn_w), _p(kn_w), nrot, eps, base, self.rhaz, _p(q_out))
+        return q_out
 
     def fill_synthetic(self):
         """The reference's timing fixture (runtime_vk/bonsai_forward.h:1355-1370): the whole KV arena

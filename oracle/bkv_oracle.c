@@ -360,6 +360,58 @@ void bko_attn_prefill(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q
                     out + i * rs, out_gated ? out_gated + i * rs : NULL, NULL, NULL, NULL, nthreads);
 }
 
+/* ------------------------------------------------------------------ QK norm + rope
+ * attn_rms_norm / attn_rope (runtime_vk/attn_vk.h:102-122) with rope_theta (:82-84): the squares are
+ * rounded before they are added (the shader materialises them, attn_norm_rope2.comp:140-150), the
+ * rotation reads the normed input for both partners and rounds each product. */
+void bko_norm_rope_row(int hd, int nrot, float eps, float freq_base, const float *x, const float *w,
+                       uint32_t pos, int libm_float, float *y) {
+  float ss = 0.0f;
+  for (int d = 0; d < hd; ++d) {
+    const float sq = x[d] * x[d];
+    ss = ss + sq;
+  }
+  const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+  float n[256];
+  for (int d = 0; d < hd; ++d) {
+    const float t = x[d] * inv;
+    n[d] = t * w[d];
+  }
+  const int half = nrot / 2;
+  for (int p = 0; p < half; ++p) {
+    const float ex = -2.0f * (float)p / (float)nrot;
+    const float th = libm_float ? powf(freq_base, ex) : (float)pow((double)freq_base, (double)ex);
+    const float a = (float)pos * th;
+    const float cs = libm_float ? cosf(a) : (float)cos((double)a);
+    const float sn = libm_float ? sinf(a) : (float)sin((double)a);
+    const float lo = n[p], hi = n[p + half];
+    const float l1 = lo * cs, l2 = hi * sn, h1 = hi * cs, h2 = lo * sn;
+    y[p] = l1 - l2;
+    y[p + half] = h1 + h2;
+  }
+  for (int d = nrot; d < hd; ++d) y[d] = n[d];
+}
+
+void bko_norm_rope_append(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_tok,
+                          const float *q_in, const float *k_in, const float *v_in, const float *qn_w,
+                          const float *kn_w, int nrot, float eps, float freq_base, int rhaz,
+                          float *q_out) {
+  const size_t hd = (size_t)d->hd;
+  float *kr = (float *)malloc(sizeof(float) * (size_t)n_tok * d->nkv * hd);
+  for (int t = 0; t < n_tok; ++t) {
+    for (int h = 0; h < d->nh; ++h) {
+      const size_t o = ((size_t)t * d->nh + h) * hd;
+      bko_norm_rope_row(d->hd, nrot, eps, freq_base, q_in + o, qn_w, pos0 + (uint32_t)t, 0, q_out + o);
+    }
+    for (int h = 0; h < d->nkv; ++h) {
+      const size_t o = ((size_t)t * d->nkv + h) * hd;
+      bko_norm_rope_row(d->hd, nrot, eps, freq_base, k_in + o, kn_w, pos0 + (uint32_t)t, 0, kr + o);
+    }
+  }
+  bko_kv_append(d, layer, pos0, n_tok, kr, v_in, rhaz);
+  free(kr);
+}
+
 /* ------------------------------------------------------------------ synthetic data
  * splitmix64 (Steele, Lea, Flood 2014): z = x + 0x9E3779B97F4A7C15, then two xor-shift-multiply
  * rounds and a final xor-shift. Counter-based use: value i of stream (seed, sid) is

@@ -12,6 +12,8 @@
  *   score/softmax/P16/PV .... runtime_vk/attn_vk.h:156-212 and :261-311 (attn_forward<true>)
  *   fp64 ideal leg .......... runtime_vk/attn_vk.h:320-387 (attn_forward_ideal)
  *   q8_0 reconstruction ..... runtime_vk/bonsai_forward.h:1404-1488 (kv_dump)
+ *   QK RMS norm + rope ...... runtime_vk/attn_vk.h:82-84, :102-122 (attn_rms_norm, attn_rope), with
+ *                             runtime_vk/shaders/attn_norm_rope2.comp:138-181 (the fused append)
  *   arena layout ............ runtime_vk/kv_guard.h:94-150, runtime_vk/bonsai_forward.h:1940-1973
  *
  * Parity pins (what checks each function; see tests/test_oracle_*.py):
@@ -25,6 +27,10 @@
  *                      compiled from runtime_vk/attn_vk.h (bit-exact, fp16 cache), plus closed forms:
  *                      one key -> p = 1, identical keys -> uniform p, GQA-identical scores.
  *   bko_attn_decode_ideal ... numpy float64 recomputation in tests.
+ *   bko_norm_rope_row  in libm-float mode, the reference's attn_rms_norm + attn_rope compiled from
+ *                      runtime_vk/attn_vk.h (bit-exact); closed forms: position 0 is the weighted
+ *                      norm alone, dims past n_rot pass through, the rotation preserves each pair's
+ *                      norm, a float64 recomputation to 1e-6.
  */
 #ifndef BKV_ORACLE_H
 #define BKV_ORACLE_H
@@ -84,6 +90,22 @@ void bko_attn_prefill(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q
 
 /* exp mode: 0 = correctly rounded (float)exp((double)x) (default), 1 = libm expf */
 void bko_set_exp_mode(int mode);
+
+/* Per-head RMS norm, weight and rope of one row (attn_vk.h:102-122, the shader's order
+ * attn_norm_rope2.comp:138-165): ss = sum x*x ascending, inv = 1/sqrt(ss/hd + eps),
+ * y = (x*inv)*w, then inside the first nrot dims the half-split rotation by
+ * theta_p = base^(-2p/nrot) at angle pos*theta_p. libm_float = 0: pow/cos/sin are the correctly
+ * rounded values (float)f((double)x), the contract the gfx950 kernel reproduces; 1: the C library's
+ * powf/cosf/sinf, as the reference's CPU mirror calls them. */
+void bko_norm_rope_row(int hd, int nrot, float eps, float freq_base, const float *x, const float *w,
+                       uint32_t pos, int libm_float, float *y);
+/* The fused append of n_tok tokens at pos0..: Q rows normed + roped into q_out [n_tok][nh][hd]
+ * (fp32, the values the reference packs to Q16), K rows normed + roped and appended, V appended raw
+ * (attn_norm_rope2.comp:138-217; attn_vk.h:266-281). */
+void bko_norm_rope_append(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_tok,
+                          const float *q_in, const float *k_in, const float *v_in, const float *qn_w,
+                          const float *kn_w, int nrot, float eps, float freq_base, int rhaz,
+                          float *q_out);
 
 /* seeded synthetic data: splitmix64 -> Box-Muller (double) -> float * sigma.
  * Element i of stream (seed, stream_id) is a pure function of (seed, stream_id, i). */

@@ -34,4 +34,15 @@ void ref_decode_row(int hd, int nh, int nkv, float scale, const uint32_t *q16, c
   attn_gate_row(pregate, gate, hd, gated);
 }
 
+// One row through the reference's attn_rms_norm then attn_rope (attn_vk.h:102-122), as attn_forward
+// calls them for a Q or K row (attn_vk.h:268-276), into a separate output (the alias-safe form).
+void ref_norm_rope_row(int hd, int nrot, float eps, float freq_base, const float *x, const float *w,
+                       int pos, float *y) {
+  AttnCfg c;
+  c.hd = hd; c.nrot = nrot; c.eps = eps; c.freq_base = freq_base;
+  std::vector<float> n(hd);
+  attn_rms_norm(c, x, w, n.data());
+  attn_rope(c, n.data(), pos, y);
+}
+
 }  // extern "C"

@@ -172,3 +172,29 @@ def test_prefill_interleaved_qg(mode, n_q, monkeypatch):
     b, bg = dev.prefill_chunk_qg(0, pos0, inter)
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(ag, bg)
+
+
+def test_prefill_step_is_append_then_chunk():
+    """bkv_prefill_step (append the chunk, then its attention) leaves the oracle's cache bytes and
+    gives the oracle's prefill rows; a prompt fed as three chunks equals one decode step per token
+    (the engine's prompt loop, runtime_vk/bonsai_forward.h:2752-2759) to the tolerance."""
+    from tests.gpu_util import same_bytes
+    n0, chunks = 500, [40, 17, 90]
+    n = n0 + sum(chunks)
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n0, seed=51)
+    k, v = oracle.synth_kv(n - n0, 4, 256, 52, 0, outliers=3)
+    q, g = qg(52, 0, n=n - n0)
+    pos = n0
+    for c in chunks:
+        i = pos - n0
+        host.append(0, pos, k[i:i + c], v[i:i + c])
+        want, wg = host.prefill(0, pos, q[i:i + c], g[i:i + c], nthreads=8)
+        out, og = dev.prefill_step(0, pos, torch.from_numpy(k[i:i + c]).cuda(),
+                                   torch.from_numpy(v[i:i + c]).cuda(), torch.from_numpy(q[i:i + c]).cuda(),
+                                   torch.from_numpy(g[i:i + c]).cuda())
+        torch.cuda.synchronize()
+        assert report(f"prefill_step pos={pos} n={c}", out.cpu().numpy(), want) <= TOL
+        assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
+        pos += c
+    assert not any(same_bytes(dev, host))
