@@ -22,7 +22,7 @@ EXPORTS = [
     "bkv_geom_check", "bkv_slot_bytes", "bkv_max_positions", "bkv_kv_append", "bkv_attn_decode",
     "bkv_decode_step", "bkv_attn_prefill_chunk", "bkv_workspace_bytes", "bkv_strerror",
     "bkv_last_hip_error", "bkv_version", "bkv_debug_layout", "bkv_workspace_init", "bkv_decode_path",
-    "bkv_kv_fill_synthetic", "bkv_attn_decode_qg", "bkv_decode_step_qg", "bkv_attn_prefill_chunk_qg", "bkv_prefill_step", "bkv_qk_norm_rope_append",
+    "bkv_kv_fill_synthetic", "bkv_attn_decode_qg", "bkv_decode_step_qg", "bkv_attn_prefill_chunk_qg", "bkv_prefill_step", "bkv_qk_norm_rope_append", "bkv_attn_decode_window",
 ]
 
 
@@ -82,6 +82,7 @@ def lib():
         "bkv_decode_step_qg": (i32, [D, i32, u32, P, P, P, P, P, P, sz, P]),
         "bkv_attn_prefill_chunk_qg": (i32, [D, i32, u32, i32, P, P, P, P, sz, P]),
         "bkv_prefill_step": (i32, [D, i32, u32, i32, P, P, P, P, P, P, P, sz, P]),
+        "bkv_attn_decode_window": (i32, [D, i32, u32, u32, P, P, P, P, P, sz, P]),
         "bkv_qk_norm_rope_append": (i32, [D, i32, u32, i32, P, P, P, P, P, i32, ctypes.c_float,
                                           ctypes.c_float, P, P]),
     }

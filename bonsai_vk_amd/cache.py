@@ -233,6 +233,20 @@ class KvCache:
                                            self._stream()), "bkv_workspace_init")
         return self._pws
 
+    def decode_window(self, layer, kstart, nfill, q, gate=None):
+        """bkv_attn_decode_window: attention over keys [kstart, nfill) (an evicted prefix)."""
+        q = self._f32(q, (self.nh, self.hd))
+        out = torch.empty((self.nh, self.hd), dtype=torch.float32, device=self.device)
+        og = None
+        if gate is not None:
+            gate = self._f32(gate, (self.nh, self.hd))
+            og = torch.empty_like(out)
+        check(lib().bkv_attn_decode_window(ctypes.byref(self.desc), layer, kstart, nfill, q.data_ptr(),
+                                           self._ptr(gate), out.data_ptr(), self._ptr(og),
+                                           self.workspace.data_ptr(), self.workspace.numel(),
+                                           self._stream()), "bkv_attn_decode_window")
+        return out, og
+
     def decode_qg(self, layer, nfill, qg, gated=True):
         """bkv_attn_decode_qg: q and gate from the interleaved attn_q output [nh][2*hd]."""
         qg = self._f32(qg, (self.nh, 2 * self.hd))

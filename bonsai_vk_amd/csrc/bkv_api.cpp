@@ -257,6 +257,7 @@ static LayerView view(const bkv_cache_desc *d, int layer) {
   L.vs = at(d->v_scales, 3);
   L.bt = d->page_tokens > 0 ? d->block_table + (int64_t)layer * d->max_pages : nullptr;
   L.page = d->page_tokens > 0 ? d->page_tokens : 0;
+  L.base = 0;
   return L;
 }
 
@@ -264,7 +265,8 @@ static LayerView view(const bkv_cache_desc *d, int layer) {
 // attn_q output, q then gate per head)
 static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *q,
                          const float *gate, float *out, float *out_gated, void *ws, size_t ws_bytes,
-                         hipStream_t st, const AppendArgs *fused, int qs = kHd, int gs = kHd) {
+                         hipStream_t st, const AppendArgs *fused, int qs = kHd, int gs = kHd,
+                         uint32_t kstart = 0) {
   int rc = check(d);
   if (rc) return rc;
   if ((rc = check_kernels(d))) return rc;
@@ -275,10 +277,14 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   if (gate && (!aligned16(gate) || !aligned16(out_gated))) return BKV_EALIGN;
   if (!ws) return BKV_EWORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return BKV_EALIGN;
+  // a window [kstart, nfill): the kernels see nfill - kstart keys starting at position kstart
+  if (kstart >= nfill) return BKV_EINVAL;
+  nfill -= kstart;
   const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
   if (ws_bytes < p.total) return BKV_EWORKSPACE;
   char *w = (char *)ws;
-  const LayerView L = view(d, layer);
+  LayerView L = view(d, layer);
+  L.base = kstart;
 
   const int path = choose_path(p);
   if (path == kPathResident) {
@@ -455,6 +461,13 @@ int bkv_decode_step(const bkv_cache_desc *d, int layer, uint32_t pos, const floa
 
 // the _qg variants read Q and the gate from the engine's attn_q output: per head, hd values of q
 // then hd values of the gate (the layout deint_qg splits, runtime_vk/shaders/deint_qg.comp)
+int bkv_attn_decode_window(const bkv_cache_desc *d, int layer, uint32_t kstart, uint32_t nfill,
+                           const float *q, const float *gate, float *out, float *out_gated,
+                           void *workspace, size_t ws_bytes, hipStream_t stream) {
+  return decode_common(d, layer, nfill, q, gate, out, out_gated, workspace, ws_bytes, stream,
+                       nullptr, kHd, kHd, kstart);
+}
+
 int bkv_attn_decode_qg(const bkv_cache_desc *d, int layer, uint32_t nfill, const float *qg,
                        float *out, float *out_gated, void *workspace, size_t ws_bytes,
                        hipStream_t stream) {

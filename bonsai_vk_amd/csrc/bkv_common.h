@@ -91,9 +91,11 @@ struct LayerView {
   const uint8_t *kd, *ks, *vd, *vs;   // this layer's arrays (scales may be null)
   const int32_t *bt;                  // this layer's block-table row, or null (contiguous)
   int page;                           // tokens per page (paged) or 0
+  int64_t base;                       // key index 0 is position base (a window's first live key)
 };
 
 __device__ __forceinline__ int64_t slot_of(const LayerView &L, int64_t pos) {
+  pos += L.base;
   if (L.page == 0) return pos;
   const int64_t pg = pos / L.page;
   return (int64_t)L.bt[pg] * L.page + (pos - pg * L.page);
@@ -104,9 +106,9 @@ __device__ __forceinline__ int64_t slot_of(const LayerView &L, int64_t pos) {
 template <bool PG>
 __device__ __forceinline__ int64_t slot_t(const LayerView &L, int64_t pos) {
   if constexpr (!PG) {
-    return pos;
+    return pos + L.base;
   } else {
-    const uint32_t p = (uint32_t)pos, pg = p / (uint32_t)L.page;
+    const uint32_t p = (uint32_t)(pos + L.base), pg = p / (uint32_t)L.page;
     return (int64_t)L.bt[pg] * L.page + (int64_t)(p - pg * (uint32_t)L.page);
   }
 }

@@ -8,10 +8,10 @@ side so an engine that moves onto libbkv keeps the same decisions:
   KvGuard ....... KvGuard (runtime_vk/kv_guard.h:579-648): blocks of blk_slots positions, and one
                   decision per block boundary from the next position and the spill metric.
 
-KV_EVICT is returned as the reference returns it (evict the farthest block); acting on it means
-excluding that block's keys from the softmax, which the reference does with its additive score
-mask. libbkv's attention has no key mask, so an engine on libbkv can act on KV_REFUSE (and on
-BKV_ECAP from the kernels, the geometry ceiling) but has no masked-out prefix to evict into.
+KV_EVICT is returned as the reference returns it (evict the farthest block). Acting on it means
+excluding that block's keys from the softmax, which the reference does with -INF in its additive
+score mask; with libbkv the engine advances live_low by one block and attends with
+bkv_attn_decode_window(kstart = live_low), the same computation (a -INF key adds exactly +0).
 """
 from dataclasses import dataclass, field
 
@@ -72,6 +72,7 @@ class KvGuard:
         if value > self.g_spill_hard and growing:
             if self.allow_evict and b >= 1 and self.n_blk >= 2:
                 self.n_evict += 1
+                self.live_low += self.blk_slots
                 return KV_EVICT, "spill: evict the farthest KV block"
             self.n_refuse += 1
             return KV_REFUSE, "spill: refuse new KV blocks"

@@ -150,6 +150,16 @@ int bkv_prefill_step(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
                      const float *v, const float *q, const float *gate, float *out,
                      float *out_gated, void *workspace, size_t ws_bytes, hipStream_t stream);
 
+/* Attention over the live window of keys [kstart, nfill) only: bkv_attn_decode as if the keys
+ * before kstart did not exist. This is the reference's eviction of the farthest KV blocks, which
+ * masks them out of the softmax with -INF in the additive score mask (runtime_vk/kv_guard.h:579-637
+ * decides, runtime_vk/bonsai_forward.h the MASK window); a -INF key adds exactly +0 to the serial
+ * sum and nothing to PV, so the window is the same computation. kstart < nfill; workspace sized for
+ * nfill - kstart keys or more. */
+int bkv_attn_decode_window(const bkv_cache_desc *d, int layer, uint32_t kstart, uint32_t nfill,
+                           const float *q, const float *gate, float *out, float *out_gated,
+                           void *workspace, size_t ws_bytes, hipStream_t stream);
+
 /* Q and the gate straight from the engine's attn_q output, qg = [nh][2*hd] per query: head h's
  * hd query values, then its hd gate values (the per-head interleave that deint_qg splits,
  * runtime_vk/shaders/deint_qg.comp:1-45, before attn_qk_softmax and attn_pv_q8v read q and the gate,

@@ -281,3 +281,28 @@ def oracle_like(cache):
         def arrays(self):
             return [None if a is None else a.numpy() for a in cache.host_arrays()]
     return _H()
+
+
+@pytest.mark.parametrize("page", [0, 64])
+def test_decode_window_equals_evicted_prefix(path, page):
+    """bkv_attn_decode_window over keys [kstart, nfill) equals, bit for bit, the decode of a cache
+    holding only those keys (the reference's eviction masks the farthest blocks out of the softmax
+    with -INF, which adds exactly nothing), and matches the oracle."""
+    n, kstart = 2600, 640
+    pool = 48
+    bt = np.stack([np.random.default_rng(7).permutation(pool)]).astype(np.int32) if page else None
+    kw = dict(page_tokens=page, max_pages=pool, block_table=bt) if page else {}
+    dev, _ = pair(1, pool * 64 if page else n, BKV_Q8_0, BKV_Q8_0, **kw)
+    win, host = pair(1, n - kstart, BKV_Q8_0, BKV_Q8_0)
+    k, v = oracle.synth_kv(n, 4, 256, 61, 0, outliers=3)
+    dev.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    win.append(0, 0, torch.from_numpy(k[kstart:]).cuda(), torch.from_numpy(v[kstart:]).cuda())
+    host.append(0, 0, k[kstart:], v[kstart:])
+    q, g = qg(61, 0)
+    qd, gd = torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda()
+    a, ag = dev.decode_window(0, kstart, n, qd, gd)
+    b, bg = win.decode(0, n - kstart, qd, gd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(ag, bg)
+    want, _ = host.decode(0, n - kstart, q, nthreads=8)
+    assert report("window", a.cpu().numpy(), want) <= TOL

@@ -31,6 +31,7 @@ def test_decisions():
     assert kg.decide(640, value=10.0, have_counter=True, growing=True)[0] == KV_OK
     ev = KvGuard(blk_slots=64).init(g, 1024, 1 << 30, evict=True)
     assert ev.decide(640, value=100.0, have_counter=True, growing=True)[0] == KV_EVICT
+    assert ev.live_low == 64                                  # the window now starts one block later
     assert ev.decide(63, value=100.0, have_counter=True, growing=True)[0] == KV_REFUSE   # block 0
     small = KvGuard(blk_slots=64).init(g, 100, 1 << 30, evict=True)          # one whole block only
     assert small.decide(70, value=100.0, have_counter=True, growing=True)[0] == KV_REFUSE
