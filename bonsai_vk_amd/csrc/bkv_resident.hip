@@ -497,6 +497,34 @@ __device__ __forceinline__ T pick4(const T (&v)[kGqa], int i) {
   return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
 }
 
+// PV over a wave's register-resident q8_0 V rows (slots s: key 32 s + 4 wave + vkk), probabilities
+// from p[k] (4 fp16 per key). DELTA: the probabilities are p[k] - q[k] (exact in fp32), and a slot
+// no lane of the wave needs is skipped.
+template <bool DELTA>
+__device__ __forceinline__ void pv_res_slots(const uint4 (&vd)[kResVTiles], const uint32_t (&vsw)[kResVTiles],
+                                             const uint2 *p16, const uint2 *q16, int nk, int wave, int vkk,
+                                             int vsub, float (&acc)[kGqa][KRow<BKV_Q8_0>::EPL]) {
+#pragma unroll
+  for (int s = 0; s < kResVTiles; ++s) {
+    if (s * 32 < nk) {
+      const int k = s * 32 + wave * 4 + vkk;
+      const uint2 pw = k < nk ? p16[k] : make_uint2(0u, 0u);
+      float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
+                       f16_to_f32(pw.y >> 16)};
+      if constexpr (DELTA) {
+        const uint2 qw = k < nk ? q16[k] : make_uint2(0u, 0u);
+        if (!__any(pw.x != qw.x || pw.y != qw.y)) continue;
+        p[0] -= f16_to_f32(qw.x & 0xFFFFu);
+        p[1] -= f16_to_f32(qw.x >> 16);
+        p[2] -= f16_to_f32(qw.y & 0xFFFFu);
+        p[3] -= f16_to_f32(qw.y >> 16);
+      }
+      const float vsc = k < nk ? f16_to_f32(((vsub >> 1) & 1) ? (vsw[s] >> 16) : (vsw[s] & 0xFFFFu)) : 0.0f;
+      v_accum<BKV_Q8_0>(vd[s], vsc, p, acc);
+    }
+  }
+}
+
 template <int KF, int VF, bool VRES, bool PG>
 __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   constexpr int NT = kResNT, NW = kResNW;
@@ -522,7 +550,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   __shared__ float4 s_wf[NW];
   __shared__ double s_wd[NW * kGqa];
   __shared__ int s_wc[NW * kGqa];
-  __shared__ float s_M[kGqa], s_S[kGqa];
+  __shared__ float s_M[kGqa], s_S[kGqa], s_Sa[kGqa];
   __shared__ double s_P0[kGqa];
   __shared__ int s_ok[kGqa];
   __shared__ long long s_tt[kGqa];
@@ -671,12 +699,17 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     const float mw = lane < G ? __uint_as_float((unsigned)(v[0] >> 32)) : -INFINITY;
     const float lw = lane < G ? __uint_as_float((unsigned)v[0] & ~3u) : 0.0f;
     const float m = wave_max(mw);
-    double p = lane < wi ? (double)lw * exp((double)mw - (double)m) : 0.0;
+    const double lx = lane < G ? (double)lw * exp((double)mw - (double)m) : 0.0;
+    double p = lane < wi ? lx : 0.0, t = lx;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) p += __shfl_xor(p, o);
+    for (int o = 32; o > 0; o >>= 1) {
+      p += __shfl_xor(p, o);
+      t += __shfl_xor(t, o);
+    }
     if (lane == 0) {
       s_M[wave] = m;
       s_P0[wave] = p;
+      s_Sa[wave] = (float)t;   // the sum from the statistics: within ~1e-6 of the exact one
     }
   }
   __syncthreads();
@@ -837,7 +870,19 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       nspc[h] += s_tc[h];
     }
   }
-  __syncthreads();                         // s_spec complete
+  // VRES: p16' = f16(e / S_a), the probabilities with the sum barrier A already gives, into the
+  // (now free) K tile area, for the speculative PV of waves kGqa.. during the walk
+  uint2 *s_ps = reinterpret_cast<uint2 *>(lds);
+  if constexpr (VRES) {
+    if (tid < nk) {
+      _Float16 pk[kGqa];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) pk[h] = (_Float16)(ev[0][h] / s_Sa[h]);
+      s_ps[tid] = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16),
+                             (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16));
+    }
+  }
+  __syncthreads();                         // s_spec complete (and s_ps)
   // (spec timestamp removed)
   // wave h writes head h's specials (staged in LDS) and record: only waves 0..3 store anything
   // barrier B waits for
@@ -857,6 +902,26 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   }
   RTS(3);
+  // VRES: waves kGqa.. (idle through barrier B and the walk) accumulate PV over their register
+  // rows with p16', and park the partial in the K tile area; after the walk they add
+  // (p16 - p16') only for the keys whose rounding the exact sum changes
+  float *s_acc = reinterpret_cast<float *>(lds) + 2048;   // [kGqa*EPL][NW-kGqa][64], past s_ps
+  if constexpr (VRES) {
+    static_assert(2048 * 4 >= SB * sizeof(uint2), "s_ps must end before s_acc");
+    static_assert((2048 + kGqa * VR::EPL * (NW - kGqa) * 64) * 4 <= sizeof(lds), "s_acc must fit");
+    if (wave >= kGqa) {
+      float sacc[kGqa][VR::EPL];
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+        for (int i = 0; i < VR::EPL; ++i) sacc[h][i] = 0.0f;
+      pv_res_slots<false>(vd, vsw, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+        for (int i = 0; i < VR::EPL; ++i) s_acc[((h * VR::EPL + i) * (NW - kGqa) + wave - kGqa) * 64 + lane] = sacc[h][i];
+    }
+  }
 
   // ---------------------------------------------------------------- barrier B: the exact sums
   // wave h polls head h's records of every workgroup, then walks them (every workgroup of the
@@ -961,16 +1026,14 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       xw = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
       xs = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
     }
+    if (wave < kGqa) {
+      pv_res_slots<false>(vd, vsw, s_p16, nullptr, nk, wave, vkk, vsub, acc);
+    } else {
 #pragma unroll
-    for (int s = 0; s < kResVTiles; ++s) {
-      if (s * 32 < nk) {
-        const int k = s * 32 + wave * 4 + vkk;
-        const uint2 pw = k < nk ? s_p16[k] : make_uint2(0u, 0u);
-        const float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
-                               f16_to_f32(pw.y >> 16)};
-        const float vsc = k < nk ? f16_to_f32(((vsub >> 1) & 1) ? (vsw[s] >> 16) : (vsw[s] & 0xFFFFu)) : 0.0f;
-        v_accum<BKV_Q8_0>(vd[s], vsc, p, acc);
-      }
+      for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+        for (int i = 0; i < VR::EPL; ++i) acc[h][i] = s_acc[((h * VR::EPL + i) * (NW - kGqa) + wave - kGqa) * 64 + lane];
+      pv_res_slots<true>(vd, vsw, s_p16, s_ps, nk, wave, vkk, vsub, acc);
     }
     if (kResVTiles * 32 < nk) {
       float p[kGqa];
