@@ -812,6 +812,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       }
     }
   }
+  RTS(10);
   // the tail's steps come after every key of the passes: wave 0 places them with DPP-row scans
   // (lane 16 h + t: key NT + t, head h) on the running sums carried so far
   float evt = 0.0f;
@@ -882,6 +883,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
                              (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16));
     }
   }
+  RTS(11);
   __syncthreads();                         // s_spec complete (and s_ps)
   // (spec timestamp removed)
   // wave h writes head h's specials (staged in LDS) and record: only waves 0..3 store anything
@@ -1088,9 +1090,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       acc[h][i] = v;
     }
   RTS(14);
-  RTSW(10, 7);
   __syncthreads();                         // every wave is done with its V rows
-  RTSW(11, 7);
   float *s_red = reinterpret_cast<float *>(lds);   // [NW][kGqa][kHd]
   if (vkk == 0) {
 #pragma unroll
