@@ -556,7 +556,19 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   __shared__ long long s_tt[kGqa];
   __shared__ int s_tc[kGqa];
 
-  const int w = blockIdx.x, nkv = a.nkv, g = w % nkv, wi = w / nkv, G = a.G;
+  // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
+  // of one key range share an XCD, so the cache lines they split (each 64 B scale line holds all
+  // groups' scales of a slot) are fetched once into that XCD's L2
+  const int w = blockIdx.x, nkv = a.nkv, G = a.G;
+  int g, wi;
+  if ((G & 7) == 0 && ((int)gridDim.x & 7) == 0) {
+    const int x = w & 7, loc = w >> 3;
+    g = loc % nkv;
+    wi = x * (G >> 3) + loc / nkv;
+  } else {
+    g = w % nkv;
+    wi = w / nkv;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t kb = (int64_t)wi * a.kpw;
   const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
