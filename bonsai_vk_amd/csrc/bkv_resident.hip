@@ -456,6 +456,31 @@ __device__ __forceinline__ void classify_d(double abefore, double aafter, float 
   inc = ok ? ldexp(rint(t), B + 17) : 0.0;
 }
 
+// Across the workgroup's waves: sh[i * kGqa + h] holds wave i's total of head h. Lanes 0..kResNW-1
+// scan those totals (DPP row shifts inside the first row of 16), and every lane takes its wave's
+// exclusive prefix and the workgroup total by readlane, instead of each lane summing kResNW values.
+__device__ __forceinline__ int rd_lane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float rd_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double rd_lane(double v, int l) {
+  const long long u = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)u, l), hi = __builtin_amdgcn_readlane((int)(u >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+template <typename T>
+__device__ __forceinline__ void xwave_prefix(const T *sh, int h, int wave, T &before, T &total) {
+  static_assert(kResNW <= 16, "one DPP row holds the wave totals");
+  const int lane = threadIdx.x & 63;
+  T x = lane < kResNW ? sh[lane * kGqa + h] : T(0);
+  x += dpp0<0x111, 0xF>(x);
+  x += dpp0<0x112, 0xF>(x);
+  x += dpp0<0x114, 0xF>(x);
+  if (kResNW > 8) x += dpp0<0x118, 0xF>(x);
+  total = rd_lane(x, kResNW - 1);
+  before = wave > 0 ? rd_lane(x, wave - 1) : T(0);
+}
+
 // the workgroup-wide max / sum of four values at once (every thread receives them)
 __device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -758,17 +783,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h) fin[h] = wave_incl_scan_dpp(ev[r][h]);
       if (lane == 63) s_wf[wave] = make_float4(fin[0], fin[1], fin[2], fin[3]);
       __syncthreads();
-      float fb[kGqa] = {0.0f, 0.0f, 0.0f, 0.0f}, ft[kGqa] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float fb[kGqa], ft[kGqa];
 #pragma unroll
-      for (int i = 0; i < NW; ++i) {
-        const float4 x = s_wf[i];
-        const float xv[kGqa] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          fb[h] += i < wave ? xv[h] : 0.0f;
-          ft[h] += xv[h];
-        }
-      }
+      for (int h = 0; h < kGqa; ++h) xwave_prefix(reinterpret_cast<const float *>(s_wf), h, wave, fb[h], ft[h]);
       // per head: the step's exact increment (an integer below 2^40 in units of 2^-40: fp64 sums of
       // a workgroup's increments stay exact) or a special
       bool sp[kGqa];
@@ -796,17 +813,10 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       // (pass timestamp removed)
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
-        double ib = 0.0, it = 0.0;
-        int cb = 0, ct = 0;
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          const double x = s_wd[i * kGqa + h];
-          const int c = s_wc[i * kGqa + h];
-          ib += i < wave ? x : 0.0;
-          it += x;
-          cb += i < wave ? c : 0;
-          ct += c;
-        }
+        double ib, it;
+        int cb, ct;
+        xwave_prefix(s_wd, h, wave, ib, it);
+        xwave_prefix(s_wc, h, wave, cb, ct);
         if (sp[h]) {
           const int id = nspc[h] + cb + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(msk[h] >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)msk[h], 0u));
           if (id < kMaxSpecial) {
