@@ -9,8 +9,10 @@ scaled x8, V ~ N(0, 0.5) std, Q ~ N(0,1)) so that the timed steps attend over 32
 A second object on the same line, "prefill", times BASELINE config 5: 512 new q8_0 tokens appended
 onto an 8192-token cache, then causal GQA attention for the 512 queries over 8 layers
 (bkv_attn_prefill_chunk), on the exact path (the default) and on the MFMA-order variant.
+A third, "other_configs", gives us/token and roofline fractions of BASELINE configs 2 (8 layers at
+4096 keys) and 4 (65536 keys, 256-token pages of a 320-page pool, f16 and q8_0).
 
-    python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu] [--no-prefill]
+    python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu] [--no-prefill] [--no-configs]
 """
 import argparse
 import ctypes
@@ -30,6 +32,72 @@ def algorithmic_bytes(n, gated=False):
     K/V read 2176 B/key, append write 2176 B, K/V fp32 input 8192 B, Q 16384 B, out 16384 B
     (+ gate read and gated write 32768 B)."""
     return 2176 * n + 43136 + (32768 if gated else 0)
+
+
+def algorithmic_bytes_f16(n):
+    """As algorithmic_bytes for an f16 K+V cache: read 4096 B/key, append write 4096 B, K/V input
+    8192 B, Q 16384 B, out 16384 B."""
+    return 4096 * n + 45056
+
+
+def time_decode(cache, layers, n0, steps, warmup, seed):
+    """Mean us/token of `steps` decode_steps x `layers` layers over keys n0 + 1 .. (after `warmup`
+    untimed ones, which the caller counts into n0), with HIP events around the timed region."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    tot = warmup + steps
+    knew = torch.randn(tot, layers, 1, 4, 256, generator=g, device="cuda")
+    vnew = torch.randn(tot, layers, 1, 4, 256, generator=g, device="cuda") * 0.5
+    q = torch.randn(tot, layers, 16, 256, generator=g, device="cuda")
+    out = torch.empty(layers, 16, 256, device="cuda")
+    base = n0 - warmup
+
+    def step(i):
+        for layer in range(layers):
+            cache.decode_step(layer, base + i, knew[i, layer], vnew[i, layer], q[i, layer], None,
+                              out[layer])
+
+    for i in range(warmup):
+        step(i)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        step(warmup + i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / steps
+
+
+def other_configs(steps=16, warmup=2):
+    """BASELINE configs 2 (8 layers, 4096 keys, q8_0) and 4 (65536 keys in 256-token pages of a
+    320-page pool, seeded permuted block tables, f16 and q8_0), us/token over `steps` decode steps
+    (each appending one token per layer) and the fraction of the HBM roofline."""
+    import numpy as np
+    import torch
+    from bonsai_vk_amd import BKV_F16, BKV_Q8_0, KvCache
+    res = {}
+    L = 8
+    cache = KvCache(n_layers=L, cap=4096 + steps + warmup + 1, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0)
+    gen_cache(cache, 4096 - warmup, seed=1, layers=L)
+    us = time_decode(cache, L, 4096, steps, warmup, seed=11)
+    b = sum(L * algorithmic_bytes(4097 + i) for i in range(steps)) / steps
+    res["config2_q8_4k"] = {"us_per_token": round(us, 2), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del cache
+    bt = np.stack([np.random.default_rng(3).permutation(320) for _ in range(L)]).astype(np.int32)
+    for name, fmt, fb in (("config4_paged_f16_64k", BKV_F16, algorithmic_bytes_f16),
+                          ("config4_paged_q8_64k", BKV_Q8_0, algorithmic_bytes)):
+        torch.cuda.empty_cache()
+        cache = KvCache(n_layers=L, cap=320 * 256, k_fmt=fmt, v_fmt=fmt, page_tokens=256,
+                        max_pages=320, block_table=bt)
+        gen_cache(cache, 65536 - warmup, seed=3, layers=L)
+        us = time_decode(cache, L, 65536, steps, warmup, seed=13)
+        b = sum(L * fb(65537 + i) for i in range(steps)) / steps
+        res[name] = {"us_per_token": round(us, 2), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del cache
+    torch.cuda.empty_cache()
+    return res
 
 
 def gen_cache(cache, n, seed, layers):
@@ -183,6 +251,7 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config-2 and config-4 timings")
     ap.add_argument("--gate", action="store_true", help="also read the gate and write GOUT")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="after the timed region, copy a MIB MiB buffer once (a reference kernel for "
@@ -273,6 +342,11 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctx)
+    if not args.no_configs:
+        del cache
+        torch.cuda.empty_cache()
+        cache = None
+        line["other_configs"] = other_configs()
     if not args.no_prefill:
         del cache
         torch.cuda.empty_cache()
