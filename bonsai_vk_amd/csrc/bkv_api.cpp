@@ -101,7 +101,7 @@ size_t prefill_workspace_bound(int nh, int nkv, size_t base) {
   return worst;
 }
 
-DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page) {
   DecodePlan p;
   p.qk_chunk = qk_keys_per_wg(kfmt);
   p.nch_qk = (int)cdiv(n, p.qk_chunk);
@@ -159,10 +159,12 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n) {
   if (rcap >= nkv && rsync_fits && rtags_fit) {
     const int64_t gmax = std::min<int64_t>(rcap / nkv, kResMaxGroupWgs);
     const int64_t kpw = cdiv(n, std::min<int64_t>(gmax, cdiv(n, 64)));
-    if (kpw <= (int64_t)kResMaxPass * kResNT) {
+    // paged: a workgroup's keys must span at most kResPgMax pages (the kernel's LDS page table)
+    const bool pages_fit = page <= 0 || cdiv(kpw, page) + 1 <= kResPgMax;
+    if (kpw <= (int64_t)kResMaxPass * kResNT && pages_fit) {
       p.rkpw = (int)kpw;
       p.rG = (int)cdiv(n, kpw);
-      p.rvres = vfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
+      p.rvres = vfmt == BKV_Q8_0 && kfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
       size_t f = kSyncBytes;
       p.r_spec = f;   f += align256((size_t)nh * gmax * kMaxSpecial * sizeof(Special));
       p.r_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
@@ -243,7 +245,7 @@ static int64_t max_positions(const bkv_cache_desc *d) {
 
 // where a prefill's own arrays begin: past the largest decode plan this cache allows
 static size_t prefill_base(const bkv_cache_desc *d) {
-  return align256(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_positions(d)).total);
+  return align256(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_positions(d), d->page_tokens).total);
 }
 
 static LayerView view(const bkv_cache_desc *d, int layer) {
@@ -280,7 +282,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   // a window [kstart, nfill): the kernels see nfill - kstart keys starting at position kstart
   if (kstart >= nfill) return BKV_EINVAL;
   nfill -= kstart;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill, d->page_tokens);
   if (ws_bytes < p.total) return BKV_EWORKSPACE;
   char *w = (char *)ws;
   LayerView L = view(d, layer);
@@ -603,7 +605,7 @@ size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx) {
     return std::max(prefill_workspace_bound(d->nh, d->nkv, prefill_base(d)),
                     prefill_exact_workspace(d->nh, d->nkv, max_ctx, prefill_base(d)));
   if (op != BKV_OP_DECODE) return 0;
-  return plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx).total;
+  return plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, max_ctx, d->page_tokens).total;
 }
 
 const char *bkv_strerror(int err) {
@@ -624,7 +626,7 @@ int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
   const int rc = check(d);
   if (rc) return rc;
   if (!out || nfill == 0) return BKV_EINVAL;
-  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill);
+  const DecodePlan p = plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill, d->page_tokens);
   const int path = choose_path(p);
   out[0] = (uint64_t)p.ld;
   out[1] = path == kPathSplit ? p.off_score : 0;
@@ -667,7 +669,7 @@ int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream) {
 
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill) {
   if (check(d) || nfill == 0) return -1;
-  return choose_path(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill));
+  return choose_path(plan_decode(d->nh, d->nkv, d->k_fmt, d->v_fmt, nfill, d->page_tokens));
 }
 
 const char *bkv_last_hip_error(void) { return g_hip_err; }

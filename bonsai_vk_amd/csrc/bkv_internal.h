@@ -132,6 +132,7 @@ struct FusedArgs {
 // 512 + kResTail keys it keeps its V rows in LDS, streamed in behind the exact-sum walk.
 constexpr int kResNT = 512;
 constexpr int kResMaxPass = 4;
+constexpr int kResPgMax = 64;                  // block-table entries a paged workgroup copies into LDS
 constexpr int kResTail = 16;                   // keys past kResNT a q8_0-V workgroup may hold
 constexpr int kResMaxGroupWgs = 64;           // workgroups per KV group at most (walk scratch)
 constexpr int kResGroupLines = 9;              // generation + 2 parities x 4 phase counters
@@ -250,7 +251,7 @@ struct DecodePlan {
   size_t r_spec, r_e, r_sum, r_status, r_part, r_total;
 };
 
-DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill);
+DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill, int page = 0);
 int qk_keys_per_wg(int kfmt);
 
 int fused_max_workgroups(int kf, int vf);

@@ -77,8 +77,29 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
+// Cache slots of a workgroup's keys kb + k (0 <= k < nk). Paged: through an LDS copy of the block-
+// table entries its keys span (lut[p - pf] for page p), so that no lookup is a global load (whose
+// wait would also wait for every tile load in flight). The host takes this kernel only when a
+// workgroup's keys span at most kResPgMax pages.
+struct SlotMap {
+  const LayerView *L;
+  int64_t kb;
+  const int *lut;
+  uint32_t pf;
+};
+template <bool PG>
+__device__ __forceinline__ int64_t slot_k(const SlotMap &m, int k) {
+  if constexpr (!PG) {
+    return m.kb + k + m.L->base;
+  } else {
+    const uint32_t pgs = (uint32_t)m.L->page, p = (uint32_t)(m.kb + k + m.L->base), pg = p / pgs;
+    return (int64_t)m.lut[min(pg - m.pf, (uint32_t)kResPgMax - 1u)] * pgs + (int64_t)(p - pg * pgs);
+  }
+}
+
+// k0: the first key (within the workgroup's range) of the n rows staged
 template <int KF, bool PG>
-__device__ __forceinline__ void stage_k_wave(uint4 *kt, const LayerView &L, int nkv, int g, int64_t j0,
+__device__ __forceinline__ void stage_k_wave(uint4 *kt, const SlotMap &sm, int nkv, int g, int k0,
                                              int n, int ch) {
   // direct-to-LDS: load i writes the 64 consecutive tile slots 64 i .. 64 i + 63 (row = slot / kUPR,
   // column = slot % kUPR); column 16 is the q8_0 scale row (for fp16 K an unused copy of column 0).
@@ -87,13 +108,20 @@ __device__ __forceinline__ void stage_k_wave(uint4 *kt, const LayerView &L, int 
   const int lane = threadIdx.x & 63;
   constexpr int RB = row_bytes(KF);
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(kt));
+  // q8_0 K: every slot first, so no lookup (an LDS read when paged) sits between the tile loads;
+  // fp16 K, whose scores hold more registers, looks each one up in turn
+  constexpr bool PRE = KF == BKV_Q8_0;
+  uint32_t sls[PRE ? kUPR : 1];
+  if constexpr (PRE)
+#pragma unroll
+    for (int i = 0; i < kUPR; ++i) sls[i] = (uint32_t)slot_k<PG>(sm, k0 + min((64 * i + lane) / kUPR, n - 1));
 #pragma unroll
   for (int i = 0; i < kUPR; ++i) {
     const int slotx = 64 * i + lane, row = slotx / kUPR, col = slotx - row * kUPR;
-    const int64_t sl = slot_t<PG>(L, j0 + min(row, n - 1));
+    const int64_t sl = PRE ? (int64_t)sls[PRE ? i : 0] : slot_k<PG>(sm, k0 + min(row, n - 1));
     const uint8_t *src = (KF == BKV_Q8_0 && col == 16)
-                             ? L.ks + (sl * nkv + g) * kScaleRowBytes
-                             : L.kd + (sl * nkv + g) * RB + (ch * 16 + (col & 15)) * 16;
+                             ? sm.L->ks + (sl * nkv + g) * kScaleRowBytes
+                             : sm.L->kd + (sl * nkv + g) * RB + (ch * 16 + (col & 15)) * 16;
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(src), "s"(base + 1024u * i) : "memory", "m0");
   }
@@ -101,52 +129,32 @@ __device__ __forceinline__ void stage_k_wave(uint4 *kt, const LayerView &L, int 
 template <int N>
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
-// Resident q8_0 V. The rows 32s + 4*vw + kk (s < kResVTiles, kk < 4) that wave vw consumes in PV
-// live in vw's K tile once the scores are done: slot s holds 64 x 16 B (lane l: bytes 16*(l%16)..
-// of row 32s + 4*vw + l/16) at tile + 1024 s, and the rows' 16 B block-scale rows follow at
-// tile + 16 KiB + 16 (4s + kk). Waves kResNW/2.. issue these direct-to-LDS loads for their own tile
-// and for the tile of wave w - kResNW/2, so that the other half's memory queues stay free for the
-// barriers and the walk (loads return in issue order). Rows >= nk repeat row nk-1; their
-// probabilities are zero.
-constexpr int kResVTiles = 16;
-template <bool PG>
-__device__ __forceinline__ void load_v_tile(uint4 *tile, int vw, const LayerView &L, int nkv, int g,
-                                            int64_t kb, int nk) {
-  const int lane = threadIdx.x & 63, vsub = lane & 15, vkk = lane >> 4;
-  {
-    const int s = lane >> 2, kk = lane & 3;
-    const int k = min(s * 32 + vw * 4 + kk, nk - 1);
-    const int64_t slot = slot_t<PG>(L, kb + k);
-    __builtin_amdgcn_global_load_lds(
-        (const void __attribute__((address_space(1))) *)(L.vs + (slot * nkv + g) * kScaleRowBytes),
-        (void __attribute__((address_space(3))) *)(tile + kResVTiles * 64), 16, 0, 0);
-  }
-  // every slot is loaded (slots past nk repeat row nk-1), so slot s has landed once at most
-  // kResVTiles-1-s of this wave's loads are outstanding
-#pragma unroll
-  for (int s = 0; s < kResVTiles; ++s) {
-    const int k = min(s * 32 + vw * 4 + vkk, nk - 1);
-    const int64_t slot = slot_t<PG>(L, kb + k);
-    __builtin_amdgcn_global_load_lds(
-        (const void __attribute__((address_space(1))) *)(L.vd + (slot * nkv + g) * kHd + vsub * 16),
-        (void __attribute__((address_space(3))) *)(tile + s * 64), 16, 0, 0);
-  }
-}
+constexpr int kResVTiles = 16;                // resident V row slots per lane (32 rows each)
 
 // the register-resident variant: lane (wave, vkk, vsub) slot s holds bytes 16*vsub.. of row
-// 32 s + 4 wave + vkk and that row's block-pair scale word (rows >= nk repeat row nk-1)
-template <bool PG>
-__device__ __forceinline__ void load_v_regs(uint4 (&vd)[kResVTiles], uint32_t (&vs)[kResVTiles], const LayerView &L,
-                                            int nkv, int g, int64_t kb, int nk) {
+// 32 s + 4 wave + vkk and that row's block-pair scale word (rows >= nk repeat row nk-1). XE: also
+// xd / xs, the same for row 32 kResVTiles + 4 wave + vkk, the streamed slot past the resident rows
+// (always loaded, so the count of loads in flight is fixed)
+template <bool PG, bool XE>
+__device__ __forceinline__ void load_v_regs(uint4 (&vd)[kResVTiles], uint32_t (&vs)[kResVTiles], uint4 &xd, uint32_t &xs,
+                                            const SlotMap &sm, int nkv, int g, int nk) {
+  const LayerView &L = *sm.L;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, vsub = lane & 15, vkk = lane >> 4;
 #pragma unroll
   for (int s = 0; s < kResVTiles; ++s) {
-    const int64_t slot = slot_t<PG>(L, kb + min(s * 32 + wave * 4 + vkk, nk - 1));
+    const int64_t slot = slot_k<PG>(sm, min(s * 32 + wave * 4 + vkk, nk - 1));
     vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
     vs[s] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
   }
+  if constexpr (XE) {
+    const int64_t slot = slot_k<PG>(sm, min(kResVTiles * 32 + wave * 4 + vkk, nk - 1));
+    xd = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+    xs = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+  }
 }
-constexpr int kVLoads = 2 * kResVTiles;      // vector loads load_v_regs issues per wave
+// vector loads load_v_regs issues per wave
+template <bool XE>
+constexpr int kVLoads = 2 * kResVTiles + (XE ? 2 : 0);
 
 // PV over the resident slots, waiting for slot S only: out += p16 * V for the wave's rows
 // 32 s + 4 wave + vkk, 16 elements per lane (attn_vk.h:194-205; q8_0 V = f16(scale) * int8)
@@ -619,6 +627,18 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   RTS(0);
 
+  // paged: the block-table entries of this workgroup's keys into LDS (the append's wait and
+  // barrier below also cover these loads when it runs)
+  __shared__ int s_pg[kResPgMax];
+  SlotMap sm{&L, kb, s_pg, 0u};
+  if constexpr (PG) {
+    const uint32_t pgs = (uint32_t)L.page, pg0 = (uint32_t)(kb + L.base) / pgs,
+                   pg1 = (uint32_t)(kb + max(nk, 1) - 1 + L.base) / pgs;
+    sm.pf = pg0;
+    if (tid <= (int)min(pg1 - pg0, (uint32_t)kResPgMax - 1u)) s_pg[tid] = L.bt[pg0 + tid];
+    if (!a.ap.k) __syncthreads();
+  }
+
   if (a.ap.k) {                                 // decode_step: append the new token first
     if (wave == 0 && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke)
       append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, lane);
@@ -637,6 +657,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // loaded right behind the first K tile so that they stream in during the scores
   uint4 vd[VRES ? kResVTiles : 1];
   uint32_t vsw[VRES ? kResVTiles : 1];
+  // XE (q8_0 K, contiguous: the variant with registers to spare): the streamed slot's V row loads
+  // with the resident ones instead of at the start of PV, where its latency would sit on the
+  // critical path
+  constexpr bool XE = VRES && KF == BKV_Q8_0 && !PG;
+  uint4 xw = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t xs = 0u;
   float sc[MP][kGqa];
   float mloc[kGqa];
 #pragma unroll
@@ -646,15 +672,16 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) sc[r][h] = 0.0f;
     const int64_t j0 = kb + (int64_t)r * NT + wave * 64;
+    const int k0 = r * NT + wave * 64;
     const int n = (int)max((int64_t)0, min((int64_t)64, ke - j0));
     if (n > 0) {
       float acc[kGqa];
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) acc[h] = 0.0f;
-      stage_k_wave<KF, PG>(kt, L, nkv, g, j0, n, 0);
+      stage_k_wave<KF, PG>(kt, sm, nkv, g, k0, n, 0);
       if (VRES && r == 0) {
-        if constexpr (VRES) load_v_regs<PG>(vd, vsw, L, nkv, g, kb, nk);
-        wait_vm<kVLoads>();                // the K tile has landed; the V rows stay in flight
+        if constexpr (VRES) load_v_regs<PG, XE>(vd, vsw, xw, xs, sm, nkv, g, nk);
+        wait_vm<kVLoads<XE>>();                // the K tile has landed; the V rows stay in flight
       } else {
         wait_vm<0>();
       }
@@ -663,7 +690,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       } else {
         qk_f16_half<0>(kt + lane * kUPR, qv, acc);
         wave_lds_sync();
-        stage_k_wave<KF, PG>(kt, L, nkv, g, j0, n, 1);
+        stage_k_wave<KF, PG>(kt, sm, nkv, g, k0, n, 1);
         wait_vm<0>();
         qk_f16_half<1>(kt + lane * kUPR, qv, acc);
       }
@@ -674,7 +701,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         if (lane < n) mloc[h] = fmaxf(mloc[h], acc[h] * a.scale);
       }
     } else if (r == 0) {
-      if constexpr (VRES) load_v_regs<PG>(vd, vsw, L, nkv, g, kb, nk);
+      if constexpr (VRES) load_v_regs<PG, XE>(vd, vsw, xw, xs, sm, nkv, g, nk);
     }
   }
   // the tail (keys NT .. nk-1, at most kResTail): wave 0, lane = 16 h + t scores key NT + t against
@@ -689,7 +716,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     for (int j = 0; j < kHd / 16; ++j) qt[j] = round_f16(qh[16 * j]);
 #pragma unroll
     for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
-    stage_k_wave<KF, PG>(kt, L, nkv, g, kb + NT, tn, 0);
+    stage_k_wave<KF, PG>(kt, sm, nkv, g, NT, tn, 0);
     wait_vm<0>();
     asm volatile("s_nop 4");
     float acc1 = 0.0f;
@@ -698,7 +725,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     } else {
       qk_f16_half1<0>(kt + tt * kUPR, qt, acc1);
       wave_lds_sync();
-      stage_k_wave<KF, PG>(kt, L, nkv, g, kb + NT, tn, 1);
+      stage_k_wave<KF, PG>(kt, sm, nkv, g, NT, tn, 1);
       wait_vm<0>();
       qk_f16_half1<1>(kt + tt * kUPR, qt, acc1);
     }
@@ -1043,10 +1070,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   if constexpr (VRES) {
     // rows 32*kResVTiles.. (at most one slot) are not resident: this wave's row of that slot
     const int kx = kResVTiles * 32 + wave * 4 + vkk;
-    uint4 xw = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t xs = 0u;
-    if (kResVTiles * 32 < nk) {
-      const int64_t slot = slot_t<PG>(L, kb + min(kx, nk - 1));
+    if (!XE && kResVTiles * 32 < nk) {
+      const int64_t slot = slot_k<PG>(sm, min(kx, nk - 1));
       xw = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
       xs = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
     }
@@ -1076,7 +1101,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         kl[u] = base + u * RS + wave * VR::KPW + vkk;
-        const int64_t slot = slot_t<PG>(L, kb + min(kl[u], nk - 1));
+        const int64_t slot = slot_k<PG>(sm, min(kl[u], nk - 1));
         wv[u] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * RB + vsub * 16);
         sw[u] = 0u;
         if (VF == BKV_Q8_0)
@@ -1225,7 +1250,7 @@ static void launch_res(const ResArgs &a, hipStream_t st) {
 // so on a device not held by other long-running kernels every wait is reached by its producers.
 hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st) {
   BKV_FMT_SWITCH(kf, vf, {
-    if constexpr (VF_ == BKV_Q8_0) {
+    if constexpr (VF_ == BKV_Q8_0 && KF_ == BKV_Q8_0) {
       if (vres) {
         launch_res<KF_, VF_, true>(a, st);
         return hipGetLastError();

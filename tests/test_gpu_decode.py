@@ -189,6 +189,35 @@ def test_paged_matches_oracle_and_contiguous(kf, vf, path):
     assert torch.equal(out, o2)
 
 
+@pytest.mark.parametrize("page", [1, 3])
+@pytest.mark.parametrize("kf,vf", [(BKV_Q8_0, BKV_Q8_0), (BKV_F16, BKV_F16)])
+def test_small_pages(kf, vf, page, path):
+    """Pages of 1 and 3 tokens at 8200 keys: a workgroup's 129 keys span 129 pages, more than the
+    resident kernel's LDS page table holds, so the call takes the fused kernel; or 44 pages, the
+    resident kernel with a page size that is no power of two. Matches the oracle and equals the
+    contiguous cache."""
+    n = 8200
+    pool = -(-n // page) + 5
+    bt = np.random.default_rng(11).permutation(pool)[None].astype(np.int32)
+    say(f"small pages kf={kf} vf={vf} page={page} path={path}")
+    dev, host = pair(1, pool * page, kf, vf, page_tokens=page, max_pages=pool, block_table=bt)
+    flat, _ = pair(1, pool * page, kf, vf)
+    if path == "resident":
+        assert dev.decode_path(n) == (1 if page == 1 else 2)
+    k, v = fill(dev, host, 0, n, seed=11)
+    flat.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    q, g = qg(11, 0)
+    want, _ = host.decode(0, n, q, g, nthreads=8)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    o2, _ = flat.decode(0, n, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    assert report(f"pages of {page}", out.cpu().numpy(), want) <= TOL
+    if dev.decode_path(n) == flat.decode_path(n):
+        assert torch.equal(out, o2)
+    else:                                  # other kernels, other PV summation order
+        assert oracle.rel_err(out.cpu().numpy(), o2.cpu().numpy()) <= TOL
+
+
 def test_consecutive_decode_steps(path):
     """BASELINE config 3's pattern at a smaller context: consecutive decode_steps on one workspace
     (each call appends one token and attends over all of them), every step checked against the
