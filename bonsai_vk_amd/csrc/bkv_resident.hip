@@ -525,6 +525,15 @@ __device__ __forceinline__ void block_sum4(float (&v)[kGqa], float *sh) {
   __syncthreads();
 }
 
+// qv[h][j] for a per-lane h, as masked bits (a select chain would be folded into an indexed
+// access, which moves qv to private memory)
+__device__ __forceinline__ float pick4h(const float (&qv)[kGqa][kHd / 16], int h, int j) {
+  uint32_t b = 0u;
+#pragma unroll
+  for (int i = 0; i < kGqa; ++i) b |= __float_as_uint(qv[i][j]) & (0u - (uint32_t)(h == i));
+  return __uint_as_float(b);
+}
+
 template <typename T>
 __device__ __forceinline__ T pick4(const T (&v)[kGqa], int i) {
   return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
@@ -566,7 +575,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   constexpr bool TAIL = VRES;
   constexpr int SB = MP * NT + (TAIL ? kResTail : 0);   // binade-map row per head
   using VR = KRow<VF>;
-  static_assert(!VRES || VF == BKV_Q8_0, "registers hold q8_0 V rows only");
+  static_assert(!VRES || (VF == BKV_Q8_0 && KF == BKV_Q8_0), "register V rows and the tail: q8_0 K and V only");
   // T: per-wave K tiles (64 rows x kUPR uint4 each); after the scores, each wave's q8_0 V rows
   // (68 rows x 256 B, the same bytes) and at the end the PV reduction and the merge.
   // X: the binade map, then the walk scratch, then the fp16 probabilities.
@@ -627,6 +636,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   RTS(0);
 
+  // decode_step: the workgroup whose keys hold the new token appends it, and only that workgroup
+  // reads the row back (the others need not wait for anything before their first tile)
+  const bool appender = a.ap.k && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke;
   // paged: the block-table entries of this workgroup's keys into LDS (the append's wait and
   // barrier below also cover these loads when it runs)
   __shared__ int s_pg[kResPgMax];
@@ -636,23 +648,30 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
                    pg1 = (uint32_t)(kb + max(nk, 1) - 1 + L.base) / pgs;
     sm.pf = pg0;
     if (tid <= (int)min(pg1 - pg0, (uint32_t)kResPgMax - 1u)) s_pg[tid] = L.bt[pg0 + tid];
-    if (!a.ap.k) __syncthreads();
+    if (!appender) __syncthreads();
   }
 
-  if (a.ap.k) {                                 // decode_step: append the new token first
-    if (wave == 0 && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke)
-      append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, lane);
+  if (appender) {
+    if (wave == 0) append_token<KF, VF, false>(a.ap, a.ap.pos, 0, g, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
   // ---------------------------------------------------------------- QK
+  // the first pass's K tile goes out before q is read, so both arrive in one round trip (the wait
+  // for q, issued after the tile, also covers it: loads complete in order)
+  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
+  uint4 *kt = lds + wave * 64 * kUPR;
+  const int n_first = (int)max((int64_t)0, min((int64_t)64, ke - (kb + wave * 64)));
+  if (n_first > 0) stage_k_wave<KF, PG>(kt, sm, nkv, g, wave * 64, n_first, 0);
+  // the tail's rows (keys NT .., wave 0) into the exchange area, free until the e phase
+  const int tn = TAIL ? max(0, nk - NT) : 0;
+  uint4 *tail_t = ldx;
+  if (TAIL && tn > 0 && wave == 0) stage_k_wave<KF, PG>(tail_t, sm, nkv, g, NT, tn, 0);
   float qv[kGqa][kHd / 16];
   load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
   asm volatile("s_nop 4");
 
-  const int vsub = lane % VR::LPR, vkk = lane / VR::LPR;
-  uint4 *kt = lds + wave * 64 * kUPR;
   // VRES: this wave's V rows 32 s + 4 wave + vkk (s < kResVTiles) and their block-pair scale words,
   // loaded right behind the first K tile so that they stream in during the scores
   uint4 vd[VRES ? kResVTiles : 1];
@@ -678,7 +697,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       float acc[kGqa];
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) acc[h] = 0.0f;
-      stage_k_wave<KF, PG>(kt, sm, nkv, g, k0, n, 0);
+      if (r > 0) stage_k_wave<KF, PG>(kt, sm, nkv, g, k0, n, 0);
       if (VRES && r == 0) {
         if constexpr (VRES) load_v_regs<PG, XE>(vd, vsw, xw, xs, sm, nkv, g, nk);
         wait_vm<kVLoads<XE>>();                // the K tile has landed; the V rows stay in flight
@@ -705,31 +724,21 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   }
   // the tail (keys NT .. nk-1, at most kResTail): wave 0, lane = 16 h + t scores key NT + t against
-  // head h, with its own head's q16 broadcast along the lane's DPP row
-  const int tn = TAIL ? max(0, nk - NT) : 0;
+  // head h, with its own head's q16 broadcast along the lane's DPP row (qv[h][j] holds q16[h][16 j +
+  // lane % 16]: the lane's row of head th); its rows were staged with the first tile, so only the V
+  // loads (issued after them) may still be in flight
   const int th = lane >> 4, tt = lane & 15;
   float sct = 0.0f;
   if (TAIL && tn > 0 && wave == 0) {
     float qt[kHd / 16];
-    const float *qh = a.q + ((size_t)g * kGqa + th) * a.qs + tt;
 #pragma unroll
-    for (int j = 0; j < kHd / 16; ++j) qt[j] = round_f16(qh[16 * j]);
+    for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, th, j);
 #pragma unroll
     for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
-    stage_k_wave<KF, PG>(kt, sm, nkv, g, NT, tn, 0);
-    wait_vm<0>();
+    wait_vm<kVLoads<XE>>();
     asm volatile("s_nop 4");
     float acc1 = 0.0f;
-    if (KF == BKV_Q8_0) {
-      qk_row_dot1(kt + tt * kUPR, qt, acc1);
-    } else {
-      qk_f16_half1<0>(kt + tt * kUPR, qt, acc1);
-      wave_lds_sync();
-      stage_k_wave<KF, PG>(kt, sm, nkv, g, NT, tn, 1);
-      wait_vm<0>();
-      qk_f16_half1<1>(kt + tt * kUPR, qt, acc1);
-    }
-    wave_lds_sync();
+    qk_row_dot1(tail_t + tt * kUPR, qt, acc1);
     sct = acc1;
     if (tt < tn)
 #pragma unroll
