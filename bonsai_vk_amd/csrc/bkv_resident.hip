@@ -546,24 +546,35 @@ template <bool DELTA>
 __device__ __forceinline__ void pv_res_slots(const uint4 (&vd)[kResVTiles], const uint32_t (&vsw)[kResVTiles],
                                              const uint2 *p16, const uint2 *q16, int nk, int wave, int vkk,
                                              int vsub, float (&acc)[kGqa][KRow<BKV_Q8_0>::EPL]) {
+  // each slot's probabilities are read from LDS one slot ahead (a read and its wait back to back
+  // would stall every slot); keys past nk get zero weights by a select, not a branch
+  const int kw = wave * 4 + vkk;
+  uint2 pn = p16[kw], qn = DELTA ? q16[kw] : make_uint2(0u, 0u);
 #pragma unroll
   for (int s = 0; s < kResVTiles; ++s) {
-    if (s * 32 < nk) {
-      const int k = s * 32 + wave * 4 + vkk;
-      const uint2 pw = k < nk ? p16[k] : make_uint2(0u, 0u);
-      float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
-                       f16_to_f32(pw.y >> 16)};
-      if constexpr (DELTA) {
-        const uint2 qw = k < nk ? q16[k] : make_uint2(0u, 0u);
-        if (!__any(pw.x != qw.x || pw.y != qw.y)) continue;
-        p[0] -= f16_to_f32(qw.x & 0xFFFFu);
-        p[1] -= f16_to_f32(qw.x >> 16);
-        p[2] -= f16_to_f32(qw.y & 0xFFFFu);
-        p[3] -= f16_to_f32(qw.y >> 16);
-      }
-      const float vsc = k < nk ? f16_to_f32(((vsub >> 1) & 1) ? (vsw[s] >> 16) : (vsw[s] & 0xFFFFu)) : 0.0f;
-      v_accum<BKV_Q8_0>(vd[s], vsc, p, acc);
+    if (s * 32 >= nk) break;
+    const int k = s * 32 + kw;
+    const bool live = k < nk;
+    uint2 pw = pn, qw = qn;
+    if (s + 1 < kResVTiles) {
+      pn = p16[k + 32];
+      if constexpr (DELTA) qn = q16[k + 32];
     }
+    pw.x = live ? pw.x : 0u;
+    pw.y = live ? pw.y : 0u;
+    float p[kGqa] = {f16_to_f32(pw.x & 0xFFFFu), f16_to_f32(pw.x >> 16), f16_to_f32(pw.y & 0xFFFFu),
+                     f16_to_f32(pw.y >> 16)};
+    if constexpr (DELTA) {
+      qw.x = live ? qw.x : 0u;
+      qw.y = live ? qw.y : 0u;
+      if (!__any(pw.x != qw.x || pw.y != qw.y)) continue;
+      p[0] -= f16_to_f32(qw.x & 0xFFFFu);
+      p[1] -= f16_to_f32(qw.x >> 16);
+      p[2] -= f16_to_f32(qw.y & 0xFFFFu);
+      p[3] -= f16_to_f32(qw.y >> 16);
+    }
+    const float vsc = live ? f16_to_f32(((vsub >> 1) & 1) ? (vsw[s] >> 16) : (vsw[s] & 0xFFFFu)) : 0.0f;
+    v_accum<BKV_Q8_0>(vd[s], vsc, p, acc);
   }
 }
 
