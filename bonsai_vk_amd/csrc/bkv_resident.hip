@@ -1143,27 +1143,46 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   }
   RTS(13);
   RTSW(15, 7);
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h)
+  // the 4 row groups' sums: q8_0 V (16-lane rows) by a reduce-scatter that leaves row group r with
+  // head r's totals in red[i]; fp16 V (two 32-lane rows) by one swap, both rows with every head
+  float red[VR::EPL];
+  if constexpr (VR::LPR == 16) {
 #pragma unroll
     for (int i = 0; i < VR::EPL; ++i) {
-      float v = acc[h][i];
-      if (VR::LPR == 16) {
-        v = sum4rows(v);
-      } else {
-        const auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(a2[0]) + __uint_as_float(a2[1]);
-      }
-      acc[h][i] = v;
+      // permlane32_swap(x, y) pairs lanes l < 32 of y with lanes l + 32 of x: the two halves' sums
+      // of head 0 (head 1) land in lanes 0-31, those of head 2 (head 3) in lanes 32-63
+      const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][i]), __float_as_uint(acc[2][i]), false, false);
+      const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[1][i]), __float_as_uint(acc[3][i]), false, false);
+      const float za = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+      const float zb = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+      // permlane16_swap(x, y) pairs odd rows of x with even rows of y: row r then holds head r's sum
+      const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(za), __float_as_uint(zb), false, false);
+      red[i] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
     }
-  RTS(14);
-  __syncthreads();                         // every wave is done with its V rows
-  float *s_red = reinterpret_cast<float *>(lds);   // [NW][kGqa][kHd]
-  if (vkk == 0) {
+  } else {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h)
 #pragma unroll
-      for (int i = 0; i < VR::EPL; ++i) s_red[(wave * kGqa + h) * kHd + vsub * VR::EPL + i] = acc[h][i];
+      for (int i = 0; i < VR::EPL; ++i) {
+        const auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[h][i]), __float_as_uint(acc[h][i]), false, false);
+        acc[h][i] = __uint_as_float(a2[0]) + __uint_as_float(a2[1]);
+      }
+  }
+  RTS(14);
+  __syncthreads();                         // every wave is done with its V rows
+  // [NW][kGqa][EPL][LPR]: element d = LPR-chunk vsub, index i of head h. After the row reduction
+  // every row group holds the sums; row group h writes head h's, one float per lane per store,
+  // consecutive lanes to consecutive words (no bank conflicts)
+  float *s_red = reinterpret_cast<float *>(lds);
+  static_assert(VR::LPR * VR::EPL == kHd && (VR::LPR != 16 || 64 / VR::LPR == kGqa), "partial layout");
+  if constexpr (VR::LPR == 16) {
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + vkk) * VR::EPL + i) * VR::LPR + vsub] = red[i];
+  } else if (vkk == 0) {
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + h) * VR::EPL + i) * VR::LPR + vsub] = acc[h][i];
   }
   __syncthreads();
   // the partial, each element tagged with the call's generation: {float bits, gen} in one 64-bit
@@ -1173,10 +1192,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   {
     static_assert(kGqa * kHd == 2 * NT, "two partial elements per thread");
     float2 v = make_float2(0.0f, 0.0f);
+    const int hh = (2 * tid) / kHd, dd = (2 * tid) % kHd;   // elements (hh, dd) and (hh, dd + 1)
+    const int ro = (hh * VR::EPL + dd % VR::EPL) * VR::LPR + dd / VR::EPL;
 #pragma unroll
     for (int wv = 0; wv < NW; ++wv) {
-      v.x += s_red[wv * kGqa * kHd + 2 * tid];
-      v.y += s_red[wv * kGqa * kHd + 2 * tid + 1];
+      v.x += s_red[wv * kGqa * kHd + ro];
+      v.y += s_red[wv * kGqa * kHd + ro + VR::LPR];
     }
     unsigned long long *dst = part_g + (size_t)wi * kGqa * kHd + 2 * tid;
     st_agent(dst, (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)gen << 32));
