@@ -218,6 +218,27 @@ def test_small_pages(kf, vf, page, path):
         assert oracle.rel_err(out.cpu().numpy(), o2.cpu().numpy()) <= TOL
 
 
+@pytest.mark.parametrize("n", [32768, 33792, 33793])
+def test_register_v_boundary(n):
+    """The resident kernel's q8_0 form keeps a workgroup's V rows in registers up to 512 + 16 keys:
+    32768 keys (no tail), 33792 (the longest tail) and 33793 (the two-pass form) all match the
+    oracle, through decode_step (the appended token lands in the last workgroup's range)."""
+    say(f"register-V boundary n={n}")
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n - 1, seed=31)
+    k, v = oracle.synth_kv(1, 4, 256, 32, 0, outliers=3)
+    q, g = qg(31, 0)
+    host.append(0, n - 1, k, v)
+    want, wg = host.decode(0, n, q, g, nthreads=8)
+    out, og = dev.decode_step(0, n - 1, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                              torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    assert dev.decode_path(n) == 2
+    assert report(f"n={n}", out.cpu().numpy(), want) <= TOL
+    assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
+    assert same_bytes(dev, host) == [0, 0, 0, 0]
+
+
 def test_consecutive_decode_steps(path):
     """BASELINE config 3's pattern at a smaller context: consecutive decode_steps on one workspace
     (each call appends one token and attends over all of them), every step checked against the
