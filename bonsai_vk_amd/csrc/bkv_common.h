@@ -128,16 +128,6 @@ constexpr int kScaleRowBytes = kHd / 32 * 2;   // 8 fp16 = 16 B
 
 namespace bkv {
 
-// fp16 rounding of a wave-uniform value, written in integer arithmetic so that it stays on the
-// scalar unit. Half-normal range: round to nearest even at f32 mantissa bit 13. Everything else
-// (half subnormals, overflow, Inf/NaN) takes the general conversion.
-__device__ __forceinline__ float round_f16_uniform(float x) {
-  const uint32_t u = __float_as_uint(x), a = u & 0x7FFFFFFFu;
-  if (a >= 0x38800000u && a < 0x477FF000u)
-    return __uint_as_float(((a + 0xFFFu + ((a >> 13) & 1u)) & 0xFFFFE000u) | (u & 0x80000000u));
-  return f16_to_f32(f32_to_f16_rne(x));
-}
-
 // exp of a float argument, correctly rounded to float: the value of (float)exp((double)x).
 // Fast path: x = k ln2 + r (|r| <= ln2/2, ln2 split so that k*ln2_hi is exact), exp(r) by its
 // Taylor polynomial to degree 11 in fp64 (truncation < 2^-50, rounding ~2^-52), scaled by 2^k and
@@ -179,15 +169,6 @@ __device__ __forceinline__ T wave_incl_scan(T v, int lane) {
   }
   return v;
 }
-template <typename T>
-__device__ __forceinline__ T wave_incl_max_scan(T v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const T t = __shfl_up(v, o);
-    if (lane >= o) v = v > t ? v : t;
-  }
-  return v;
-}
 // exclusive prefix sum over the workgroup; *total receives the sum. sh: NT/64 scratch slots.
 template <int NT, typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T *sh, T *total) {
@@ -204,22 +185,6 @@ __device__ __forceinline__ T block_excl_scan(T v, T *sh, T *total) {
   __syncthreads();
   *total = tot;
   return base + inc - v;
-}
-// exclusive running max over the workgroup (identity `lo`)
-template <int NT, typename T>
-__device__ __forceinline__ T block_excl_max_scan(T v, T lo, T *sh) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const T inc = wave_incl_max_scan(v, lane);
-  T ex = __shfl_up(inc, 1);
-  if (lane == 0) ex = lo;
-  if (lane == 63) sh[w] = inc;
-  __syncthreads();
-  T base = lo;
-#pragma unroll
-  for (int i = 0; i < NT / 64; ++i)
-    if (i < w) base = base > sh[i] ? base : sh[i];
-  __syncthreads();
-  return base > ex ? base : ex;
 }
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float *sh) {

@@ -372,33 +372,6 @@ __device__ __forceinline__ T wave_incl_scan_dpp(T v) {
   v += dpp0<0x143, 0xC>(v);
   return v;
 }
-// K exclusive prefix sums over the workgroup at once, totals in tot; sh: kResNW * K slots.
-// Exact for integer-valued doubles below 2^53; for floats the order of the additions is free.
-template <int K, typename T>
-__device__ __forceinline__ void block_excl_scan_dpp(const T (&v)[K], T (&ex)[K], T (&tot)[K], T *sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  T inc[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) inc[k] = wave_incl_scan_dpp(v[k]);
-  if (lane == 63)
-#pragma unroll
-    for (int k = 0; k < K; ++k) sh[wave * K + k] = inc[k];
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    T base = 0, t = 0;
-#pragma unroll
-    for (int i = 0; i < kResNW; ++i) {
-      const T x = sh[i * K + k];
-      if (i < wave) base += x;
-      t += x;
-    }
-    ex[k] = base + inc[k] - v[k];
-    tot[k] = t;
-  }
-  __syncthreads();
-}
-
 // one query head's score of one key (the tail): as qk_row_dot, with qt[j] = q16[h][16j + lane%16]
 // for the head h of the lane's DPP row
 __device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
@@ -421,18 +394,6 @@ __device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[
     acc = __fadd_rn(acc, __fmul_rn(sc, inner));
   }
 }
-template <int CH>
-__device__ __forceinline__ void qk_f16_half1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
-    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
-    Dot16<16>::run(acc, qt[CH * 8 + j], x);
-  }
-}
 // inclusive prefix sum inside each DPP row of 16 lanes
 template <typename T>
 __device__ __forceinline__ T row_incl_scan_dpp(T v) {
@@ -441,14 +402,6 @@ __device__ __forceinline__ T row_incl_scan_dpp(T v) {
   v += dpp0<0x114, 0xF>(v);
   v += dpp0<0x118, 0xF>(v);
   return v;
-}
-
-// the sum over the four DPP rows (lanes l, l^16, l^32, l^48) in every lane
-__device__ __forceinline__ float sum4rows(float v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // classify (bkv_device.h) without branches, the increment as an exact double
