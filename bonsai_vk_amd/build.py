@@ -1,6 +1,8 @@
 """Build libbkv.so (the gfx950 KV-cache path) in-tree with hipcc.
 
-    python -m bonsai_vk_amd.build        # or bonsai_vk_amd.build.build()
+    python -m bonsai_vk_amd.build               # or bonsai_vk_amd.build.build()
+    python -m bonsai_vk_amd.build --timestamps  # libbkv_ts.so: the decode kernel records per-phase
+                                                # clocks (read by bonsai_vk_amd.phase_times)
 """
 import os
 import subprocess
@@ -9,6 +11,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbkv.so")
+LIB_TS = os.path.join(HERE, "libbkv_ts.so")
 SOURCES = ["bkv_api.cpp", "bkv_decode.hip", "bkv_fused.hip", "bkv_resident.hip", "bkv_prefill.hip", "bkv_norm_rope.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -22,12 +25,14 @@ FLAGS = [
 ]
 
 
-def build(verbose=False, jobs=None):
-    """Compile every source to an object in parallel (under bonsai_vk_amd/_build), then link."""
+def build(verbose=False, jobs=None, timestamps=False):
+    """Compile every source to an object in parallel (under bonsai_vk_amd/_build), then link.
+    timestamps: the instrumented library libbkv_ts.so instead (objects under _build_ts)."""
     from concurrent.futures import ThreadPoolExecutor
-    obj_dir = os.path.join(HERE, "_build")
+    obj_dir = os.path.join(HERE, "_build_ts" if timestamps else "_build")
+    out = LIB_TS if timestamps else LIB
     os.makedirs(obj_dir, exist_ok=True)
-    cflags = [f for f in FLAGS if f != "-shared"]
+    cflags = [f for f in FLAGS if f != "-shared"] + (["-DBKV_EXPERIMENT_TS"] if timestamps else [])
 
     def compile_one(src):
         obj = os.path.join(obj_dir, src + ".o")
@@ -44,14 +49,14 @@ def build(verbose=False, jobs=None):
         if r.returncode != 0:
             sys.stderr.write(r.stdout + r.stderr)
             raise RuntimeError(f"hipcc failed compiling {os.path.basename(obj)}")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", LIB + ".tmp"] + [o for o, _ in results]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", "-o", out + ".tmp"] + [o for o, _ in results]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed linking libbkv.so")
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+        raise RuntimeError(f"hipcc failed linking {os.path.basename(out)}")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, timestamps="--timestamps" in sys.argv[1:]))

@@ -1,0 +1,70 @@
+"""Per-phase clocks of the resident decode kernel (one launch per layer), for finding where a
+layer's time goes. Needs the instrumented build:
+
+    python -m bonsai_vk_amd.build --timestamps
+    BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so python -m bonsai_vk_amd.phase_times [ctx] [--paged]
+
+With BKV_EXPERIMENT_TS every workgroup's thread 0 writes the GPU wall clock (100 MHz) at each phase
+boundary into the workspace at byte 131072 ([workgroup][16] u32). The probe runs six decode_steps
+of one q8_0 layer at ctx keys (256-token pages with --paged), and prints min / median / max over
+the workgroups of the last call, in microseconds from the first workgroup's start.
+"""
+import sys
+
+import numpy as np
+import torch
+
+from bonsai_vk_amd import BKV_Q8_0, KvCache
+
+# slot -> phase, in launch order (slot 15 is wave 7's end of PV; the others are thread 0's)
+PHASES = [(0, "start"), (1, "scores done (wave 0)"), (2, "barrier A passed"), (10, "e main pass"),
+          (11, "e tail + p16'"), (3, "records stored"), (4, "barrier B passed"), (5, "walk done"),
+          (12, "p16 done"), (13, "PV done (wave 0)"), (15, "PV done (wave 7)"), (14, "PV rows reduced"),
+          (6, "partials stored"), (7, "merge polled"), (8, "end")]
+TS_WORD = 131072 // 4
+
+
+def probe(ctx=32768, paged=False, calls=6):
+    """Timestamps [workgroups][16] (raw 100 MHz clocks) of the last of `calls` decode_steps."""
+    if paged:
+        npg = (ctx + calls + 255) // 256
+        bt = np.random.default_rng(3).permutation(npg).astype(np.int32)[None]
+        cache = KvCache(n_layers=1, cap=npg * 256, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=ctx + calls,
+                        page_tokens=256, max_pages=npg, block_table=bt)
+    else:
+        cache = KvCache(n_layers=1, cap=ctx + calls, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=ctx + calls)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    for s in range(0, ctx, 8192):
+        e = min(ctx, s + 8192)
+        cache.append(0, s, torch.randn(e - s, 4, 256, generator=g, device="cuda"),
+                     torch.randn(e - s, 4, 256, generator=g, device="cuda") * 0.5)
+    k = torch.randn(1, 4, 256, device="cuda")
+    v = torch.randn(1, 4, 256, device="cuda")
+    q = torch.randn(16, 256, device="cuda")
+    nwg = torch.cuda.get_device_properties(0).multi_processor_count
+    ts = None
+    for i in range(calls):
+        cache.decode_step(0, ctx + i, k, v, q)
+        torch.cuda.synchronize()
+        ts = cache.workspace.view(torch.int32)[TS_WORD:TS_WORD + nwg * 16].cpu().numpy()
+    ts = ts.astype(np.int64).reshape(nwg, 16)
+    if not ts[:, 8].any():
+        raise RuntimeError("no timestamps written: load the instrumented build "
+                           "(BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so after build --timestamps)")
+    return ts[ts[:, 0] != 0]
+
+
+def main(argv):
+    ctx = int(next((a for a in argv if not a.startswith("-")), 32768))
+    ts = probe(ctx, "--paged" in argv)
+    t0 = ts[:, 0].min()
+    print(f"ctx {ctx}{' paged' if '--paged' in argv else ''}: phase clocks in us from the first "
+          f"workgroup's start, min / median / max over {len(ts)} workgroups")
+    for slot, name in PHASES:
+        col = (ts[:, slot] - t0) / 100.0
+        print(f"  {name:22s} {col.min():8.2f} {np.median(col):8.2f} {col.max():8.2f}")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
