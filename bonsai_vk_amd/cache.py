@@ -288,8 +288,20 @@ class KvCache:
         check(lib().bkv_kv_fill_synthetic(ctypes.byref(self.desc), self._stream()), "bkv_kv_fill_synthetic")
 
     def decode_path(self, nfill):
-        """1: fused single launch, 0: split path"""
+        """2: resident single launch (the default), 1: fused single launch, 0: split path"""
         return lib().bkv_decode_path(ctypes.byref(self.desc), nfill)
+
+    def check_workspace(self):
+        """bkv_workspace_error on the decode workspace (synchronises the stream): raises BkvError
+        (BKV_ETIMEOUT) if a decode since the last check gave up waiting, and clears the flag."""
+        check(lib().bkv_workspace_error(ctypes.byref(self.desc), self.workspace.data_ptr(),
+                                        self.workspace.numel(), self._stream()), "bkv_workspace_error")
+
+    def error_word_offsets(self):
+        """Byte offsets of the resident and fused kernels' error words in the workspace."""
+        out = (ctypes.c_uint64 * 2)()
+        check(lib().bkv_error_words(ctypes.byref(self.desc), out), "bkv_error_words")
+        return int(out[0]), int(out[1])
 
     # ---------------------------------------------------------------- inspection
     def debug_intermediates(self, nfill):

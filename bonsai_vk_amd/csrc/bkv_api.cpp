@@ -618,8 +618,45 @@ const char *bkv_strerror(int err) {
     case BKV_EWORKSPACE: return "workspace missing or smaller than bkv_workspace_bytes()";
     case BKV_EHIP: return "HIP runtime error (see bkv_last_hip_error)";
     case BKV_EUNSUPPORTED: return "shape not supported by the gfx950 kernels (hd 256, nh = 4*nkv)";
+    case BKV_ETIMEOUT: return "a decode kernel's workgroup wait timed out (its output is not valid)";
     default: return "unknown error";
   }
+}
+
+// byte offsets of the resident and fused kernels' error words (see their sync-line layouts)
+static void error_word_offsets(int nkv, uint64_t out[2]) {
+  out[0] = kResSyncOffset + (uint64_t)nkv * kResGroupLines * kCounterStride * sizeof(unsigned);
+  out[1] = ((uint64_t)nkv * kGroupLines + 10) * kCounterStride * sizeof(unsigned);
+}
+
+int bkv_error_words(const bkv_cache_desc *d, uint64_t out[2]) {
+  const int rc = check(d);
+  if (rc) return rc;
+  if (!out) return BKV_EINVAL;
+  error_word_offsets(d->nkv, out);
+  return BKV_OK;
+}
+
+int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  const int rc = check(d);
+  if (rc) return rc;
+  if (!workspace || ws_bytes < kSyncBytes) return BKV_EWORKSPACE;
+  uint64_t off[2];
+  error_word_offsets(d->nkv, off);
+  hipError_t e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e);
+  int result = BKV_OK;
+  for (uint64_t o : off) {
+    unsigned v = 0;
+    char *p = static_cast<char *>(workspace) + o;
+    if ((e = hipMemcpy(&v, p, sizeof v, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e);
+    if (v) {
+      const unsigned zero = 0;
+      if ((e = hipMemcpy(p, &zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e);
+      result = BKV_ETIMEOUT;
+    }
+  }
+  return result;
 }
 
 int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {

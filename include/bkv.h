@@ -46,7 +46,8 @@ enum bkv_err {
   BKV_EALIGN      = -4,  /* a device pointer not 16-byte aligned                                */
   BKV_EWORKSPACE  = -5,  /* workspace NULL or smaller than bkv_workspace_bytes()                */
   BKV_EHIP        = -6,  /* the HIP runtime reported an error on launch                         */
-  BKV_EUNSUPPORTED = -7  /* a valid request this build does not implement                       */
+  BKV_EUNSUPPORTED = -7, /* a valid request this build does not implement                       */
+  BKV_ETIMEOUT    = -8   /* a decode kernel's bounded wait gave up (bkv_workspace_error)        */
 };
 
 /* bkv_workspace_bytes() op codes */
@@ -175,6 +176,18 @@ int bkv_decode_step_qg(const bkv_cache_desc *d, int layer, uint32_t pos, const f
 int bkv_attn_prefill_chunk_qg(const bkv_cache_desc *d, int layer, uint32_t pos0, int n_q,
                               const float *qg, float *out, float *out_gated, void *workspace,
                               size_t ws_bytes, hipStream_t stream);
+
+/* Whether a decode on this workspace gave up waiting (no counterpart in the reference, whose
+ * Vulkan fences abort on a device loss; for callers that check their results). The single-launch
+ * decode kernels synchronise their workgroups with bounded polls. A poll that runs out (the grid
+ * was not co-resident, e.g. another kernel held CUs) sets an error word in the workspace, and that
+ * call's output is not valid. This synchronises `stream`, returns BKV_ETIMEOUT if any error word
+ * is set (and clears them), else BKV_OK. */
+int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Diagnostics: byte offsets in the workspace of the error words bkv_workspace_error reads
+ * (out[0]: resident kernel, out[1]: fused kernel). */
+int bkv_error_words(const bkv_cache_desc *d, uint64_t out[2]);
 
 /* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
  * single launch (one workgroup per CU, the default), 1 = the older fused single launch, 0 = the

@@ -239,6 +239,27 @@ def test_register_v_boundary(n):
     assert same_bytes(dev, host) == [0, 0, 0, 0]
 
 
+def test_workspace_error_flag():
+    """bkv_workspace_error: clean after ordinary decodes; reports BKV_ETIMEOUT (and clears it) for
+    an error word set from the host, for the resident and the fused kernel's word."""
+    from bonsai_vk_amd import BkvError
+    dev, host = pair(1, 600, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, 600, seed=41)
+    q, _ = qg(41, 0)
+    dev.decode(0, 600, torch.from_numpy(q).cuda())
+    dev.check_workspace()
+    for off in dev.error_word_offsets():
+        dev.workspace[off:off + 4].view(torch.int32).fill_(1)
+        with pytest.raises(BkvError) as e:
+            dev.check_workspace()
+        assert e.value.code == -8
+        dev.check_workspace()                 # cleared
+    out, _ = dev.decode(0, 600, torch.from_numpy(q).cuda())
+    want, _ = host.decode(0, 600, q, nthreads=8)
+    assert report("after the error check", out.cpu().numpy(), want) <= TOL
+    dev.check_workspace()
+
+
 def test_consecutive_decode_steps(path):
     """BASELINE config 3's pattern at a smaller context: consecutive decode_steps on one workspace
     (each call appends one token and attends over all of them), every step checked against the
