@@ -327,10 +327,11 @@ def main():
         "metric": "us/token decode attn+KV append at 32K ctx (8 layers); achieved HBM GB/s % peak",
         "value": round(ms_step * 1e3, 3), "unit": "us/token", "n_gpus": 1, "steps": K,
         "warmup": W, "ms_per_step": round(ms_step, 5), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 cache, fp32 accumulate",
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded torch.randn K/V/Q, 3 outlier K channels x8 per layer/head)",
         "config": {"workload": "bkv_decode_step x 8 layers, q8_0 K+V, keys 32769..32768+steps "
                                "(BASELINE config 3)", "ctx": ctx, "layers": L, "nh": 16, "nkv": 4,
+                   "kv_format": "q8_0 K+V (fp32 scores and accumulation, fp64 exact-sum bookkeeping)",
                    "hd": 256, "gate": bool(args.gate)},
         "achieved_gbs_step": round(bytes_step / (ms_step / 1e3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": kernel_name(cache, ns[0]),
