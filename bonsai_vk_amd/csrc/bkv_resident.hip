@@ -835,6 +835,15 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   }
   RTS(10);
+  // TAIL: the passes' specials go out now, so that their stores have landed by the time the record
+  // (which must not be seen before them) is written after the tail
+  int ns_main = 0;
+  if constexpr (TAIL) __syncthreads();     // s_spec holds every pass's specials
+  if (TAIL && wave < kGqa) {
+    const int h = wave;
+    ns_main = min(pick4(nspc, h), kMaxSpecial);
+    if (lane < ns_main) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
+  }
   // the tail's steps come after every key of the passes: wave 0 places them with DPP-row scans
   // (lane 16 h + t: key NT + t, head h) on the running sums carried so far
   float evt = 0.0f;
@@ -912,7 +921,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // barrier B waits for
   if (wave < kGqa) {
     const int h = wave, ns = min(pick4(nspc, h), kMaxSpecial);
-    if (lane < ns) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
+    if (lane >= ns_main && lane < ns) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
     if (ns > 0) __builtin_amdgcn_s_waitcnt(0);   // the specials are visible before the record is
     if (lane == 0) {
       ChunkRec rc;
