@@ -116,6 +116,26 @@ def test_config5_sampled_rows():
     assert worst <= TOL
 
 
+def test_config5_full_layer():
+    """BASELINE config 5 at its true shape for one layer, every row: 512 queries appended onto 8192
+    cached tokens (q8_0 K+V, seed 4, prefill_step: the chunk's K/V appended, then its attention),
+    all 512 x 16 output rows and the gated rows against the oracle's prefill."""
+    pos0, n_q = 8192, 512
+    dev, host = pair(1, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, pos0, seed=4, outliers=0)
+    k, v = oracle.synth_kv(n_q, 4, 256, 4, 0, outliers=0, stream_base=70000)
+    q, g = qg(4, 0, n=n_q)
+    host.append(0, pos0, k, v)
+    want, wg = host.prefill(0, pos0, q, g, nthreads=16)
+    out, og = dev.prefill_step(0, pos0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                               torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    from tests.gpu_util import same_bytes
+    assert not any(same_bytes(dev, host))
+    assert report("config5 all rows", out.cpu().numpy(), want) <= TOL
+    assert report("config5 all rows, gated", og.cpu().numpy(), wg) <= TOL
+
+
 def test_prefill_errors():
     from bonsai_vk_amd import BkvError
     dev, _ = pair(1, 100, BKV_Q8_0, BKV_Q8_0)
