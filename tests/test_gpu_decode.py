@@ -239,6 +239,36 @@ def test_register_v_boundary(n):
     assert same_bytes(dev, host) == [0, 0, 0, 0]
 
 
+@pytest.mark.parametrize("kf,vf", [(BKV_F16, BKV_Q8_0), (BKV_Q8_0, BKV_F16)])
+def test_mixed_formats_multipass(kf, vf):
+    """Mixed K/V formats beyond the register-V range: 40000 keys (the resident kernel's two-pass
+    form), against the oracle."""
+    n = 40000
+    dev, host = pair(1, n, kf, vf)
+    fill(dev, host, 0, n, seed=44)
+    q, g = qg(44, 0)
+    want, wg = host.decode(0, n, q, g, nthreads=8)
+    out, og = dev.decode(0, n, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    assert dev.decode_path(n) == 2
+    assert report(f"mixed kf={kf} vf={vf} n={n}", out.cpu().numpy(), want) <= TOL
+    assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
+
+
+@pytest.mark.parametrize("n,path_want", [(131072, 2), (131073, 0)])
+def test_longest_resident_context(n, path_want):
+    """64 x 4 x 512 = 131072 keys is the longest context the resident kernel holds (four passes per
+    workgroup); one more key takes the split path. Both match the oracle."""
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n, seed=45, chunk=16384)
+    q, _ = qg(45, 0)
+    want, _ = host.decode(0, n, q, nthreads=8)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    assert dev.decode_path(n) == path_want
+    assert report(f"n={n} path={path_want}", out.cpu().numpy(), want) <= TOL
+
+
 def test_workspace_error_flag():
     """bkv_workspace_error: clean after ordinary decodes; reports BKV_ETIMEOUT (and clears it) for
     an error word set from the host, for the resident and the fused kernel's word."""
