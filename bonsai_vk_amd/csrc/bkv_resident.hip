@@ -534,9 +534,11 @@ __device__ __forceinline__ void pv_res_slots(const uint4 (&vd)[kResVTiles], cons
 template <int KF, int VF, bool VRES, bool PG>
 __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   constexpr int NT = kResNT, NW = kResNW;
-  // VRES: one pass of NT keys plus a tail of at most kResTail keys (wave 0, one lane per key and head)
+  // VRES: one pass of NT keys plus a tail of at most kResTail keys (wave 0, one lane per key and head).
+  // The multi-pass form (q8_0 K) also ends in a tail when the keys past its whole passes are at most
+  // kResTail, instead of a pass for them.
   constexpr int MP = VRES ? 1 : kResMaxPass;
-  constexpr bool TAIL = VRES;
+  constexpr bool TAIL = VRES || KF == BKV_Q8_0;
   constexpr int SB = MP * NT + (TAIL ? kResTail : 0);   // binade-map row per head
   using VR = KRow<VF>;
   static_assert(!VRES || (VF == BKV_Q8_0 && KF == BKV_Q8_0), "register V rows and the tail: q8_0 K and V only");
@@ -629,9 +631,14 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   const int n_first = (int)max((int64_t)0, min((int64_t)64, ke - (kb + wave * 64)));
   if (n_first > 0) stage_k_wave<KF, PG>(kt, sm, nkv, g, wave * 64, n_first, 0);
   // the tail's rows (keys NT .., wave 0) into the exchange area, free until the e phase
-  const int tn = TAIL ? max(0, nk - NT) : 0;
+  // tb: the keys the passes cover, and the first tail key (the tail holds keys tb .. nk-1); the
+  // forms whose tail is fixed keep constants (VRES: one pass, its tail starts at NT; no tail: nk)
+  constexpr bool MTAIL = TAIL && !VRES;
+  const int tb = MTAIL ? (nk > NT && nk % NT <= kResTail ? nk - nk % NT : nk) : VRES ? NT : nk;
+  const int tpk = MTAIL ? tb : nk;         // pass keys are those below tpk
+  const int tn = TAIL ? max(0, nk - tb) : 0;
   uint4 *tail_t = ldx;
-  if (TAIL && tn > 0 && wave == 0) stage_k_wave<KF, PG>(tail_t, sm, nkv, g, NT, tn, 0);
+  if (TAIL && tn > 0 && wave == 0) stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 0);
   float qv[kGqa][kHd / 16];
   load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
   asm volatile("s_nop 4");
@@ -656,7 +663,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     for (int h = 0; h < kGqa; ++h) sc[r][h] = 0.0f;
     const int64_t j0 = kb + (int64_t)r * NT + wave * 64;
     const int k0 = r * NT + wave * 64;
-    const int n = (int)max((int64_t)0, min((int64_t)64, ke - j0));
+    const int n = (int)max((int64_t)0, min((int64_t)64, kb + tpk - j0));
     if (n > 0) {
       float acc[kGqa];
 #pragma unroll
@@ -720,7 +727,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     float l = 0.0f;
 #pragma unroll
     for (int r = 0; r < MP; ++r)
-      if (r * NT + tid < nk) l += __expf(sc[r][h] * a.scale - mloc[h]);
+      if (r * NT + tid < tpk) l += __expf(sc[r][h] * a.scale - mloc[h]);
     if (TAIL && wave == 0 && th == h && tt < tn) l += __expf(sct * a.scale - mloc[h]);
     lsum[h] = l;
   }
@@ -767,9 +774,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   for (int r = 0; r < MP; ++r) {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) ev[r][h] = 0.0f;
-    if (r * NT < nk) {
+    if (r * NT < tpk) {
       const int kl = r * NT + tid;
-      const bool valid = kl < nk;
+      const bool valid = kl < tpk;
       const int64_t j = kb + kl;
       // the key's position on the running sum: the fp64 start of this workgroup plus an fp32
       // exclusive scan inside it (relative error ~1e-7, far inside the classification margin)
@@ -838,8 +845,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // TAIL: the passes' specials go out now, so that their stores have landed by the time the record
   // (which must not be seen before them) is written after the tail
   int ns_main = 0;
-  if constexpr (TAIL) __syncthreads();     // s_spec holds every pass's specials
-  if (TAIL && wave < kGqa) {
+  if (TAIL && tn > 0) __syncthreads();    // s_spec holds every pass's specials (tn: uniform)
+  if (TAIL && tn > 0 && wave < kGqa) {
     const int h = wave;
     ns_main = min(pick4(nspc, h), kMaxSpecial);
     if (lane < ns_main) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
@@ -861,7 +868,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         for (int h = 1; h < kGqa; ++h)
           if (th == h) { Mt = Mh[h]; ct = carry[h]; it = itot[h]; ns = nspc[h]; }
         evt = valid ? exp_cr(sct * a.scale - Mt) : 0.0f;
-        if (valid && a.keep_e) a.e[(size_t)(g * kGqa + th) * a.ld + kb + NT + tt] = evt;
+        if (valid && a.keep_e) a.e[(size_t)(g * kGqa + th) * a.ld + kb + tb + tt] = evt;
         const float fin = row_incl_scan_dpp(evt);
         const double ab = ct + (double)(fin - evt);
         bool sp;
@@ -870,7 +877,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         classify_d(ab, ab + (double)evt, evt, sp, bin, dinc);
         sp = sp && valid;
         if (!valid) dinc = 0.0;
-        s_bin[th * SB + NT + tt] = (valid && !sp) ? (int8_t)bin : kNoBin8;
+        s_bin[th * SB + tb + tt] = (valid && !sp) ? (int8_t)bin : kNoBin8;
         wave_lds_sync();
         const unsigned long long msk = __ballot(sp);
         const unsigned rowm = (unsigned)(msk >> (16 * th)) & 0xFFFFu;
@@ -878,12 +885,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         if (sp) {
           const int id = ns + __popc(rowm & ((1u << tt) - 1u));
           if (id < kMaxSpecial) {
-            const int8_t bp8 = s_bin[th * SB + NT + tt - 1];
+            const int8_t bp8 = s_bin[th * SB + tb + tt - 1];
             const int bprev = bp8 == kNoBin8 ? kNoBinade : bp8;
             Special x;
             x.ipre = it + (long long)(din - dinc);
             x.e = evt;
-            x.meta = (NT + tt) | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+            x.meta = (tb + tt) | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
             s_spec[th * kMaxSpecial + id] = x;
           }
         }
@@ -981,10 +988,10 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     if (!a.keep_e) {
 #pragma unroll
       for (int r = 0; r < MP; ++r)
-        if (r * NT + tid < nk)
+        if (r * NT + tid < tpk)
 #pragma unroll
           for (int h = 0; h < kGqa; ++h) a.e[(size_t)(g * kGqa + h) * a.ld + kb + r * NT + tid] = ev[r][h];
-      if (TAIL && wave == 0 && tt < tn) a.e[(size_t)(g * kGqa + th) * a.ld + kb + NT + tt] = evt;
+      if (TAIL && wave == 0 && tt < tn) a.e[(size_t)(g * kGqa + th) * a.ld + kb + tb + tt] = evt;
     }
     __threadfence();
     group_barrier(cnt + 3 * kCounterStride, (unsigned)G, err);
@@ -1016,11 +1023,11 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     for (int h = 0; h < kGqa; ++h) S[h] = s_S[h];
 #pragma unroll
     for (int r = 0; r < MP; ++r) {
-      if (r * NT < nk) {
+      if (r * NT < tpk) {
         const int kl = r * NT + tid;
         _Float16 pk[kGqa];
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h) pk[h] = (_Float16)(kl < nk ? ev[r][h] / S[h] : 0.0f);
+        for (int h = 0; h < kGqa; ++h) pk[h] = (_Float16)(kl < tpk ? ev[r][h] / S[h] : 0.0f);
         uint2 pw;
         pw.x = (uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16);
         pw.y = (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16);
@@ -1032,7 +1039,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 #pragma unroll
       for (int h = 1; h < kGqa; ++h)
         if (th == h) St = S[h];
-      reinterpret_cast<_Float16 *>(s_p16 + NT + tt)[th] = (_Float16)(evt / St);
+      reinterpret_cast<_Float16 *>(s_p16 + tb + tt)[th] = (_Float16)(evt / St);
     }
   }
   __syncthreads();
