@@ -394,6 +394,18 @@ __device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[
     acc = __fadd_rn(acc, __fmul_rn(sc, inner));
   }
 }
+template <int CH>
+__device__ __forceinline__ void qk_f16_half1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+    Dot16<16>::run(acc, qt[CH * 8 + j], x);
+  }
+}
 // inclusive prefix sum inside each DPP row of 16 lanes
 template <typename T>
 __device__ __forceinline__ T row_incl_scan_dpp(T v) {
@@ -535,10 +547,10 @@ template <int KF, int VF, bool VRES, bool PG>
 __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   constexpr int NT = kResNT, NW = kResNW;
   // VRES: one pass of NT keys plus a tail of at most kResTail keys (wave 0, one lane per key and head).
-  // The multi-pass form (q8_0 K) also ends in a tail when the keys past its whole passes are at most
+  // The multi-pass form also ends in a tail when the keys past its whole passes are at most
   // kResTail, instead of a pass for them.
   constexpr int MP = VRES ? 1 : kResMaxPass;
-  constexpr bool TAIL = VRES || KF == BKV_Q8_0;
+  constexpr bool TAIL = true;
   constexpr int SB = MP * NT + (TAIL ? kResTail : 0);   // binade-map row per head
   using VR = KRow<VF>;
   static_assert(!VRES || (VF == BKV_Q8_0 && KF == BKV_Q8_0), "register V rows and the tail: q8_0 K and V only");
@@ -709,7 +721,15 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     wait_vm<kVLoads<XE>>();
     asm volatile("s_nop 4");
     float acc1 = 0.0f;
-    qk_row_dot1(tail_t + tt * kUPR, qt, acc1);
+    if constexpr (KF == BKV_Q8_0) {
+      qk_row_dot1(tail_t + tt * kUPR, qt, acc1);
+    } else {                               // fp16 rows: the second half row follows the first
+      qk_f16_half1<0>(tail_t + tt * kUPR, qt, acc1);
+      wave_lds_sync();
+      stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 1);
+      wait_vm<0>();
+      qk_f16_half1<1>(tail_t + tt * kUPR, qt, acc1);
+    }
     sct = acc1;
     if (tt < tn)
 #pragma unroll
