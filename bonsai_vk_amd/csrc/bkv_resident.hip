@@ -203,6 +203,32 @@ __device__ __forceinline__ void qk_f16_half(const uint4 *row, const float (&qv)[
 // ---------------------------------------------------------------- the walk (one wave, one head)
 // walk_heads (bkv_device.h) for a group of at most 64 workgroups whose records the wave already
 // holds (lane c: record of workgroup c, valid for c < gg).
+// inclusive prefix sums over the wave by DPP row shifts and row broadcasts (no LDS round trips);
+// lanes whose source lies outside the pattern read 0. 64-bit values move as two 32-bit halves.
+template <int CTRL, int RM>
+__device__ __forceinline__ long long dpp0_i64(long long v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, RM, 0xF, false);
+  return ((long long)hi << 32) | (long long)(unsigned)lo;
+}
+__device__ __forceinline__ long long wave_scan_i64(long long v) {
+  v += dpp0_i64<0x111, 0xF>(v);
+  v += dpp0_i64<0x112, 0xF>(v);
+  v += dpp0_i64<0x114, 0xF>(v);
+  v += dpp0_i64<0x118, 0xF>(v);
+  v += dpp0_i64<0x142, 0xA>(v);
+  v += dpp0_i64<0x143, 0xC>(v);
+  return v;
+}
+__device__ __forceinline__ int wave_scan_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
 template <typename WS>
 __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t kpw, int64_t nfill, WS &w,
                          float &s_out, bool &good_out) {
@@ -215,8 +241,8 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
   const long long tot = in ? x.tot : 0;
   const int cnt = in ? min(x.nsp, kMaxSpecial) : 0;
   const bool over = in && x.nsp > kMaxSpecial;
-  const long long incl = wave_incl_scan<long long>(tot, lane);
-  const int oincl = wave_incl_scan<int>(cnt, lane);
+  const long long incl = wave_scan_i64(tot);
+  const int oincl = wave_scan_i32(cnt);
   int bp = __shfl_up(in ? x.blast : kNoBinade, 1);
   if (lane == 0) bp = kNoBinade;
   if (in) {
@@ -224,9 +250,10 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
     w.wg_off[lane] = oincl - cnt;
     w.wg_bp[lane] = bp;
   }
-  const int T0 = __shfl(oincl, 63);
+  const int T0 = __builtin_amdgcn_readlane(oincl, 63);
   if (lane == 0) w.wg_off[gg] = T0;
-  const long long itot = __shfl(incl, 63);
+  const long long itot = ((long long)__builtin_amdgcn_readlane((int)(incl >> 32), 63) << 32) |
+                         (long long)(unsigned)__builtin_amdgcn_readlane((int)incl, 63);
   const int blast_last = __shfl(in ? x.blast : kNoBinade, gg - 1);
   ok = ok && !__any(over) && T0 <= kWalkCap;
   const int T = ok ? T0 : 0;
