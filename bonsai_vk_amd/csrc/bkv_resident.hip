@@ -387,6 +387,10 @@ __device__ __forceinline__ double dpp0(double v) {
   const int lo = dpp0<CTRL, RM>((int)u), hi = dpp0<CTRL, RM>((int)(u >> 32));
   return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
 }
+template <int C, int RM>
+struct DppCtl {
+  static constexpr int c = C, rm = RM;
+};
 // inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 inside each row of 16 lanes, then
 // row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3)
 template <typename T>
@@ -482,11 +486,25 @@ __device__ __forceinline__ void xwave_prefix(const T *sh, int h, int wave, T &be
 }
 
 // the workgroup-wide max / sum of four values at once (every thread receives them)
+// the wave's max (sum) in lane 63: DPP row reductions, then row_bcast 15 into rows 1, 3 and row_bcast
+// 31 into rows 2, 3 (rows a broadcast does not write read the neutral element)
+__device__ __forceinline__ float wave_max_l63(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp((int)0xFF800000u, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp((int)0xFF800000u, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_l63(float v) {
+  v = row16_sum(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+  return v;
+}
 __device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) v[h] = wave_max(v[h]);
-  if (lane == 0)
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_max_l63(v[h]);
+  if (lane == 63)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
   __syncthreads();
@@ -502,8 +520,8 @@ __device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
 __device__ __forceinline__ void block_sum4(float (&v)[kGqa], float *sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) v[h] = wave_sum(v[h]);
-  if (lane == 0)
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_sum_l63(v[h]);
+  if (lane == 63)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
   __syncthreads();
@@ -789,14 +807,24 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     poll_tagged(tstats + wave * GM, 1, 1, G, tag, v, err);
     const float mw = lane < G ? __uint_as_float((unsigned)(v[0] >> 32)) : -INFINITY;
     const float lw = lane < G ? __uint_as_float((unsigned)v[0] & ~3u) : 0.0f;
-    const float m = wave_max(mw);
+    // the max and the prefix sums by DPP (max scan / add scan, then readlane): no LDS round trips
+    // (lanes without a source read -inf)
+    auto dmax = [](float v, auto ctl) {
+      constexpr int C = decltype(ctl)::c, RM = decltype(ctl)::rm;
+      const int ninf = (int)0xFF800000u;
+      return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), C, RM, 0xF, false)));
+    };
+    float mx = mw;
+    mx = dmax(mx, DppCtl<0x111, 0xF>{});
+    mx = dmax(mx, DppCtl<0x112, 0xF>{});
+    mx = dmax(mx, DppCtl<0x114, 0xF>{});
+    mx = dmax(mx, DppCtl<0x118, 0xF>{});
+    mx = dmax(mx, DppCtl<0x142, 0xA>{});
+    mx = dmax(mx, DppCtl<0x143, 0xC>{});
+    const float m = rd_lane(mx, 63);
     const double lx = lane < G ? (double)lw * exp((double)mw - (double)m) : 0.0;
-    double p = lane < wi ? lx : 0.0, t = lx;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      p += __shfl_xor(p, o);
-      t += __shfl_xor(t, o);
-    }
+    const double sx = wave_incl_scan_dpp(lx);
+    const double p = wi > 0 ? rd_lane(sx, wi - 1) : 0.0, t = rd_lane(sx, 63);
     if (lane == 0) {
       s_M[wave] = m;
       s_P0[wave] = p;
