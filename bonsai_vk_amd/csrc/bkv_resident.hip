@@ -254,7 +254,7 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
   if (lane == 0) w.wg_off[gg] = T0;
   const long long itot = ((long long)__builtin_amdgcn_readlane((int)(incl >> 32), 63) << 32) |
                          (long long)(unsigned)__builtin_amdgcn_readlane((int)incl, 63);
-  const int blast_last = __shfl(in ? x.blast : kNoBinade, gg - 1);
+  const int blast_last = __builtin_amdgcn_readlane(in ? x.blast : kNoBinade, gg - 1);
   ok = ok && !__any(over) && T0 <= kWalkCap;
   const int T = ok ? T0 : 0;
   __builtin_amdgcn_wave_barrier();
@@ -969,7 +969,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
             s_spec[th * kMaxSpecial + id] = x;
           }
         }
-        tot_l = (long long)__shfl(din, 16 * th + 15);
+        tot_l = (long long)dpp0<0x15F, 0xF>(din);   // row_newbcast:15, the row's last lane
         tot_c = __popc(rowm);
       }
       if (tt == 0) {
