@@ -36,13 +36,14 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // by a bound that grows monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx.
 // BKV_DECODE selects a decode implementation: "split" (four launches), "fused" (the older single
 // launch) or "resident" (the default). Read on every call, so tests can switch it.
-enum { kPathSplit = 0, kPathFused = 1, kPathResident = 2 };
+enum { kPathSplit = 0, kPathFused = 1, kPathResident = 2, kPathStream = 3 };
 static int forced_path() {
   const char *e = std::getenv("BKV_DECODE");
   if (!e) return -1;
   if (std::strcmp(e, "split") == 0) return kPathSplit;
   if (std::strcmp(e, "fused") == 0) return kPathFused;
   if (std::strcmp(e, "resident") == 0) return kPathResident;
+  if (std::strcmp(e, "stream") == 0) return kPathStream;
   return -1;
 }
 
@@ -154,6 +155,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
   // the resident path: one workgroup per CU, up to kResMaxG per KV group, >= 128 keys each
   // (below 16K keys fewer, longer workgroups finish sooner: 4K keys run 4 % faster at 32 per group than at 64)
   p.rG = 0;
+  p.rvres = p.rstream = false;
   const int rcap = resident_max_workgroups(kfmt, vfmt);
   const bool rsync_fits = kResSyncOffset + ((size_t)nkv * kResGroupLines + 1) * kCounterStride * sizeof(unsigned) <= kSyncBytes;
   const bool rtags_fit = kResTagOffset + (size_t)nh * kResMaxGroupWgs * 3 * sizeof(unsigned long long) <= kResSyncOffset;
@@ -166,6 +168,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
       p.rkpw = (int)kpw;
       p.rG = (int)cdiv(n, kpw);
       p.rvres = vfmt == BKV_Q8_0 && kfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
+      p.rstream = p.rvres && p.rG * nkv <= stream_max_workgroups(page > 0);
       size_t f = kSyncBytes;
       p.r_spec = f;   f += align256((size_t)nh * gmax * kMaxSpecial * sizeof(Special));
       p.r_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
@@ -176,6 +179,10 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
       total = std::max(total, f);
     }
   }
+#ifdef BKV_EXPERIMENT_TS
+  total = align256(total) + 131072;
+  p.ts_off = total - 131072;
+#endif
   p.total = total;
   return p;
 }
@@ -192,6 +199,8 @@ static int choose_path(const DecodePlan &p) {
   const int f = forced_path();
   if (f == kPathSplit) return kPathSplit;
   if (f == kPathFused) return p.gg > 0 ? kPathFused : kPathSplit;
+  if (f == kPathResident && p.rG > 0) return kPathResident;
+  if (p.rstream) return kPathStream;
   if (p.rG > 0) return kPathResident;
   return p.gg > 0 ? kPathFused : kPathSplit;
 }
@@ -290,7 +299,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
   L.base = kstart;
 
   const int path = choose_path(p);
-  if (path == kPathResident) {
+  if (path == kPathResident || path == kPathStream) {
     ResArgs ra{};
     ra.L = L; ra.nkv = d->nkv; ra.nh = d->nh; ra.nfill = nfill; ra.scale = d->scale;
     ra.G = p.rG; ra.kpw = p.rkpw; ra.ld = p.ld; ra.q = q; ra.qs = qs; ra.gs = gs;
@@ -301,13 +310,19 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
     ra.spec = (Special *)(w + p.r_spec);
     ra.e = (float *)(w + p.r_e);
     ra.keep_e = keep_intermediates() ? 1 : 0;
+    {
+      const char *vs = std::getenv("BKV_VSTAGE");
+      ra.vstage = vs ? std::atoi(vs) : 3;
+    }
     ra.sum = (float *)(w + p.r_sum);
     ra.status = (unsigned *)(w + p.r_status);
     ra.part = (unsigned long long *)(w + p.r_part);
     ra.sync = (unsigned *)(w + kResSyncOffset);
 #ifdef BKV_EXPERIMENT_TS
     ra.ts = (unsigned *)w + 32768;
+    ra.tsw = (unsigned *)(w + p.ts_off);
 #endif
+    if (path == kPathStream) return hip_fail(launch_stream(ra, st));
     return hip_fail(launch_resident(ra, d->k_fmt, d->v_fmt, p.rvres, st));
   }
   if (path == kPathFused) {
@@ -668,9 +683,10 @@ int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
   const int path = choose_path(p);
   out[0] = (uint64_t)p.ld;
   out[1] = path == kPathSplit ? p.off_score : 0;
-  out[2] = path == kPathResident ? p.r_e : path == kPathFused ? p.f_e : p.off_e;
-  out[3] = path == kPathResident ? p.r_sum : path == kPathFused ? p.f_sum : p.off_sum;
-  out[4] = path == kPathResident ? p.r_status : path == kPathFused ? p.f_status : p.off_status;
+  const bool res = path == kPathResident || path == kPathStream;
+  out[2] = res ? p.r_e : path == kPathFused ? p.f_e : p.off_e;
+  out[3] = res ? p.r_sum : path == kPathFused ? p.f_sum : p.off_sum;
+  out[4] = res ? p.r_status : path == kPathFused ? p.f_status : p.off_status;
   out[5] = p.total;
   return BKV_OK;
 }

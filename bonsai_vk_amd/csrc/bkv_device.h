@@ -121,6 +121,27 @@ __device__ __forceinline__ void load_q16_rows(const float *q, float (&qv)[kGqa][
 // ascending d (attn_vk.h:156-170). row: the key's LDS row - q8_0: 16 data uint4 then the scale
 // uint4; fp16: 32 data uint4. The caller guarantees at least two VALU cycles between writing qv and
 // this call (DPP source hazard).
+// the 16 steps i of several independent chains interleaved, step by step (chain c: acc[c] =
+// acc[c] + q[c] (broadcast of lane i of the row) * x[c][i]), so that consecutive FMAs never depend on
+// each other; each chain's own order is the reference's ascending one
+template <int C, int I = 0>
+struct DotIl {
+  static __device__ __forceinline__ void run(float (&acc)[C], const float (&q)[C], const float (&x)[C][16]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) fmac_bc<I>(acc[c], q[c], x[c][I]);
+    DotIl<C, I + 1>::run(acc, q, x);
+  }
+};
+template <int C>
+struct DotIl<C, 16> {
+  static __device__ __forceinline__ void run(float (&)[C], const float (&)[C], const float (&)[C][16]) {}
+};
+
+// Scores of one cached key against the group's 4 query heads, each one accumulation chain in
+// ascending d (attn_vk.h:156-170). row: the key's LDS row - q8_0: 16 data uint4 then the scale
+// uint4; fp16: 32 data uint4. The chains of the 4 heads (and, q8_0, of two blocks, whose inner sums
+// are independent) are interleaved. The caller guarantees at least two VALU cycles between writing qv
+// and this call (DPP source hazard).
 template <int KF>
 __device__ __forceinline__ void qk_row_dot(const uint4 *row, const float (&qv)[kGqa][kHd / 16],
                                            float (&acc)[kGqa]) {
@@ -129,37 +150,55 @@ __device__ __forceinline__ void qk_row_dot(const uint4 *row, const float (&qv)[k
   if (KF == BKV_Q8_0) {
     const uint4 scl = row[16];
 #pragma unroll
-    for (int b = 0; b < kHd / 32; ++b) {
-      // the block's two 16-element halves in turn, each head's inner chain continuing across them
-      float inner[kGqa];
+    for (int bp = 0; bp < kHd / 64; ++bp) {
+      // blocks 2 bp and 2 bp + 1: their inner sums over the two 16-element halves, 8 chains
+      float inner[2 * kGqa];
+#pragma unroll
+      for (int c = 0; c < 2 * kGqa; ++c) inner[c] = 0.0f;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const uint4 w = row[2 * b + half];
-        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-        float x[16];
+        float x[2 * kGqa][16], q[2 * kGqa];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = sbyte(u[i >> 2], i & 3);
+        for (int bb = 0; bb < 2; ++bb) {
+          const uint4 w = row[2 * (2 * bp + bb) + half];
+          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          if (half == 0) inner[h] = 0.0f;
-          Dot16<16>::run(inner[h], qv[h][2 * b + half], x);
+          for (int i = 0; i < 16; ++i) x[bb * kGqa][i] = sbyte(u[i >> 2], i & 3);
+#pragma unroll
+          for (int h = 0; h < kGqa; ++h) {
+            q[bb * kGqa + h] = qv[h][2 * (2 * bp + bb) + half];
+            if (h > 0)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) x[bb * kGqa + h][i] = x[bb * kGqa][i];
+          }
         }
+        DotIl<2 * kGqa>::run(inner, q, x);
       }
-      const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
-      const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
 #pragma unroll
-      for (int h = 0; h < kGqa; ++h) acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner[h]));
+      for (int bb = 0; bb < 2; ++bb) {
+        const int b = 2 * bp + bb;
+        const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
+        const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner[bb * kGqa + h]));
+      }
     }
   } else {
 #pragma unroll
     for (int j = 0; j < kHd / 16; ++j) {
       const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
       const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      float x[16];
+      float x[kGqa][16], q[kGqa];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+      for (int i = 0; i < 16; ++i) x[0][i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
 #pragma unroll
-      for (int h = 0; h < kGqa; ++h) Dot16<16>::run(acc[h], qv[h][j], x);   // exact products
+      for (int h = 0; h < kGqa; ++h) {
+        q[h] = qv[h][j];
+        if (h > 0)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) x[h][i] = x[0][i];
+      }
+      DotIl<kGqa>::run(acc, q, x);                  // exact products
     }
   }
 }

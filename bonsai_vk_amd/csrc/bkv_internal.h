@@ -161,6 +161,8 @@ struct ResArgs {
   unsigned long long *part;      // [nkv][G][kGqa][hd] {float bits, call generation}
   unsigned *sync;                // the resident kernel's sync lines
   unsigned *ts;                  // phase timestamps (experiment builds), or null
+  unsigned *tsw;                 // per-wave phase timestamps [workgroup][8 waves][8] (experiment builds)
+  int vstage;                    // stream kernel: when the V waves start their loads (tuning)
 };
 
 // ------------------------------------------------------------------ chunked prefill (MFMA)
@@ -247,8 +249,9 @@ struct DecodePlan {
   size_t f_stats, f_sub, f_rec, f_spec, f_e, f_sum, f_status, f_part, f_total;
   // resident path (rG == 0: not available for this nfill)
   int rG, rkpw;
-  bool rvres;
+  bool rvres, rstream;
   size_t r_spec, r_e, r_sum, r_status, r_part, r_total;
+  size_t ts_off;                 // experiment builds: per-wave timestamps (the last 128 KiB)
 };
 
 DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill, int page = 0);
@@ -259,6 +262,8 @@ int fused_keys_per_pass(int kf);
 hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st);
 int resident_max_workgroups(int kf, int vf);
 hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st);
+int stream_max_workgroups(bool paged);
+hipError_t launch_stream(const ResArgs &a, hipStream_t st);
 hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st);
 hipError_t launch_fill_words(unsigned *p, size_t nwords, unsigned value, hipStream_t st);
 hipError_t launch_append(const AppendArgs &a, int kf, int vf, int n_tok, hipStream_t st);

@@ -1,0 +1,467 @@
+// bkv_res_shared.h - device pieces of the single-launch decode kernels (bkv_resident.hip,
+// bkv_stream.hip): LDS-DMA K staging, tagged cross-workgroup hand-off words and bounded polls, DPP
+// scans and the exact-sum walk over the group's chunk records.
+#pragma once
+
+#include "bkv_common.h"
+#include "bkv_device.h"
+#include "bkv_internal.h"
+
+namespace bkv {
+
+constexpr unsigned kResSpin = 1u << 21;   // polls per wait (seconds) before the error word is set
+constexpr int kUPR = 17;            // LDS uint4 per staged K row: 16 data + the q8_0 scale uint4
+constexpr int kResNW = kResNT / 64;
+constexpr int kResXBytes = 23040;    // LDS beside the K tiles (160 KiB in all)
+constexpr int8_t kNoBin8 = -128;     // kNoBinade in the int8 binade map
+
+#ifdef BKV_EXPERIMENT_TS
+#define RTS(i) do { if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+#define RTSW(i, wv) do { if (threadIdx.x == 64 * (wv) && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+#define RTSV(i) do { if ((threadIdx.x & 63) == 0 && a.tsw) a.tsw[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 + (i)] = (unsigned)wall_clock64(); } while (0)
+#else
+#define RTSV(i) do { } while (0)
+#define RTSW(i, wv) do { } while (0)
+#define RTS(i) do { } while (0)
+#endif
+
+// every LDS access of this wave issued so far has completed, and the compiler keeps memory
+// operations on their side of this point
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Arrive at a group barrier and wait until n workgroups have arrived. Waves below storing_waves
+// first wait for their own stores (write-through stores complete at the device coherence point;
+// the other waves have none this call needs, and their loads stay in flight), then one atomic per
+// workgroup. The wait is bounded: a timeout sets the error word and lets the kernel finish.
+__device__ __forceinline__ void group_barrier(unsigned *cnt, unsigned n, unsigned *err,
+                                              int storing_waves = kResNT / 64) {
+  if ((int)(threadIdx.x >> 6) < storing_waves) __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicAdd(cnt, 1u);
+    unsigned spins = 0;
+    while (ld_agent(cnt) < n) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kResSpin) {
+        atomicOr(err, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Chunk ch of the K rows of this wave's keys j0 .. j0+63 (rows >= n repeat row n-1) into
+// kt[row * kUPR + col]: 16 uint4 per row (q8_0: the whole 256 B row; fp16: half a row), and for
+// q8_0 the row's 16 B of block scales at column 16. Load i reads rows 4i..4i+3, 16 lanes per row.
+// LDS address (32-bit, LDS aperture) of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Cache slots of a workgroup's keys kb + k (0 <= k < nk). Paged: through an LDS copy of the block-
+// table entries its keys span (lut[p - pf] for page p), so that no lookup is a global load (whose
+// wait would also wait for every tile load in flight). The host takes this kernel only when a
+// workgroup's keys span at most kResPgMax pages.
+struct SlotMap {
+  const LayerView *L;
+  int64_t kb;
+  const int *lut;
+  uint32_t pf;
+};
+template <bool PG>
+__device__ __forceinline__ int64_t slot_k(const SlotMap &m, int k) {
+  if constexpr (!PG) {
+    return m.kb + k + m.L->base;
+  } else {
+    const uint32_t pgs = (uint32_t)m.L->page, p = (uint32_t)(m.kb + k + m.L->base), pg = p / pgs;
+    return (int64_t)m.lut[min(pg - m.pf, (uint32_t)kResPgMax - 1u)] * pgs + (int64_t)(p - pg * pgs);
+  }
+}
+
+// k0: the first key (within the workgroup's range) of the n rows staged
+template <int KF, bool PG>
+__device__ __forceinline__ void stage_k_wave(uint4 *kt, const SlotMap &sm, int nkv, int g, int k0,
+                                             int n, int ch) {
+  // direct-to-LDS: load i writes the 64 consecutive tile slots 64 i .. 64 i + 63 (row = slot / kUPR,
+  // column = slot % kUPR); column 16 is the q8_0 scale row (for fp16 K an unused copy of column 0).
+  // Issued as inline asm, so the compiler neither waits for these loads nor counts them: the caller
+  // waits with wait_vm<N>() before reading the tile, N = vector memory operations issued since.
+  const int lane = threadIdx.x & 63;
+  constexpr int RB = row_bytes(KF);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(kt));
+  // q8_0 K: every slot first, so no lookup (an LDS read when paged) sits between the tile loads;
+  // fp16 K, whose scores hold more registers, looks each one up in turn
+  constexpr bool PRE = KF == BKV_Q8_0;
+  uint32_t sls[PRE ? kUPR : 1];
+  if constexpr (PRE)
+#pragma unroll
+    for (int i = 0; i < kUPR; ++i) sls[i] = (uint32_t)slot_k<PG>(sm, k0 + min((64 * i + lane) / kUPR, n - 1));
+#pragma unroll
+  for (int i = 0; i < kUPR; ++i) {
+    const int slotx = 64 * i + lane, row = slotx / kUPR, col = slotx - row * kUPR;
+    const int64_t sl = PRE ? (int64_t)sls[PRE ? i : 0] : slot_k<PG>(sm, k0 + min(row, n - 1));
+    const uint8_t *src = (KF == BKV_Q8_0 && col == 16)
+                             ? sm.L->ks + (sl * nkv + g) * kScaleRowBytes
+                             : sm.L->kd + (sl * nkv + g) * RB + (ch * 16 + (col & 15)) * 16;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(base + 1024u * i) : "memory", "m0");
+  }
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// ---------------------------------------------------------------- the walk (one wave, one head)
+// walk_heads (bkv_device.h) for a group of at most 64 workgroups whose records the wave already
+// holds (lane c: record of workgroup c, valid for c < gg).
+// inclusive prefix sums over the wave by DPP row shifts and row broadcasts (no LDS round trips);
+// lanes whose source lies outside the pattern read 0. 64-bit values move as two 32-bit halves.
+template <int CTRL, int RM>
+__device__ __forceinline__ long long dpp0_i64(long long v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, RM, 0xF, false);
+  return ((long long)hi << 32) | (long long)(unsigned)lo;
+}
+__device__ __forceinline__ long long wave_scan_i64(long long v) {
+  v += dpp0_i64<0x111, 0xF>(v);
+  v += dpp0_i64<0x112, 0xF>(v);
+  v += dpp0_i64<0x114, 0xF>(v);
+  v += dpp0_i64<0x118, 0xF>(v);
+  v += dpp0_i64<0x142, 0xA>(v);
+  v += dpp0_i64<0x143, 0xC>(v);
+  return v;
+}
+__device__ __forceinline__ int wave_scan_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+  return v;
+}
+template <typename WS>
+__device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t kpw, int64_t nfill, WS &w,
+                         float &s_out, bool &good_out, unsigned *tsw = nullptr) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kWalkCap = WS::kCap;
+  static_assert(WS::kWg <= 64, "one record per lane");
+  bool ok = gg <= WS::kWg;
+  // 1. prefix scans over the records
+  const bool in = lane < gg;
+  const long long tot = in ? x.tot : 0;
+  const int cnt = in ? min(x.nsp, kMaxSpecial) : 0;
+  const bool over = in && x.nsp > kMaxSpecial;
+  const long long incl = wave_scan_i64(tot);
+  const int oincl = wave_scan_i32(cnt);
+  int bp = __shfl_up(in ? x.blast : kNoBinade, 1);
+  if (lane == 0) bp = kNoBinade;
+  if (in) {
+    w.wg_ib[lane] = incl - tot;
+    w.wg_off[lane] = oincl - cnt;
+    w.wg_bp[lane] = bp;
+  }
+  const int T0 = __builtin_amdgcn_readlane(oincl, 63);
+  if (lane == 0) w.wg_off[gg] = T0;
+  const long long itot = ((long long)__builtin_amdgcn_readlane((int)(incl >> 32), 63) << 32) |
+                         (long long)(unsigned)__builtin_amdgcn_readlane((int)incl, 63);
+  const int blast_last = __builtin_amdgcn_readlane(in ? x.blast : kNoBinade, gg - 1);
+  ok = ok && !__any(over) && T0 <= kWalkCap;
+  const int T = ok ? T0 : 0;
+  __builtin_amdgcn_wave_barrier();
+  // 2. the specials, resolved to global key index, increment prefix and starting binade
+  for (int o = lane; o < T; o += 64) {
+    int l = 0, hi = gg - 1;
+    while (l < hi) {
+      const int mid = (l + hi + 1) >> 1;
+      if (w.wg_off[mid] <= o) l = mid; else hi = mid - 1;
+    }
+    const Special sx = ld_spec(&spec[(size_t)l * kMaxSpecial + (o - w.wg_off[l])]);
+    const int bf = (sx.meta >> 16) & 0xFF;
+    w.si[o] = w.wg_ib[l] + sx.ipre;
+    w.sk[o] = (int)(l * kpw + (sx.meta & 0xFFFF));
+    w.se[o] = sx.e;
+    w.sck[o] = bf == 255 ? w.wg_bp[l] : (bf == 0 ? kNoBinade : bf - 128);
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (tsw && threadIdx.x == 0) *tsw = (unsigned)wall_clock64();   // (instrumented builds)
+  // 3. per special: the ulps of the segment before it in its binade
+  bool bad = false;
+  for (int o = lane; o < T; o += 64) {
+    const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+    const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+    int du = 0, ck = -1;
+    if (gap > 1) {
+      const int B = w.sck[o];
+      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24)) {
+        bad = true;
+      } else {
+        du = (int)(di >> (B + 17));
+        ck = B + 127;
+      }
+    } else if (di != 0) {
+      bad = true;
+    }
+    w.sdu[o] = du;
+    w.sck[o] = ck;
+  }
+  ok = ok && !__any(bad);
+  const int Tc = ok ? T : 0;
+  __builtin_amdgcn_wave_barrier();
+  // 4. the chain, 16 steps per unrolled block; entries past Tc are du 0, e 0 (no change)
+  float s = 0.0f;
+  bool bad2 = false;
+  for (int base = 0; base < Tc; base += 64) {
+    const int o = base + lane;
+    const bool inn = o < Tc;
+    const int du_l = inn ? w.sdu[o] : 0, ck_l = inn ? w.sck[o] : -1;
+    const float e_l = inn ? w.se[o] : 0.0f;
+    uint32_t pre = 0u;
+    const int n = min(64, Tc - base);
+    for (int j0 = 0; j0 < n; j0 += 16) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = j0 + jj;
+        const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l, j);
+        const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), j));
+        const uint32_t bits = __float_as_uint(s);
+        pre = lane == j ? bits : pre;
+        s = __fadd_rn(__uint_as_float(bits + du), ev);
+      }
+    }
+    if (ck_l >= 0) bad2 |= (int)(pre >> 23) != ck_l || (int)((pre + (uint32_t)du_l) >> 23) != ck_l;
+  }
+  bool good = ok && !__any(bad2);
+  const long long k_last = Tc > 0 ? w.sk[Tc - 1] : -1, i_last = Tc > 0 ? w.si[Tc - 1] : 0;
+  if (good && nfill - 1 - k_last > 0) good = advance(s, blast_last, itot - i_last);
+  s_out = s;
+  good_out = good;
+}
+
+// ---------------------------------------------------------------- tagged hand-off words
+// A per-workgroup value and its arrival in one 64-bit store: the two low bits carry the call's tag
+// (1 or 2 by call parity; 0 = cleared). Every call clears the entries of workgroups it does not
+// run, so an entry read during a call holds that call's tag, the previous call's tag, or 0.
+__device__ __forceinline__ unsigned long long pack_stats(float m, float l, unsigned tag) {
+  return ((unsigned long long)__float_as_uint(m) << 32) | ((__float_as_uint(l) & ~3u) | tag);
+}
+// record: tot (< 2^51) in w0 bits 2.., nsp in w1 bits 2..17, blast+128 (0: none) in bits 18..25
+__device__ __forceinline__ void pack_rec(const ChunkRec &r, unsigned tag, unsigned long long &w0,
+                                         unsigned long long &w1) {
+  w0 = ((unsigned long long)r.tot << 2) | tag;
+  const unsigned b = r.blast == kNoBinade ? 0u : (unsigned)(r.blast + 128);
+  w1 = ((unsigned long long)(unsigned)r.nsp << 2) | ((unsigned long long)b << 18) | tag;
+}
+__device__ __forceinline__ ChunkRec unpack_rec(unsigned long long w0, unsigned long long w1) {
+  ChunkRec r;
+  r.tot = (long long)(w0 >> 2);
+  r.nsp = (int)((w1 >> 2) & 0xFFFFu);
+  const unsigned b = (unsigned)((w1 >> 18) & 0xFFu);
+  r.blast = b == 0 ? kNoBinade : (int)b - 128;
+  return r;
+}
+// wait until lanes < n of the wave see `tag` in the low bits of their word(s); bounded
+__device__ __forceinline__ void poll_tagged(const unsigned long long *p, int stride, int words, int n,
+                                            unsigned tag, unsigned long long (&v)[2], unsigned *err) {
+  const int lane = threadIdx.x & 63;
+  unsigned spins = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (i < words) {
+        v[i] = lane < n ? ld_agent(p + (size_t)lane * stride + i) : (unsigned long long)tag;
+        ok = ok && (unsigned)(v[i] & 3u) == tag;
+      }
+    }
+    if (__all(ok)) return;
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > kResSpin) {
+      if (lane == 0) atomicOr(err, 1u);
+      return;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- DPP scans
+// A DPP move in which lanes whose source lies outside the pattern (or in a masked row) read 0.
+template <int CTRL, int RM>
+__device__ __forceinline__ int dpp0(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, RM, 0xF, false);
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ float dpp0(float v) {
+  return __builtin_bit_cast(float, dpp0<CTRL, RM>(__builtin_bit_cast(int, v)));
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ double dpp0(double v) {
+  const long long u = __builtin_bit_cast(long long, v);
+  const int lo = dpp0<CTRL, RM>((int)u), hi = dpp0<CTRL, RM>((int)(u >> 32));
+  return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+template <int C, int RM>
+struct DppCtl {
+  static constexpr int c = C, rm = RM;
+};
+// inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 inside each row of 16 lanes, then
+// row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3)
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan_dpp(T v) {
+  v += dpp0<0x111, 0xF>(v);
+  v += dpp0<0x112, 0xF>(v);
+  v += dpp0<0x114, 0xF>(v);
+  v += dpp0<0x118, 0xF>(v);
+  v += dpp0<0x142, 0xA>(v);
+  v += dpp0<0x143, 0xC>(v);
+  return v;
+}
+// one query head's score of one key (the tail): as qk_row_dot, with qt[j] = q16[h][16j + lane%16]
+// for the head h of the lane's DPP row
+__device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
+  const uint4 scl = row[16];
+#pragma unroll
+  for (int b = 0; b < kHd / 32; ++b) {
+    const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
+    float x0[16], x1[16];
+    const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x0[i] = sbyte(u0[i >> 2], i & 3);
+      x1[i] = sbyte(u1[i >> 2], i & 3);
+    }
+    const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
+    const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+    float inner = 0.0f;
+    Dot16<16>::run(inner, qt[2 * b], x0);
+    Dot16<16>::run(inner, qt[2 * b + 1], x1);
+    acc = __fadd_rn(acc, __fmul_rn(sc, inner));
+  }
+}
+template <int CH>
+__device__ __forceinline__ void qk_f16_half1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+    Dot16<16>::run(acc, qt[CH * 8 + j], x);
+  }
+}
+// inclusive prefix sum inside each DPP row of 16 lanes
+template <typename T>
+__device__ __forceinline__ T row_incl_scan_dpp(T v) {
+  v += dpp0<0x111, 0xF>(v);
+  v += dpp0<0x112, 0xF>(v);
+  v += dpp0<0x114, 0xF>(v);
+  v += dpp0<0x118, 0xF>(v);
+  return v;
+}
+
+// classify (bkv_device.h) without branches, the increment as an exact double
+__device__ __forceinline__ void classify_d(double abefore, double aafter, float e, bool &special, int &bin,
+                                           double &inc) {
+  const int B = ilogb(aafter);
+  const double lo = ldexp(1.0, B);
+  const double t = ldexp((double)e, 23 - B);
+  const bool ok = aafter >= 0x1p-17 && aafter < 0x1p22 && !(aafter > 2.0 * lo * (1.0 - kMargin)) &&
+                  !(abefore < lo * (1.0 + kMargin)) && (t - floor(t) != 0.5);
+  special = !ok;
+  bin = ok ? B : kNoBinade;
+  inc = ok ? ldexp(rint(t), B + 17) : 0.0;
+}
+
+// Across the workgroup's waves: sh[i * kGqa + h] holds wave i's total of head h. Lanes 0..kResNW-1
+// scan those totals (DPP row shifts inside the first row of 16), and every lane takes its wave's
+// exclusive prefix and the workgroup total by readlane, instead of each lane summing kResNW values.
+__device__ __forceinline__ int rd_lane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float rd_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double rd_lane(double v, int l) {
+  const long long u = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)u, l), hi = __builtin_amdgcn_readlane((int)(u >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+template <typename T>
+__device__ __forceinline__ void xwave_prefix(const T *sh, int h, int wave, T &before, T &total) {
+  static_assert(kResNW <= 16, "one DPP row holds the wave totals");
+  const int lane = threadIdx.x & 63;
+  T x = lane < kResNW ? sh[lane * kGqa + h] : T(0);
+  x += dpp0<0x111, 0xF>(x);
+  x += dpp0<0x112, 0xF>(x);
+  x += dpp0<0x114, 0xF>(x);
+  if (kResNW > 8) x += dpp0<0x118, 0xF>(x);
+  total = rd_lane(x, kResNW - 1);
+  before = wave > 0 ? rd_lane(x, wave - 1) : T(0);
+}
+
+// the workgroup-wide max / sum of four values at once (every thread receives them)
+// the wave's max (sum) in lane 63: DPP row reductions, then row_bcast 15 into rows 1, 3 and row_bcast
+// 31 into rows 2, 3 (rows a broadcast does not write read the neutral element)
+__device__ __forceinline__ float wave_max_l63(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp((int)0xFF800000u, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp((int)0xFF800000u, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_l63(float v) {
+  v = row16_sum(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+  return v;
+}
+__device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_max_l63(v[h]);
+  if (lane == 63)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float r = sh[h];
+#pragma unroll
+    for (int i = 1; i < kResNW; ++i) r = fmaxf(r, sh[i * kGqa + h]);
+    v[h] = r;
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ void block_sum4(float (&v)[kGqa], float *sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) v[h] = wave_sum_l63(v[h]);
+  if (lane == 63)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float r = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kResNW; ++i) r += sh[i * kGqa + h];
+    v[h] = r;
+  }
+  __syncthreads();
+}
+
+// qv[h][j] for a per-lane h, as masked bits (a select chain would be folded into an indexed
+// access, which moves qv to private memory)
+__device__ __forceinline__ float pick4h(const float (&qv)[kGqa][kHd / 16], int h, int j) {
+  uint32_t b = 0u;
+#pragma unroll
+  for (int i = 0; i < kGqa; ++i) b |= __float_as_uint(qv[i][j]) & (0u - (uint32_t)(h == i));
+  return __uint_as_float(b);
+}
+
+template <typename T>
+__device__ __forceinline__ T pick4(const T (&v)[kGqa], int i) {
+  return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
+// PV over a wave's register-resident q8_0 V rows (slots s: key 32 s + 4 wave + vkk), probabilities
+// from p[k] (4 fp16 per key). DELTA: the probabilities are p[k] - q[k] (exact in fp32), and a slot
+
+}  // namespace bkv

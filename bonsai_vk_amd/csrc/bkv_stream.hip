@@ -1,0 +1,990 @@
+// bkv_stream.hip - the default decode kernel for q8_0 K and V when a KV group's keys fit 64
+// workgroups of at most 512 + kResTail keys: one launch per layer and token, one 512-thread
+// workgroup per CU, every workgroup resident for the whole call.
+//
+// Every wave requests its share of the whole K and V stream up front (a K tile of 64 rows into LDS
+// by direct-to-LDS loads, 17 slots of V rows into registers), so the stream runs at full bandwidth
+// and has landed by the time the scores are done. A wave's vector load completes only after every
+// older load of its CU's queue, so the cross-workgroup polls (waves 0..3) come after the stream.
+//
+// Per call:
+//  1. Loads; wave 0 also brings q (and decode_step's new K and V) into LDS. The new token is
+//     quantised into the cache and patched into the LDS tile (no round trip through memory).
+//  2. Scores in the reference's order (attn_vk.h:156-170), one key per lane and wave; the tail keys
+//     (past 512, at most kResTail) 8 lanes per (key, head), one per 32-element block. The
+//     workgroup's (max, sum exp) per head go out as tagged words; barrier A gives the global max M,
+//     the sum estimate S_a and the workgroup's position on the running sum.
+//  3. e = exp(s*scale - M) correctly rounded, positions by fp32 DPP scans, each step of the serial
+//     fp32 sum classified as an exact integer increment in its binade or a special; the workgroup's
+//     record and specials go out. p16' = f16(e / S_a); the keys whose p16 the exact sum may still
+//     change ("at risk") keep their V rows in LDS.
+//  4. Every wave: PV over its slots with p16'. Waves 0..3 then poll the records (barrier B), walk
+//     them to the exact serial sums (every workgroup walks the group's records itself), form
+//     p16 = f16(e / sum) and add (p16 - p16') * v for the keys whose rounding changed.
+//  5. The workgroup's [4][256] partial goes out as tagged words, and workgroup i sums slice i of
+//     the group's partials in workgroup order (+ gate).
+#include <cstdlib>
+
+#include "bkv_res_shared.h"
+
+namespace bkv {
+
+constexpr int kSwKW = 4;                 // waves 0..3 poll, walk and correct
+constexpr int kSwNP = kResNT;            // pass keys per workgroup (one per thread)
+constexpr int kSwSlots = 17;             // V slots per lane: 16 x 32 pass rows, 1 x 16 tail rows (waves 0..3)
+constexpr int kSwKeys = kSwNP + kResTail;
+constexpr int kSwTailLoads = (kResTail * kUPR + 63) / 64;   // direct-to-LDS loads of the tail rows
+constexpr int kSwBlocks = kSwNP / 64 + 1;                  // e-pass blocks: 8 of 64 keys, the tail
+constexpr int kSwRisk = 128;             // at-risk V rows the LDS keeps (more: re-read from the cache)
+// relative distance from S_a inside which the exact sum is expected (it changes ~2e-6 relative on
+// these shapes); a key is at risk when p16' would round differently anywhere inside it
+constexpr float kSwRiskBand = 0x1p-17f;
+
+// rows [0, n) of the tail (keys k0 ..) into tt (kUPR uint4 per row), lanes past the rows masked
+template <bool PG>
+__device__ __forceinline__ void stage_tail(uint4 *tt, const SlotMap &sm, int nkv, int g, int k0, int n) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(tt));
+#pragma unroll
+  for (int i = 0; i < kSwTailLoads; ++i) {
+    const int slotx = 64 * i + lane, row = slotx / kUPR, col = slotx - row * kUPR;
+    const int64_t sl = slot_k<PG>(sm, k0 + min(row, n - 1));
+    const uint8_t *src = col == 16 ? sm.L->ks + (sl * nkv + g) * kScaleRowBytes
+                                   : sm.L->kd + (sl * nkv + g) * kHd + col * 16;
+    if (slotx < kResTail * kUPR)
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base + 1024u * i)
+                   : "memory", "m0");
+  }
+}
+
+// The new token's row of one tensor for group g, quantised (q8_0, round half to even): lanes
+// s = 0..15 of each 32-lane half own elements 16 s .. 16 s + 15 (lanes 0..31: K, 32..63: V). d gets
+// the lane's 16 data bytes, sw (lanes s % 4 == 0) the scale word of blocks s/2 and s/2 + 1. The rows
+// are stored to the cache slot here (attn_norm_rope2.comp:184-217 for the arithmetic).
+__device__ __forceinline__ void append_q8_rows(const AppendArgs &ap, int64_t slot, const float *xk, const float *xv,
+                                               int g, int lane, uint4 &d, uint32_t &sw) {
+  const int s = lane & 15;
+  const float *x = (lane < 32 ? xk : xv) + 16 * s;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = x[i];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  const float id = q8_iscale(amax);
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = q8_byte<false>(v[4 * i], id) | (q8_byte<false>(v[4 * i + 1], id) << 8) |
+           (q8_byte<false>(v[4 * i + 2], id) << 16) | (q8_byte<false>(v[4 * i + 3], id) << 24);
+  const uint32_t h = f32_to_f16_rne(q8_scale(amax));
+  const uint32_t hn = __shfl_down(h, 2);
+  d = make_uint4(w[0], w[1], w[2], w[3]);
+  sw = h | (hn << 16);
+  if ((lane & 31) < 16) {
+    const bool isk = lane < 32;
+    uint8_t *dr = const_cast<uint8_t *>(isk ? ap.L.kd : ap.L.vd) + (slot * ap.nkv + g) * kHd;
+    uint8_t *sr = const_cast<uint8_t *>(isk ? ap.L.ks : ap.L.vs) + (slot * ap.nkv + g) * kScaleRowBytes;
+    *reinterpret_cast<uint4 *>(dr + 16 * s) = d;
+    if ((s & 3) == 0) *reinterpret_cast<uint32_t *>(sr + (s >> 2) * 4) = sw;
+  }
+}
+
+// 2^(j/32), j = 0..31, correctly rounded to fp64
+__constant__ double kExp2Tab[32] = {
+    0x1.0000000000000p+0, 0x1.059b0d3158574p+0, 0x1.0b5586cf9890fp+0, 0x1.11301d0125b51p+0,
+    0x1.172b83c7d517bp+0, 0x1.1d4873168b9aap+0, 0x1.2387a6e756238p+0, 0x1.29e9df51fdee1p+0,
+    0x1.306fe0a31b715p+0, 0x1.371a7373aa9cbp+0, 0x1.3dea64c123422p+0, 0x1.44e086061892dp+0,
+    0x1.4bfdad5362a27p+0, 0x1.5342b569d4f82p+0, 0x1.5ab07dd485429p+0, 0x1.6247eb03a5585p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.71f75e8ec5f74p+0, 0x1.7a11473eb0187p+0, 0x1.82589994cce13p+0,
+    0x1.8ace5422aa0dbp+0, 0x1.93737b0cdc5e5p+0, 0x1.9c49182a3f090p+0, 0x1.a5503b23e255dp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b7f76f2fb5e47p+0, 0x1.c199bdd85529cp+0, 0x1.cb720dcef9069p+0,
+    0x1.d5818dcfba487p+0, 0x1.dfc97337b9b5fp+0, 0x1.ea4afa2a490dap+0, 0x1.f50765b6e4540p+0,
+};
+
+// v = fma(p, r, c) with c an SGPR pair (the compiler's accumulator form would move each constant
+// into VGPRs first)
+__device__ __forceinline__ double fma_sc(double p, double r, double c) {
+  double v;
+  asm("v_fma_f64 %0, %1, %2, %3" : "=v"(v) : "v"(p), "v"(r), "s"(c));
+  return v;
+}
+
+// exp of a float argument, correctly rounded to float: the value of (float)exp((double)x), as
+// exp_cr, by a table. x = (k/32) ln2 + r with |r| <= ln2/64 (ln2/32 split so that k*hi is exact for
+// |k| < 2^12), exp(r) by its degree-5 Taylor polynomial in fp64 (truncation < 2^-48.6), times
+// t2[k mod 32] = 2^((k mod 32)/32) and 2^floor(k/32), rounded once to float. When the fp64 value lies
+// within 64 units of its last place of a float rounding boundary (the error is below 16), or x is
+// outside (-87, 88), the library fp64 exp decides. t2: kExp2Tab in LDS. Checked on the host against
+// (float)exp((double)x) over every float in [-104, 89] (tests/test_exp_table.py runs a stride of it).
+__device__ __forceinline__ float exp_cr_t(float xf, const double *t2) {
+  const float kf = __builtin_rintf(xf * 46.16624130844683f);      // 32 / ln2
+  const int k = (int)kf;
+  const double x = xf, kd = kf;
+  double r = fma(-kd, 0x1.62e42fefa3800p-6, x);                     // ln2/32, 41 bits
+  r = fma(-kd, 0x1.ef35793c76730p-50, r);                           // the rest of ln2/32
+  double p = fma_sc(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5); // 1/120 r + 1/24
+  p = fma_sc(p, r, 0x1.5555555555555p-3);
+  p = fma_sc(p, r, 0.5);
+  p = fma_sc(p, r, 1.0);
+  p = fma_sc(p, r, 1.0);
+  const double y = ldexp(p * t2[k & 31], k >> 5);
+  const long long low = (long long)(__double_as_longlong(y) & 0x1FFFFFFFll) - 0x10000000ll;
+  float res = (float)y;
+  if (!(xf > -87.0f && xf < 88.0f) || (low >= -64 && low <= 64)) res = (float)exp(x);
+  return res;
+}
+
+// binade classification of one step of the running sum from its fp32 position before and after
+// (the fp32 error of a position is far inside the 2^-14 relative margin): B and the step's exact
+// increment in ulps of that binade (an integer below 2^24), or a special
+__device__ __forceinline__ void classify_i(float abefore, float aafter, float e, bool &special, int &bin, int &inc) {
+  const int B = (int)((__float_as_uint(aafter) >> 23) & 0xFF) - 127;
+  const float lo = __uint_as_float((uint32_t)min(max(B + 127, 1), 254) << 23);
+  const float t = ldexpf(e, 23 - B);
+  const float r = __builtin_rintf(t);
+  const bool ok = aafter >= 0x1p-17f && aafter < 0x1p22f && !(aafter > 2.0f * lo * (float)(1.0 - kMargin)) &&
+                  !(abefore < lo * (float)(1.0 + kMargin)) && (t - __builtin_floorf(t) != 0.5f);
+  special = !ok;
+  bin = B;
+  inc = ok ? (int)r : 0;
+}
+
+// s_waitcnt vmcnt(n) for a runtime n (a branch per value; an n the compiler knows folds away)
+__device__ __forceinline__ void wait_vm_n(int n) {
+  switch (n) {
+#define BKV_WAIT_CASE(i) case i: wait_vm<i>(); break;
+    BKV_WAIT_CASE(0) BKV_WAIT_CASE(1) BKV_WAIT_CASE(2) BKV_WAIT_CASE(3) BKV_WAIT_CASE(4) BKV_WAIT_CASE(5)
+    BKV_WAIT_CASE(6) BKV_WAIT_CASE(7) BKV_WAIT_CASE(8) BKV_WAIT_CASE(9) BKV_WAIT_CASE(10) BKV_WAIT_CASE(11)
+    BKV_WAIT_CASE(12) BKV_WAIT_CASE(13) BKV_WAIT_CASE(14) BKV_WAIT_CASE(15) BKV_WAIT_CASE(16) BKV_WAIT_CASE(17)
+    BKV_WAIT_CASE(18) BKV_WAIT_CASE(19) BKV_WAIT_CASE(20) BKV_WAIT_CASE(21) BKV_WAIT_CASE(22) BKV_WAIT_CASE(23)
+    BKV_WAIT_CASE(24) BKV_WAIT_CASE(25) BKV_WAIT_CASE(26) BKV_WAIT_CASE(27) BKV_WAIT_CASE(28) BKV_WAIT_CASE(29)
+    BKV_WAIT_CASE(30) BKV_WAIT_CASE(31) BKV_WAIT_CASE(32) BKV_WAIT_CASE(33) BKV_WAIT_CASE(34) BKV_WAIT_CASE(35)
+    BKV_WAIT_CASE(36) BKV_WAIT_CASE(37) BKV_WAIT_CASE(38) BKV_WAIT_CASE(39) BKV_WAIT_CASE(40)
+#undef BKV_WAIT_CASE
+    default: wait_vm<0>(); break;
+  }
+}
+
+// LDS flags between the roles. A K-wave barrier: each K wave adds one to *ctr and waits until it
+// reaches target (the V waves are busy elsewhere). A flag: the K waves each add one once their part
+// is in LDS; a V wave waits until it reaches target. LDS operations of one wave complete in order,
+// so whatever a wave wrote before its add is in LDS once the add is seen.
+__device__ __forceinline__ unsigned lds_ld(const unsigned *p) {
+  return __hip_atomic_load(const_cast<unsigned *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_arrive(unsigned *ctr) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if ((threadIdx.x & 63) == 0) atomicAdd(ctr, 1u);
+}
+__device__ __forceinline__ void lds_wait(const unsigned *ctr, unsigned target) {
+  while (lds_ld(ctr) < target) __builtin_amdgcn_s_sleep(1);
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void kwave_sync(unsigned *ctr, unsigned target) {
+  lds_arrive(ctr);
+  lds_wait(ctr, target);
+}
+
+// the wave's max / sum of one value per head over its 64 lanes, in every lane
+__device__ __forceinline__ float wave_max64(float v) { return rd_lane(wave_max_l63(v), 63); }
+__device__ __forceinline__ float wave_sum64(float v) { return rd_lane(wave_sum_l63(v), 63); }
+__device__ __forceinline__ int wave_sum64_i(int v) { return __builtin_amdgcn_readlane(wave_scan_i32(v), 63); }
+
+template <bool PG>
+__global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
+  constexpr int NT = kResNT, NW = kResNW, NP = kSwNP, KS = kSwKeys;
+  using WS = WalkScratchT<kResMaxGroupWgs, 192>;
+  using VR = KRow<BKV_Q8_0>;
+  // LDS. kt: the K tiles (pass key k at row k: kt + k * kUPR); once every tile is scored the same
+  // bytes hold the e values, probabilities, binade map, specials, walk scratch, the at-risk V rows
+  // and the PV reduction.
+  __shared__ uint4 kt[NP * kUPR];
+  __shared__ uint4 vsc[NW * 64];            // V scale rows: wave w, slot s < 16, row vkk at [w][4 s + vkk]
+  __shared__ uint4 ttl[kResTail * kUPR];    // the tail's K rows
+  __shared__ float4 s_q[kGqa * kHd / 4];    // the group's q rows (fp32)
+  __shared__ uint4 s_x[2 * kHd / 4];        // decode_step: the new token's K and V (fp32), then its V row
+  __shared__ float s_tsc[kResTail * kGqa];  // the tail's scores [key][head]
+  __shared__ uint32_t s_tsw[kResTail * 4];  // the tail's V scale rows
+  __shared__ int s_pg[kResPgMax];
+  __shared__ double s_t2[32];               // 2^(j/32)
+  __shared__ float shf4[NW * kGqa];
+  __shared__ float s_M[kGqa], s_Sa[kGqa], s_S[kGqa];
+  __shared__ double s_P0[kGqa];
+  __shared__ int s_ok[kGqa];
+  __shared__ float4 s_bt[kSwBlocks];        // e-pass block totals of e (positions), per head
+  __shared__ double s_bu[kSwBlocks * kGqa]; // block totals of the increments (units of 2^-40)
+  __shared__ int s_bc[kSwBlocks * kGqa];    // block counts of specials
+  __shared__ int s_nrisk;
+  __shared__ unsigned s_kctr;               // the K waves' spin barrier
+
+  // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
+  // of one key range share an XCD (each 64 B scale line holds all groups' scales of a slot)
+  const int w = blockIdx.x, nkv = a.nkv, G = a.G;
+  int g, wi;
+  if ((G & 7) == 0 && ((int)gridDim.x & 7) == 0) {
+    const int x = w & 7, loc = w >> 3;
+    g = loc % nkv;
+    wi = x * (G >> 3) + loc / nkv;
+  } else {
+    g = w % nkv;
+    wi = w / nkv;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool kwave = wave < kSwKW;
+  const int64_t kb = (int64_t)wi * a.kpw;
+  const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
+  const int nk = (int)max((int64_t)1, ke - kb);        // the plan gives every workgroup keys
+  const int np = min(nk, NP), tn = max(0, nk - NP);     // pass keys, tail keys (tn <= kResTail)
+  const LayerView &L = a.L;
+
+  // ---------------------------------------------------------------- set-up
+  unsigned *gs = a.sync + (size_t)g * kResGroupLines * kCounterStride;
+  unsigned *err = a.sync + (size_t)nkv * kResGroupLines * kCounterStride;
+  const unsigned gen = ld_agent(gs) + 1u;
+  unsigned *cnt = gs + (1 + (gen & 1u) * 4) * kCounterStride;
+  if (wi == 0 && tid < 4) st_agent(gs + (1 + ((gen + 1u) & 1u) * 4 + tid) * kCounterStride, 0u);
+  const unsigned tag = 1u + (gen & 1u);
+  constexpr int GM = kResMaxGroupWgs;
+  unsigned long long *tstats = a.tstats + (size_t)g * kGqa * GM;
+  unsigned long long *trec = a.trec + (size_t)g * kGqa * GM * 2;
+  if (wi == 0)                                 // entries of workgroups this call does not run
+    for (int i = tid; i < kGqa * (GM - G); i += NT) {
+      const int h = i / (GM - G), c = G + i % (GM - G);
+      st_agent(tstats + h * GM + c, 0ull);
+      st_agent(trec + (h * GM + c) * 2, 0ull);
+      st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
+    }
+  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; }
+  if (tid < kGqa) {                            // the tail block's totals when there is no tail
+    s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
+    s_bc[(kSwBlocks - 1) * kGqa + tid] = 0;
+  }
+  if (tid == 0) s_bt[kSwBlocks - 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tid >= 64 && tid < 96) s_t2[tid - 64] = kExp2Tab[tid - 64];
+  RTS(0);
+
+  const bool appender = a.ap.k && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke;
+  const int kp = appender ? (int)((int64_t)a.ap.pos - kb) : -1;     // the new token's key in this workgroup
+  // pass key k sits in wave k / 64 (its K tile) and V slot (k / 32, wave (k % 32) / 4, row group
+  // k % 4); tail key NP + t: its K row on wave t / 2, its V row on wave t / 4 (slot 16)
+  const int aw = kp < 0 ? -1 : (kp < NP ? kp >> 6 : (kp - NP) >> 1);   // the wave that appends it
+  SlotMap sm{&L, kb, s_pg, 0u};
+  if constexpr (PG) {
+    const uint32_t pgs = (uint32_t)L.page, pg0 = (uint32_t)(kb + L.base) / pgs,
+                   pg1 = (uint32_t)(kb + nk - 1 + L.base) / pgs;
+    sm.pf = pg0;
+    if (tid <= (int)min(pg1 - pg0, (uint32_t)kResPgMax - 1u)) s_pg[tid] = L.bt[pg0 + tid];
+  }
+  __syncthreads();                             // flags, table, page table
+
+  // scratch carved from the K tiles once every tile is scored
+  char *xb = reinterpret_cast<char *>(kt);
+  float *s_e = reinterpret_cast<float *>(xb);                         // [kGqa][KS]
+  uint2 *s_ps = reinterpret_cast<uint2 *>(xb + kGqa * KS * 4);        // [KS] p16' (4 heads per key)
+  uint2 *s_p16 = s_ps + KS;                                           // [KS] p16
+  int8_t *s_bin = reinterpret_cast<int8_t *>(s_p16 + KS);             // [kGqa][KS]
+  int16_t *s_ridx = reinterpret_cast<int16_t *>(s_bin + kGqa * KS);   // [KS] at-risk row index, -1: none
+  Special *s_spec = reinterpret_cast<Special *>(xb + 24576);          // [kGqa][kMaxSpecial]
+  WS *s_walk = reinterpret_cast<WS *>(xb + 24576 + kGqa * kMaxSpecial * sizeof(Special));
+  uint4 *s_rrow = reinterpret_cast<uint4 *>(xb + 53248);              // [kSwRisk + 8][16] at-risk V rows
+  float *s_red = reinterpret_cast<float *>(xb + 53248 + (kSwRisk + 8) * 256);  // [wave][head][EPL][LPR]
+  static_assert(kGqa * KS * 4 + 2 * KS * 8 + kGqa * KS + 2 * KS <= 24576, "e, p16', p16, binade map, risk index");
+  static_assert(24576 + kGqa * kMaxSpecial * sizeof(Special) + kGqa * sizeof(WS) <= 53248, "specials, walk scratch");
+  static_assert(53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4 <= sizeof(kt), "at-risk rows, PV reduction");
+  const int th = lane >> 4, tt = lane & 15;   // tail e pass: lane 16 h + t takes tail key t, head h
+  const int vsub = lane & 15, vkk = lane >> 4;
+
+  // ---------------------------------------------------------------- loads
+  // Wave 0 first brings q (and decode_step's new K and V) into LDS; every wave then stages its K
+  // tile (pass keys 64 w ..) and its tail K rows (tail keys 2 w, 2 w + 1) by direct-to-LDS loads,
+  // its V scale rows into LDS and its V rows into registers: the whole stream is requested up front.
+  // The direct-to-LDS loads bypass the compiler's wait counting; each wait below names how many loads
+  // were issued after the ones it needs (the V loads are the compiler's and come last).
+  const bool t0 = 64 * wave < np;              // the wave's K tile holds keys
+  const int tr = min(2, max(0, tn - 2 * wave));   // the wave's tail K rows
+  const bool vt = wave < 4;                    // the wave holds a tail V slot
+  if (wave == 0) {
+    const uint32_t qb = __builtin_amdgcn_readfirstlane(lds_addr(s_q));
+    const float *qsrc = a.q + (size_t)g * kGqa * a.qs;
+#pragma unroll
+    for (int i = 0; i < kGqa; ++i)             // head i's 256 floats: 64 lanes x 16 B
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(qsrc + (size_t)i * a.qs + 4 * lane),
+                   "s"(qb + 1024u * i) : "memory", "m0");
+    if (appender) {
+      const uint32_t xbs = __builtin_amdgcn_readfirstlane(lds_addr(s_x));
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(a.ap.k + (size_t)g * kHd + 4 * lane),
+                   "s"(xbs) : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(a.ap.v + (size_t)g * kHd + 4 * lane),
+                   "s"(xbs + 1024u) : "memory", "m0");
+    }
+  }
+  if (t0) stage_k_wave<BKV_Q8_0, PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 0);
+  if (tr > 0) {                                // 2 rows x 17 uint4: lanes 0..33
+    const uint32_t tb = __builtin_amdgcn_readfirstlane(lds_addr(ttl + 2 * wave * kUPR));
+    const int row = lane / kUPR, col = lane - row * kUPR;
+    const int64_t sl = slot_k<PG>(sm, NP + 2 * wave + min(row, tr - 1));
+    const uint8_t *src = col == 16 ? L.ks + (sl * nkv + g) * kScaleRowBytes : L.kd + (sl * nkv + g) * kHd + col * 16;
+    if (lane < 2 * kUPR)
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(tb) : "memory", "m0");
+  }
+  // K first: a wave requests its V rows once its K tile and tail rows have landed, so the K
+  // stream (which the scores wait for) is not shared with the V stream (which only the PV needs)
+  wait_vm<0>();
+  RTSV(0);
+  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
+  uint32_t xs = 0u;                            // the tail slot's scale word
+  {
+    const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
+    const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
+                 "s"(sb) : "memory", "m0");
+  }
+  if (vt) {
+    const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
+    xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+  }
+#pragma unroll
+  for (int s = 0; s < kSwSlots; ++s) {
+    const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
+    const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
+    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+  }
+  __syncthreads();                             // s_q (and s_x) visible to every wave
+
+  // ---------------------------------------------------------------- scores
+  // Each lane: key 64 w + lane against the group's 4 heads (attn_vk.h:156-170). The tail keys 2 w,
+  // 2 w + 1: lane 8 p + b computes block b's inner sum of pair p (key 2 w + p / 4, head p % 4), the
+  // 8 blocks' terms are then added in order by the pair's first lane (the same arithmetic).
+  float sc[kGqa];
+  float mloc[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) { mloc[h] = -INFINITY; sc[h] = 0.0f; }
+  const int kl = 64 * wave + lane;             // this lane's pass key
+  {
+    float qv[kGqa][kHd / 16];
+    {
+      const float *qf = reinterpret_cast<const float *>(s_q) + (lane & 15);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qf[h * kHd + 16 * j]);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qv[h][j]));
+    }
+    // decode_step: the wave that holds the new token's K row quantises the token (both rows stored
+    // to the cache here), patches its K row into the tile and leaves its V row in s_x
+    uint4 ad = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t asw = 0u;
+    if (wave == aw) {
+      const float *xf = reinterpret_cast<const float *>(s_x);
+      append_q8_rows(a.ap, slot_k<PG>(sm, kp), xf, xf + kHd, g, lane, ad, asw);   // (decode_step: base 0)
+      wave_lds_sync();
+      __builtin_amdgcn_wave_barrier();
+      if (lane >= 32 && lane < 48) {           // the V patch row: 16 data uint4, then the scale row
+        s_x[lane - 32] = ad;
+        if (((lane - 32) & 3) == 0) reinterpret_cast<uint32_t *>(&s_x[16])[(lane - 32) >> 2] = asw;
+      }
+    }
+    auto patch_k = [&](uint4 *row) {          // the appended K row over its staged copy
+      if (lane < 16) {
+        row[lane] = ad;
+        if ((lane & 3) == 0) reinterpret_cast<uint32_t *>(&row[16])[lane >> 2] = asw;
+      }
+      wave_lds_sync();
+    };
+    asm volatile("s_nop 4");
+    if (t0) {
+      RTS(14);
+      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
+      float acc1[kGqa];
+      qk_row_dot<BKV_Q8_0>(kt + kl * kUPR, qv, acc1);
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        sc[h] = acc1[h];
+        if (kl < np) mloc[h] = fmaxf(mloc[h], acc1[h] * a.scale);
+      }
+      RTSV(1);
+    }
+    if (tr > 0) {
+      if (wave == aw && kp >= NP) patch_k(ttl + (kp - NP) * kUPR);
+      const int p = lane >> 3, b = lane & 7, t = 2 * wave + (p >> 2), h = p & 3;
+      const int tk = min(t, tn - 1);
+      const uint4 *row = ttl + tk * kUPR;
+      const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
+      const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      const float4 *qh = s_q + h * (kHd / 4) + 8 * b;
+      float inner = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float4 q4 = qh[c];
+        const float qq[4] = {round_f16(q4.x), round_f16(q4.y), round_f16(q4.z), round_f16(q4.w)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) inner = fmaf(qq[i], sbyte(u[c], i), inner);   // exact products
+      }
+      const uint32_t sw = reinterpret_cast<const uint32_t *>(&row[16])[b >> 1];
+      const float term = __fmul_rn(f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu)), inner);
+      // acc = ((0 + term_0) + term_1) + ... + term_7 on the pair's first lane (row_shl j brings
+      // lane + j of the same row of 16)
+      float acc1 = term;
+      acc1 = __fadd_rn(acc1, dpp<0x101>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x102>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x103>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x104>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x105>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x106>(term));
+      acc1 = __fadd_rn(acc1, dpp<0x107>(term));
+      if (b == 0 && t < tn) s_tsc[t * kGqa + h] = acc1;
+#pragma unroll
+      for (int hh = 0; hh < kGqa; ++hh) {      // fold the tail scores into the lane maxima
+        const float v = (b == 0 && t < tn && h == hh) ? acc1 * a.scale : -INFINITY;
+        mloc[hh] = fmaxf(mloc[hh], v);
+      }
+    }
+  }
+  RTS(1);
+  RTSV(2);
+  // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
+  block_max4(mloc, shf4);
+  RTSV(3);
+  float lsum[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    float l = (t0 && kl < np) ? __expf(sc[h] * a.scale - mloc[h]) : 0.0f;
+    if (wave == 0 && tt < tn && th == h) l += __expf(s_tsc[tt * kGqa + h] * a.scale - mloc[h]);
+    lsum[h] = l;
+  }
+  block_sum4(lsum, shf4);
+  if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
+  RTS(9);
+
+  // ---------------------------------------------------------------- barrier A: global max
+  // wave h polls head h's statistics of every workgroup of the group (the V stream has landed by
+  // now: a poll's load would wait for it)
+  if (kwave) {
+    unsigned long long v[2];
+    poll_tagged(tstats + wave * GM, 1, 1, G, tag, v, err);
+    const float mw = lane < G ? __uint_as_float((unsigned)(v[0] >> 32)) : -INFINITY;
+    const float lw = lane < G ? __uint_as_float((unsigned)v[0] & ~3u) : 0.0f;
+    auto dmax = [](float v, auto ctl) {
+      constexpr int C = decltype(ctl)::c, RM = decltype(ctl)::rm;
+      const int ninf = (int)0xFF800000u;
+      return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), C, RM, 0xF, false)));
+    };
+    float mx = mw;
+    mx = dmax(mx, DppCtl<0x111, 0xF>{});
+    mx = dmax(mx, DppCtl<0x112, 0xF>{});
+    mx = dmax(mx, DppCtl<0x114, 0xF>{});
+    mx = dmax(mx, DppCtl<0x118, 0xF>{});
+    mx = dmax(mx, DppCtl<0x142, 0xA>{});
+    mx = dmax(mx, DppCtl<0x143, 0xC>{});
+    const float m = rd_lane(mx, 63);
+    const double lx = lane < G ? (double)lw * exp((double)mw - (double)m) : 0.0;
+    const double sx = wave_incl_scan_dpp(lx);
+    const double p = wi > 0 ? rd_lane(sx, wi - 1) : 0.0, t = rd_lane(sx, 63);
+    if (lane == 0) {
+      s_M[wave] = m;
+      s_P0[wave] = p;
+      s_Sa[wave] = (float)t;
+    }
+  }
+  __syncthreads();
+  RTS(2);
+
+  // ---------------------------------------------------------------- e, classification, records
+  // Block w = keys 64 w .. 64 w + 63 (wave w); wave 0 also the tail (block 8, lane 16 h + t: key
+  // NP + t, head h). Each step of the serial sum is placed on its fp32 position: the workgroup's
+  // fp64 start rounded to fp32 (the classification margin is 2^-14 relative, far above the fp32
+  // error of a position), plus the blocks before and the lane's scan.
+  float Mh[kGqa], rSa[kGqa], P0f[kGqa], ev[kGqa], fin[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) { Mh[h] = s_M[h]; rSa[h] = 1.0f / s_Sa[h]; P0f[h] = (float)s_P0[h]; }
+  const bool valid = kl < np;
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    ev[h] = valid ? exp_cr_t(sc[h] * a.scale - Mh[h], s_t2) : 0.0f;
+    fin[h] = wave_incl_scan_dpp(ev[h]);
+    if (valid) s_e[h * KS + kl] = ev[h];
+  }
+  if (lane == 63) s_bt[wave] = make_float4(fin[0], fin[1], fin[2], fin[3]);
+  if (a.keep_e && valid)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) a.e[(size_t)(g * kGqa + h) * a.ld + kb + kl] = ev[h];
+  float evt = 0.0f, fint = 0.0f;
+  const bool tl = wave == 0 && tn > 0;
+  const bool tvalid = tl && tt < tn;
+  if (tl) {
+    evt = tvalid ? exp_cr_t(s_tsc[min(tt, kResTail - 1) * kGqa + th] * a.scale - pick4(Mh, th), s_t2) : 0.0f;
+    fint = row_incl_scan_dpp(evt);
+    if (tvalid) s_e[th * KS + NP + tt] = evt;
+    if (tt == 15) reinterpret_cast<float *>(&s_bt[kSwBlocks - 1])[th] = fint;
+    if (a.keep_e && tvalid) a.e[(size_t)(g * kGqa + th) * a.ld + kb + NP + tt] = evt;
+  }
+  __syncthreads();
+  bool sp[kGqa];
+  double din[kGqa], dinc[kGqa];
+  unsigned long long msk[kGqa];
+  {
+    float fb[kGqa] = {0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < wave; ++b) {
+      const float4 t = s_bt[b];
+      fb[0] += t.x; fb[1] += t.y; fb[2] += t.z; fb[3] += t.w;
+    }
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      const float ab = P0f[h] + (fb[h] + (fin[h] - ev[h]));
+      int bin, inc;
+      bool spx;
+      classify_i(ab, ab + ev[h], ev[h], spx, bin, inc);
+      spx = spx && valid;
+      sp[h] = spx;
+      if (valid) s_bin[h * KS + kl] = spx ? kNoBin8 : (int8_t)bin;
+      msk[h] = __ballot(spx);
+      // a block whose steps all sit in one binade and hold no special sums its increments as
+      // integers; otherwise an fp64 scan (exact: a workgroup's increments are integers below 2^50
+      // in units of 2^-40)
+      const int b0 = __builtin_amdgcn_readfirstlane(bin);
+      const bool uni = msk[h] == 0 && __ballot(valid && bin != b0) == 0;
+      if (uni) {
+        const int t = wave_sum64_i(valid ? inc : 0);
+        din[h] = 0.0;
+        dinc[h] = 0.0;
+        if (lane == 63) s_bu[wave * kGqa + h] = ldexp((double)t, b0 + 17);
+      } else {
+        dinc[h] = (valid && !spx) ? ldexp((double)inc, bin + 17) : 0.0;
+        din[h] = wave_incl_scan_dpp(dinc[h]);
+        if (lane == 63) s_bu[wave * kGqa + h] = din[h];
+      }
+      if (lane == 63) s_bc[wave * kGqa + h] = __popcll(msk[h]);
+    }
+  }
+  bool spt = false;
+  double dint = 0.0, dinct = 0.0;
+  unsigned rowm = 0u;
+  if (tl) {
+    float fb = 0.0f;
+#pragma unroll
+    for (int b = 0; b < kSwBlocks - 1; ++b) fb += reinterpret_cast<const float *>(&s_bt[b])[th];
+    const float ab = pick4(P0f, th) + (fb + (fint - evt));
+    int bin, inc;
+    classify_i(ab, ab + evt, evt, spt, bin, inc);
+    spt = spt && tvalid;
+    dinct = (tvalid && !spt) ? ldexp((double)inc, bin + 17) : 0.0;
+    if (tvalid) s_bin[th * KS + NP + tt] = spt ? kNoBin8 : (int8_t)bin;
+    rowm = (unsigned)(__ballot(spt) >> (16 * th)) & 0xFFFFu;
+    dint = row_incl_scan_dpp(dinct);
+    if (tt == 15) {
+      s_bu[(kSwBlocks - 1) * kGqa + th] = dint;
+      s_bc[(kSwBlocks - 1) * kGqa + th] = __popc(rowm);
+    }
+  }
+  __syncthreads();                             // block totals, the binade map
+  // specials into LDS (at most kMaxSpecial per head)
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    if (sp[h]) {
+      int cb = 0;
+      double ib = 0.0;
+      for (int b = 0; b < wave; ++b) { cb += s_bc[b * kGqa + h]; ib += s_bu[b * kGqa + h]; }
+      const int id = cb + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(msk[h] >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)msk[h], 0u));
+      if (id < kMaxSpecial) {
+        const int8_t bp8 = kl > 0 ? s_bin[h * KS + kl - 1] : (int8_t)0;
+        const int bprev = kl > 0 ? (bp8 == kNoBin8 ? kNoBinade : bp8) : 127;
+        Special x;
+        x.ipre = (long long)(ib + (din[h] - dinc[h]));
+        x.e = ev[h];
+        x.meta = kl | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+        s_spec[h * kMaxSpecial + id] = x;
+      }
+    }
+  }
+  if (spt) {
+    int cb = 0;
+    double ib = 0.0;
+    for (int b = 0; b < kSwBlocks - 1; ++b) { cb += s_bc[b * kGqa + th]; ib += s_bu[b * kGqa + th]; }
+    const int id = cb + __popc(rowm & ((1u << tt) - 1u));
+    if (id < kMaxSpecial) {
+      const int8_t bp8 = s_bin[th * KS + NP + tt - 1];
+      const int bprev = bp8 == kNoBin8 ? kNoBinade : bp8;
+      Special x;
+      x.ipre = (long long)(ib + (dint - dinct));
+      x.e = evt;
+      x.meta = (NP + tt) | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+      s_spec[th * kMaxSpecial + id] = x;
+    }
+  }
+  {
+    // p16' = f16(e * (1/S_a)) (a speculative value: any rounding of it serves, the corrections
+    // subtract exactly what the PV added); at risk: p16' would round differently somewhere within
+    // kSwRiskBand of it
+    auto risky = [](float p) {
+      const _Float16 a = (_Float16)(p * (1.0f - 2.0f * kSwRiskBand)), b = (_Float16)(p * (1.0f + 2.0f * kSwRiskBand));
+      return __builtin_bit_cast(uint16_t, a) != __builtin_bit_cast(uint16_t, b);
+    };
+    if (valid) {
+      _Float16 pk[kGqa];
+      bool r = false;
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) {
+        const float p = ev[h] * rSa[h];
+        pk[h] = (_Float16)p;
+        r = r || risky(p);
+      }
+      s_ps[kl] = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16),
+                            (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16));
+      int ri = -1;
+      if (r) {
+        ri = atomicAdd(&s_nrisk, 1);
+        if (ri >= kSwRisk) ri = -1;
+      }
+      s_ridx[kl] = (int16_t)ri;
+    } else {
+      s_ridx[kl] = -1;
+    }
+    if (wave == 1 && lane < kResTail) s_ridx[NP + lane] = -1;
+    __syncthreads();
+    if (tl) {                                  // the tail: one head per lane
+      const float p = evt * pick4(rSa, th);
+      if (tvalid) reinterpret_cast<_Float16 *>(s_ps + NP + tt)[th] = (_Float16)p;
+      const unsigned long long rm = __ballot(tvalid && risky(p));
+      const bool r = ((rm >> tt) | (rm >> (tt + 16)) | (rm >> (tt + 32)) | (rm >> (tt + 48))) & 1ull;
+      if (th == 0 && tt < tn && r) {
+        const int ri = atomicAdd(&s_nrisk, 1);
+        s_ridx[NP + tt] = (int16_t)(ri < kSwRisk ? ri : -1);
+      }
+    }
+  }
+  wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
+  __syncthreads();                             // specials, p16', the risk index, the V scale rows
+  RTS(3);
+
+  // ---------------------------------------------------------------- records (K waves)
+  if (kwave) {
+    const int h = wave;
+    int nsp = 0;
+    double t = 0.0;
+    for (int b = 0; b < kSwBlocks; ++b) { nsp += s_bc[b * kGqa + h]; t += s_bu[b * kGqa + h]; }
+    Special *spec_g = a.spec + (size_t)(g * kGqa) * G * kMaxSpecial;
+    const int ns = min(nsp, kMaxSpecial);
+    if (lane < ns) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
+    if (ns > 0) __builtin_amdgcn_s_waitcnt(0);   // the specials are visible before the record is
+    if (lane == 0) {
+      ChunkRec rc;
+      rc.tot = (long long)t;
+      rc.nsp = nsp;
+      const int8_t bl = s_bin[h * KS + nk - 1];
+      rc.blast = bl != kNoBin8 ? bl : kNoBinade;
+      unsigned long long w0, w1;
+      pack_rec(rc, tag, w0, w1);
+      st_agent(trec + (h * GM + wi) * 2, w0);
+      st_agent(trec + (h * GM + wi) * 2 + 1, w1);
+    }
+  }
+
+  // ---------------------------------------------------------------- the speculative PV (every wave)
+  // out += p16' * V over the wave's slots; each at-risk row is kept in LDS for the corrections
+  float acc[kGqa][VR::EPL];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) acc[h][i] = 0.0f;
+  const uint16_t *vsc16 = reinterpret_cast<const uint16_t *>(vsc + wave * 64);
+  auto slot_key = [&](int s) { return s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk; };
+  auto slot_scale = [&](int s) -> float {
+    if (s < kSwSlots - 1) return f16_to_f32(vsc16[(4 * s + vkk) * 8 + (vsub >> 1)]);
+    return f16_to_f32(((vsub >> 1) & 1) ? (xs >> 16) : (xs & 0xFFFFu));
+  };
+  auto p4 = [](uint2 pw, float (&p)[kGqa]) {
+    p[0] = f16_to_f32(pw.x & 0xFFFFu);
+    p[1] = f16_to_f32(pw.x >> 16);
+    p[2] = f16_to_f32(pw.y & 0xFFFFu);
+    p[3] = f16_to_f32(pw.y >> 16);
+  };
+  const int sp_slot = kp < 0 ? -1 : (kp < NP ? kp / 32 : kSwSlots - 1);
+  const int sp_w = kp < 0 ? -1 : (kp < NP ? (kp % 32) / 4 : (kp - NP) / 4), sp_kk = kp % 4;
+  auto patched = [&](int s) { return s == sp_slot && wave == sp_w && vkk == sp_kk; };
+  // the appended row (decode_step) replaces the loaded copy, which may predate it
+  const uint4 pd = s_x[vsub];
+  const uint32_t pws = reinterpret_cast<const uint32_t *>(&s_x[16])[vsub >> 2];
+  const float pscale = f16_to_f32(((vsub >> 1) & 1) ? (pws >> 16) : (pws & 0xFFFFu));
+  {
+    // each slot's LDS operands are read one slot ahead, and no further (held back by the compiler
+    // barrier at the end of a slot, they would all be read up front into registers)
+    uint2 pn = s_ps[min(slot_key(0), KS - 1)];
+    int rn = s_ridx[min(slot_key(0), KS - 1)];
+    float vn = slot_scale(0);
+#pragma unroll
+    for (int s = 0; s < kSwSlots; ++s) {
+      const int k = slot_key(s);
+      const bool live = (s < kSwSlots - 1 ? k < np : (vt && k < nk));
+      uint2 pw = pn;
+      const int ri = rn;
+      const float vs = vn;
+      if (s + 1 < kSwSlots) {
+        pn = s_ps[min(slot_key(s + 1), KS - 1)];
+        rn = s_ridx[min(slot_key(s + 1), KS - 1)];
+        vn = slot_scale(s + 1);
+      }
+      pw.x = live ? pw.x : 0u;
+      pw.y = live ? pw.y : 0u;
+      float p[kGqa];
+      p4(pw, p);
+      v_accum<BKV_Q8_0>(vd[s], live && !patched(s) ? vs : 0.0f, p, acc);
+      // (stored unconditionally, rows not at risk into spare rows: no branch per slot)
+      s_rrow[(live && ri >= 0 ? ri : kSwRisk + wave) * 16 + vsub] = vd[s];
+      asm volatile("" ::: "memory");
+    }
+    if (vt && (vsub & 3) == 0) s_tsw[(4 * wave + vkk) * 4 + (vsub >> 2)] = xs;
+    if (wave == sp_w) {                        // the appended row, by the lanes of its slot
+      uint2 pw = s_ps[kp];
+      if (vkk != sp_kk) pw = make_uint2(0u, 0u);
+      float p[kGqa];
+      p4(pw, p);
+      v_accum<BKV_Q8_0>(pd, vkk == sp_kk ? pscale : 0.0f, p, acc);
+    }
+  }
+  RTS(13);
+  RTSV(4);
+
+  if (kwave) {
+    // ---------------------------------------------------------------- barrier B, the walk
+    const int h = wave;
+    {
+      unsigned long long v[2];
+      poll_tagged(trec + h * GM * 2, 2, 2, G, tag, v, err);
+      RTS(4);
+      const ChunkRec x = unpack_rec(v[0], v[1]);
+      float sres;
+      bool gres;
+      walk_one<WS>(x, a.spec + (size_t)(g * kGqa + h) * G * kMaxSpecial, G, (int64_t)a.kpw, (int64_t)a.nfill,
+                   s_walk[h], sres, gres);
+      if (lane == 0) {
+        s_S[h] = sres;
+        s_ok[h] = gres ? 1 : 0;
+      }
+    }
+    unsigned kc = kSwKW;                       // K-wave spin barrier target
+    kwave_sync(&s_kctr, kc);
+    RTS(5);
+    if (!(s_ok[0] && s_ok[1] && s_ok[2] && s_ok[3])) {
+      // a classification assumption failed (in every workgroup of the group alike, since all walk
+      // the same records): publish e device-wide and run the serial loop (K waves only)
+      if (!a.keep_e)
+        for (int i = lane; i < nk; i += 64) a.e[(size_t)(g * kGqa + h) * a.ld + kb + i] = s_e[h * KS + i];
+      __builtin_amdgcn_s_waitcnt(0);
+      __threadfence();
+      kwave_sync(&s_kctr, kc += kSwKW);
+      if (tid == 0) {
+        unsigned *c3 = cnt + 3 * kCounterStride;
+        atomicAdd(c3, 1u);
+        unsigned spins = 0;
+        while (ld_agent(c3) < (unsigned)G) {
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins > kResSpin) {
+            atomicOr(err, 1u);
+            break;
+          }
+        }
+      }
+      kwave_sync(&s_kctr, kc += kSwKW);
+      if (!s_ok[h]) {
+        const int hh = g * kGqa + h;
+        float ss = 0.0f;
+        for (int64_t b0 = 0; b0 < (int64_t)a.nfill; b0 += 64) {
+          const int nb = (int)min((int64_t)64, (int64_t)a.nfill - b0);
+          const float x = lane < nb ? ld_agent(&a.e[(size_t)hh * a.ld + b0 + lane]) : 0.0f;
+          for (int i = 0; i < nb; ++i) ss = __fadd_rn(ss, __shfl(x, i));
+        }
+        if (lane == 0) s_S[h] = ss;
+      }
+    }
+    const float S = s_S[h];
+    if (wi == 0 && lane == 0) {
+      a.sum[g * kGqa + h] = S;
+      a.status[g * kGqa + h] = s_ok[h] ? 0u : 1u;
+    }
+    // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296) of head h
+    _Float16 *p16h = reinterpret_cast<_Float16 *>(s_p16);
+    for (int i = lane; i < KS; i += 64) {
+      const bool live = i < np || (i >= NP && i < NP + tn);
+      p16h[i * kGqa + h] = (_Float16)(live ? s_e[h * KS + i] / S : 0.0f);
+    }
+    kwave_sync(&s_kctr, kc += kSwKW);
+    RTS(12);
+    // (p16 - p16') * v for the keys whose rounding the exact sum changed: K wave w checks keys
+    // 64 (w + 4 i) + lane and takes its changed ones in order, 4 at a time (row group vkk takes one):
+    // the at-risk row from LDS, the appended row from s_x, or (a changed key not at risk) the cache
+#pragma unroll 1
+    for (int i = 0; i < 3; ++i) {
+      const int k0 = 64 * (wave + 4 * i), k = k0 + lane;
+      const bool live = k < np || (k >= NP && k < NP + tn);
+      const int kk = min(k, KS - 1);
+      const uint2 pw = s_p16[kk], qw = s_ps[kk];
+      unsigned long long m = __ballot(live && (pw.x != qw.x || pw.y != qw.y));
+      while (m) {
+        int kq[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kq[j] = __builtin_amdgcn_readfirstlane(m ? k0 + (int)__builtin_ctzll(m) : -1);
+          m &= m - 1;
+        }
+        const int kc4 = kq[vkk];
+        uint4 d = make_uint4(0u, 0u, 0u, 0u);
+        float vs = 0.0f, p[kGqa] = {0.f, 0.f, 0.f, 0.f};
+        if (kc4 >= 0) {
+          float q[kGqa];
+          p4(s_p16[kc4], p);
+          p4(s_ps[kc4], q);
+#pragma unroll
+          for (int hh = 0; hh < kGqa; ++hh) p[hh] -= q[hh];
+          if (kc4 == kp) {
+            d = pd;
+            vs = pscale;
+          } else {
+            const int ri = s_ridx[kc4];
+            const uint32_t sw = kc4 < NP ? reinterpret_cast<const uint32_t *>(vsc + ((kc4 % 32) / 4) * 64 + 4 * (kc4 / 32) + kc4 % 4)[vsub >> 2]
+                                         : s_tsw[(kc4 - NP) * 4 + (vsub >> 2)];
+            vs = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+            if (ri >= 0) {
+              d = s_rrow[ri * 16 + vsub];
+            } else {
+              const int64_t sl = slot_k<PG>(sm, kc4);
+              d = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+            }
+          }
+        }
+        v_accum<BKV_Q8_0>(d, vs, p, acc);
+      }
+    }
+    RTS(15);
+  }
+  // the 4 row groups' sums by a reduce-scatter: row group r ends with head r's totals
+  {
+    float red[VR::EPL];
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) {
+      const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[0][i]), __float_as_uint(acc[2][i]), false, false);
+      const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[1][i]), __float_as_uint(acc[3][i]), false, false);
+      const float za = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+      const float zb = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+      const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(za), __float_as_uint(zb), false, false);
+      red[i] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + vkk) * VR::EPL + i) * VR::LPR + vsub] = red[i];
+  }
+  __syncthreads();
+  RTS(10);
+  unsigned long long *part_g = a.part + (size_t)g * G * kGqa * kHd;
+  {
+    static_assert(kGqa * kHd == 2 * NT, "two partial elements per thread");
+    float2 v = make_float2(0.0f, 0.0f);
+    const int hh = (2 * tid) / kHd, dd = (2 * tid) % kHd;
+    const int ro = (hh * VR::EPL + dd % VR::EPL) * VR::LPR + dd / VR::EPL;
+#pragma unroll
+    for (int wv = 0; wv < NW; ++wv) {
+      v.x += s_red[wv * kGqa * kHd + ro];
+      v.y += s_red[wv * kGqa * kHd + ro + VR::LPR];
+    }
+    unsigned long long *dst = part_g + (size_t)wi * kGqa * kHd + 2 * tid;
+    st_agent(dst, (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)gen << 32));
+    st_agent(dst + 1, (unsigned long long)__float_as_uint(v.y) | ((unsigned long long)gen << 32));
+  }
+  RTS(6);
+  __syncthreads();                             // s_red is reused below
+
+  // ---------------------------------------------------------------- merge + gate
+  // workgroup wi sums slice wi of the group's partials in workgroup order, polling each element
+  // until it carries this call's generation
+  {
+    constexpr int E = kGqa * kHd;
+    const int sl = (E + G - 1) / G;
+    const int e0 = wi * sl, ecount = max(0, min(E, e0 + sl) - e0);
+    for (int c0 = 0; c0 < ecount; c0 += NT) {
+      const int ne = min(NT, ecount - c0);
+      const int ngrp = NT / ne;
+      const int el = tid % ne, grp = tid / ne;
+      constexpr int B = 8;
+      float sacc = 0.0f;
+      if (grp < ngrp) {
+        for (int w0 = grp; w0 < G; w0 += ngrp * B) {
+          unsigned long long t[B];
+          unsigned spins = 0;
+          for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < B; ++u) {
+              const int ww = w0 + u * ngrp;
+              t[u] = ww < G ? ld_agent(&part_g[(size_t)ww * E + e0 + c0 + el]) : ((unsigned long long)gen << 32);
+              ok = ok && (unsigned)(t[u] >> 32) == gen;
+            }
+            if (ok) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kResSpin) {
+              atomicOr(err, 1u);
+              break;
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < B; ++u) sacc += __uint_as_float((unsigned)t[u]);
+        }
+        s_red[grp * ne + el] = sacc;
+      }
+      __syncthreads();
+      if (tid < ne) {
+        float v = 0.0f;
+        for (int j = 0; j < ngrp; ++j) v += s_red[j * ne + tid];
+        const int eg = e0 + c0 + tid;
+        const size_t oi = (size_t)g * E + eg;
+        a.out[oi] = v;
+        if (a.gate) a.out_gated[oi] = v * (1.0f / (1.0f + exp_cr(-a.gate[gate_index(oi, a.gs)])));
+      }
+      __syncthreads();
+    }
+  }
+  RTS(7);
+  if (wi == 0 && tid == 0) st_agent(gs, gen);
+  RTS(8);
+}
+
+template <bool PG>
+static int stream_capacity() {
+  static int cap[64];
+  static bool done[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!done[dev]) {
+    int per = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDeviceProperties(&pr, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG>, kResNT, 0) != hipSuccess)
+      cap[dev] = 0;
+    else
+      cap[dev] = per * pr.multiProcessorCount;
+    done[dev] = true;
+  }
+  return cap[dev];
+}
+
+int stream_max_workgroups(bool paged) { return paged ? stream_capacity<true>() : stream_capacity<false>(); }
+
+// A cooperative launch: the runtime refuses a grid whose workgroups cannot all be resident at once,
+// which every wait in the kernel relies on.
+hipError_t launch_stream(const ResArgs &a, hipStream_t st) {
+  const dim3 grid(a.G * a.nkv), block(kResNT);
+  static const bool coop = [] { const char *e = std::getenv("BKV_COOP"); return e && e[0] == '1'; }();
+  if (coop) {
+    ResArgs args = a;
+    void *kp[] = {&args};
+    if (a.L.page) return hipLaunchCooperativeKernel((const void *)stream_kernel<true>, grid, block, kp, 0, st);
+    return hipLaunchCooperativeKernel((const void *)stream_kernel<false>, grid, block, kp, 0, st);
+  }
+  if (a.L.page) hipLaunchKernelGGL((stream_kernel<true>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((stream_kernel<false>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace bkv

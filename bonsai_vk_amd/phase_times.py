@@ -9,6 +9,7 @@ boundary into the workspace at byte 131072 ([workgroup][16] u32). The probe runs
 of one q8_0 layer at ctx keys (256-token pages with --paged), and prints min / median / max over
 the workgroups of the last call, in microseconds from the first workgroup's start.
 """
+import os
 import sys
 
 import numpy as np
@@ -16,7 +17,13 @@ import torch
 
 from bonsai_vk_amd import BKV_Q8_0, KvCache
 
-# slot -> phase, in launch order (slot 15 is wave 7's end of PV; the others are thread 0's)
+# slot -> phase, in launch order, of the default kernel (stream_kernel; thread 0's clocks)
+PHASES_STREAM = [(0, "start"), (14, "K tile landed (wave 0)"), (1, "scores done (wave 0)"),
+                 (9, "stats stored"), (2, "barrier A passed"), (3, "e pass done"),
+                 (13, "spec PV done (wave 0)"), (4, "barrier B passed"), (5, "walk done"),
+                 (12, "p16 done"), (15, "corrections done"), (10, "PV rows reduced"),
+                 (6, "partials stored"), (7, "merge polled"), (8, "end")]
+# the same for resident_kernel (BKV_DECODE=resident; slot 15 is wave 7's end of PV)
 PHASES = [(0, "start"), (1, "scores done (wave 0)"), (2, "barrier A passed"), (10, "e main pass"),
           (11, "e tail + p16'"), (3, "records stored"), (4, "barrier B passed"), (5, "walk done"),
           (12, "p16 done"), (13, "PV done (wave 0)"), (15, "PV done (wave 7)"), (14, "PV rows reduced"),
@@ -43,12 +50,19 @@ def probe(ctx=32768, paged=False, calls=6):
     v = torch.randn(1, 4, 256, device="cuda")
     q = torch.randn(16, 256, device="cuda")
     nwg = torch.cuda.get_device_properties(0).multi_processor_count
-    ts = None
+    ts = tw = None
+    import ctypes
+    from bonsai_vk_amd._lib import lib
     for i in range(calls):
         cache.decode_step(0, ctx + i, k, v, q)
         torch.cuda.synchronize()
         ts = cache.workspace.view(torch.int32)[TS_WORD:TS_WORD + nwg * 16].cpu().numpy()
+        out = (ctypes.c_uint64 * 6)()
+        lib().bkv_debug_layout(ctypes.byref(cache.desc), ctx + i + 1, out)
+        o = (int(out[5]) - 131072) // 4
+        tw = cache.workspace.view(torch.int32)[o:o + nwg * 64].cpu().numpy()
     ts = ts.astype(np.int64).reshape(nwg, 16)
+    probe.per_wave = tw.astype(np.int64).reshape(nwg, 8, 8)[ts[:, 0] != 0]
     if not ts[:, 8].any():
         raise RuntimeError("no timestamps written: load the instrumented build "
                            "(BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so after build --timestamps)")
@@ -58,12 +72,23 @@ def probe(ctx=32768, paged=False, calls=6):
 def main(argv):
     ctx = int(next((a for a in argv if not a.startswith("-")), 32768))
     ts = probe(ctx, "--paged" in argv)
+    phases = PHASES if os.environ.get("BKV_DECODE") == "resident" else PHASES_STREAM
     t0 = ts[:, 0].min()
     print(f"ctx {ctx}{' paged' if '--paged' in argv else ''}: phase clocks in us from the first "
           f"workgroup's start, min / median / max over {len(ts)} workgroups")
-    for slot, name in PHASES:
+    for slot, name in phases:
         col = (ts[:, slot] - t0) / 100.0
         print(f"  {name:22s} {col.min():8.2f} {np.median(col):8.2f} {col.max():8.2f}")
+    pw = getattr(probe, "per_wave", None)
+    if phases is PHASES_STREAM and pw is not None and pw.any():
+        names = ["K tile landed", "tile scored", "tail scored", "max barrier passed", "spec PV done"]
+        print("  per wave (median over workgroups): " + ", ".join(names))
+        for wv in range(8):
+            cells = []
+            for j in range(len(names)):
+                col = pw[:, wv, j]
+                cells.append(f"{(np.median(col) - t0) / 100.0:7.2f}" if col.any() else "      -")
+            print(f"    wave {wv}: " + " ".join(cells))
 
 
 if __name__ == "__main__":

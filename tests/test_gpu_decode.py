@@ -13,7 +13,7 @@ TOL = 1e-4
 pytestmark = pytest.mark.gpu
 
 
-PATHS = {"resident": 2, "fused": 1, "split": 0}
+PATHS = {"stream": 3, "resident": 2, "fused": 1, "split": 0}
 
 
 @pytest.fixture(params=list(PATHS))
@@ -203,8 +203,8 @@ def test_small_pages(kf, vf, page, path):
     say(f"small pages kf={kf} vf={vf} page={page} path={path}")
     dev, host = pair(1, pool * page, kf, vf, page_tokens=page, max_pages=pool, block_table=bt)
     flat, _ = pair(1, pool * page, kf, vf)
-    if path == "resident":
-        assert dev.decode_path(n) == (1 if page == 1 else 2)
+    if path in ("resident", "stream"):
+        assert dev.decode_path(n) == (1 if page == 1 else PATHS[path] if kf == BKV_Q8_0 else 2)
     k, v = fill(dev, host, 0, n, seed=11)
     flat.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
     q, g = qg(11, 0)
@@ -221,9 +221,10 @@ def test_small_pages(kf, vf, page, path):
 
 @pytest.mark.parametrize("n", [32768, 33792, 33793])
 def test_register_v_boundary(n):
-    """The resident kernel's q8_0 form keeps a workgroup's V rows in registers up to 512 + 16 keys:
-    32768 keys (no tail), 33792 (the longest tail) and 33793 (the two-pass form) all match the
-    oracle, through decode_step (the appended token lands in the last workgroup's range)."""
+    """The stream kernel keeps a workgroup's q8_0 V rows in registers up to 512 + 16 keys: 32768
+    keys (no tail) and 33792 (the longest tail) take it, 33793 the resident kernel's two-pass form;
+    all match the oracle, through decode_step (the appended token lands in the last workgroup's
+    range)."""
     say(f"register-V boundary n={n}")
     dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
     fill(dev, host, 0, n - 1, seed=31)
@@ -234,7 +235,7 @@ def test_register_v_boundary(n):
     out, og = dev.decode_step(0, n - 1, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
                               torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
     torch.cuda.synchronize()
-    assert dev.decode_path(n) == 2
+    assert dev.decode_path(n) == (3 if n <= 33792 else 2)
     assert report(f"n={n}", out.cpu().numpy(), want) <= TOL
     assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
     assert same_bytes(dev, host) == [0, 0, 0, 0]
@@ -316,10 +317,11 @@ def test_consecutive_decode_steps(path):
 
 
 def test_decode_path_selection(monkeypatch):
-    """The resident single launch is the default wherever it fits; BKV_DECODE forces the others."""
+    """The stream kernel is the default for q8_0 K and V up to 64 x 528 keys, the resident kernel
+    beyond (and for the other formats); BKV_DECODE forces the others."""
     dev, _ = pair(1, 70000, BKV_Q8_0, BKV_Q8_0)
     monkeypatch.delenv("BKV_DECODE", raising=False)
-    assert dev.decode_path(1) == 2 and dev.decode_path(32769) == 2 and dev.decode_path(65537) == 2
+    assert dev.decode_path(1) == 3 and dev.decode_path(32769) == 3 and dev.decode_path(65537) == 2
     for name, code in PATHS.items():
         monkeypatch.setenv("BKV_DECODE", name)
         assert dev.decode_path(32769) == code
