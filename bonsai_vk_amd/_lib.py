@@ -14,7 +14,7 @@ BKV_PREFILL_MAX_Q = 4096
 
 ERRORS = {
     0: "BKV_OK", -1: "BKV_EINVAL", -2: "BKV_ESHAPE", -3: "BKV_ECAP", -4: "BKV_EALIGN",
-    -5: "BKV_EWORKSPACE", -6: "BKV_EHIP", -7: "BKV_EUNSUPPORTED", -8: "BKV_ETIMEOUT",
+    -5: "BKV_EWORKSPACE", -6: "BKV_EHIP", -7: "BKV_EUNSUPPORTED", -8: "BKV_ETIMEOUT", -9: "BKV_ESCRATCH",
 }
 
 # every symbol include/bkv.h declares
@@ -23,7 +23,7 @@ EXPORTS = [
     "bkv_decode_step", "bkv_attn_prefill_chunk", "bkv_workspace_bytes", "bkv_strerror",
     "bkv_last_hip_error", "bkv_version", "bkv_debug_layout", "bkv_workspace_init", "bkv_decode_path",
     "bkv_kv_fill_synthetic", "bkv_attn_decode_qg", "bkv_decode_step_qg", "bkv_attn_prefill_chunk_qg", "bkv_prefill_step", "bkv_qk_norm_rope_append", "bkv_attn_decode_window",
-    "bkv_workspace_error", "bkv_error_words",
+    "bkv_workspace_error", "bkv_error_words", "bkv_decode_step_static", "bkv_static_scratch_bytes",
 ]
 
 
@@ -86,6 +86,8 @@ def lib():
         "bkv_attn_decode_window": (i32, [D, i32, u32, u32, P, P, P, P, P, sz, P]),
         "bkv_workspace_error": (i32, [D, P, sz, P]),
         "bkv_error_words": (i32, [D, ctypes.POINTER(ctypes.c_uint64)]),
+        "bkv_decode_step_static": (i32, [D, i32, u32, P, P, P, P, P, P, P]),
+        "bkv_static_scratch_bytes": (sz, []),
         "bkv_qk_norm_rope_append": (i32, [D, i32, u32, i32, P, P, P, P, P, i32, ctypes.c_float,
                                           ctypes.c_float, P, P]),
     }

@@ -15,7 +15,7 @@ namespace bkv {
 
 static thread_local char g_hip_err[256] = "";
 
-static int hip_fail(hipError_t e) {
+int hip_fail(hipError_t e) {
   if (e == hipSuccess) return BKV_OK;
   std::snprintf(g_hip_err, sizeof g_hip_err, "%s: %s", hipGetErrorName(e), hipGetErrorString(e));
   return BKV_EHIP;
@@ -632,6 +632,7 @@ const char *bkv_strerror(int err) {
     case BKV_ECAP: return "position outside the cache (pos >= cap) or empty context";
     case BKV_EALIGN: return "pointer or stride not aligned (16 B; workspace 256 B)";
     case BKV_EWORKSPACE: return "workspace missing or smaller than bkv_workspace_bytes()";
+    case BKV_ESCRATCH: return "decode plan larger than the static scratch (bkv_static_scratch_bytes())";
     case BKV_EHIP: return "HIP runtime error (see bkv_last_hip_error)";
     case BKV_EUNSUPPORTED: return "shape not supported by the gfx950 kernels (hd 256, nh = 4*nkv)";
     case BKV_ETIMEOUT: return "a decode kernel's workgroup wait timed out (its output is not valid)";

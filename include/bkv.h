@@ -47,7 +47,8 @@ enum bkv_err {
   BKV_EWORKSPACE  = -5,  /* workspace NULL or smaller than bkv_workspace_bytes()                */
   BKV_EHIP        = -6,  /* the HIP runtime reported an error on launch                         */
   BKV_EUNSUPPORTED = -7, /* a valid request this build does not implement                       */
-  BKV_ETIMEOUT    = -8   /* a decode kernel's bounded wait gave up (bkv_workspace_error)        */
+  BKV_ETIMEOUT    = -8,  /* a decode kernel's bounded wait gave up (bkv_workspace_error)        */
+  BKV_ESCRATCH    = -9   /* the call needs more than bkv_static_scratch_bytes() of workspace    */
 };
 
 /* bkv_workspace_bytes() op codes */
@@ -206,6 +207,20 @@ size_t bkv_workspace_bytes(const bkv_cache_desc *d, int op, uint32_t max_ctx);
  * walker status [nh] u32 (1 = the exact walk fell back to the serial loop), out[5] = workspace
  * bytes needed. Returns BKV_OK or an error for a bad descriptor. */
 int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]);
+
+/* bkv_decode_step with no workspace argument and no allocation anywhere (no counterpart in the
+ * reference; for callers that cannot allocate: code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc). The workspace is a static device array of
+ * bkv_static_scratch_bytes() (16 MiB) per GPU, part of the loaded library, zeroed by a small kernel
+ * on `stream` at the first call on each GPU. Calls whose decode plan needs more than that return
+ * BKV_ESCRATCH before launching anything (about 64K keys at nkv = 4; the exact need is
+ * bkv_debug_layout's out[5]). Every call on one GPU shares that GPU's array: calls that overlap in
+ * time on one GPU (two streams, two threads) race and give wrong results; serialise them. Other
+ * errors and results are those of bkv_decode_step. */
+int bkv_decode_step_static(const bkv_cache_desc *d, int layer, uint32_t pos,
+                           const float *k, const float *v, const float *q, const float *gate,
+                           float *out, float *out_gated, hipStream_t stream);
+size_t bkv_static_scratch_bytes(void);
 
 /* Human-readable text of an enum bkv_err value (static storage). */
 const char *bkv_strerror(int err);
