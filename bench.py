@@ -123,7 +123,6 @@ def kernel_name(cache, n):
                "exact sum, PV, merge)",
             2: "resident_kernel (one launch per layer, one workgroup per CU: append, QK, exact sum, "
                "PV, merge)",
-            1: "fused_kernel (one launch per layer: append, QK, exact sum, PV, merge)",
             0: "qk_kernel + e_kernel + pv_kernel + merge_kernel (four launches per layer)"}[cache.decode_path(n)]
 
 
@@ -131,7 +130,7 @@ def measured_traffic(cache, n):
     """HBM bytes per launch of the single-launch kernel this workload takes, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_q8_32k_traffic.json), or None when
     that summary is absent or the call takes the split path."""
-    name = {3: "stream_kernel", 2: "resident_kernel", 1: "fused_kernel"}.get(cache.decode_path(n))
+    name = {3: "stream_kernel", 2: "resident_kernel"}.get(cache.decode_path(n))
     path = os.path.join(ROOT, "profiles", f"{name}_q8_32k_traffic.json")
     if name is None or not os.path.exists(path):
         return None

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbkv.so")
 LIB_TS = os.path.join(HERE, "libbkv_ts.so")
-SOURCES = ["bkv_api.cpp", "bkv_decode.hip", "bkv_fused.hip", "bkv_resident.hip", "bkv_stream.hip", "bkv_prefill.hip", "bkv_norm_rope.hip", "bkv_static.hip"]
+SOURCES = ["bkv_api.cpp", "bkv_decode.hip", "bkv_resident.hip", "bkv_stream.hip", "bkv_prefill.hip", "bkv_norm_rope.hip", "bkv_static.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

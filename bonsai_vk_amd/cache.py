@@ -288,7 +288,7 @@ class KvCache:
         check(lib().bkv_kv_fill_synthetic(ctypes.byref(self.desc), self._stream()), "bkv_kv_fill_synthetic")
 
     def decode_path(self, nfill):
-        """2: resident single launch (the default), 1: fused single launch, 0: split path"""
+        """3: stream single launch (the default for q8_0 K and V), 2: resident single launch, 0: split path"""
         return lib().bkv_decode_path(ctypes.byref(self.desc), nfill)
 
     def check_workspace(self):
@@ -297,11 +297,11 @@ class KvCache:
         check(lib().bkv_workspace_error(ctypes.byref(self.desc), self.workspace.data_ptr(),
                                         self.workspace.numel(), self._stream()), "bkv_workspace_error")
 
-    def error_word_offsets(self):
-        """Byte offsets of the resident and fused kernels' error words in the workspace."""
-        out = (ctypes.c_uint64 * 2)()
+    def error_word_offset(self):
+        """Byte offset of the single-launch kernels' error word in the workspace."""
+        out = (ctypes.c_uint64 * 1)()
         check(lib().bkv_error_words(ctypes.byref(self.desc), out), "bkv_error_words")
-        return int(out[0]), int(out[1])
+        return int(out[0])
 
     # ---------------------------------------------------------------- inspection
     def debug_intermediates(self, nfill):

@@ -31,17 +31,15 @@ static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Partition sizes of the split path. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16
 // keys). Probability chunks: kE2Chunk keys. PV: enough workgroups to cover the chip (512 at nkv = 4)
-// with 16..512 keys each. The fused path: as many workgroups per KV group as stay resident (at most
-// kFusedMaxGroupWgs), each with kpw consecutive keys in at most kRMax passes. Every array is sized
+// with 16..512 keys each. Every array is sized
 // by a bound that grows monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx.
 // BKV_DECODE selects a decode implementation: "split" (four launches), "fused" (the older single
 // launch) or "resident" (the default). Read on every call, so tests can switch it.
-enum { kPathSplit = 0, kPathFused = 1, kPathResident = 2, kPathStream = 3 };
+enum { kPathSplit = 0, kPathResident = 2, kPathStream = 3 };
 static int forced_path() {
   const char *e = std::getenv("BKV_DECODE");
   if (!e) return -1;
   if (std::strcmp(e, "split") == 0) return kPathSplit;
-  if (std::strcmp(e, "fused") == 0) return kPathFused;
   if (std::strcmp(e, "resident") == 0) return kPathResident;
   if (std::strcmp(e, "stream") == 0) return kPathStream;
   return -1;
@@ -112,7 +110,10 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
   p.ld = cdiv(n, kE2Chunk) * kE2Chunk;
   const int64_t nq_bound = cdiv(n, 128);
   const int64_t np_bound = std::max<int64_t>(128, cdiv(n, kPvMaxChunk));
-  size_t o = kSyncBytes;
+  // the single-launch kernels' tagged partials sit at a fixed offset that no other array of any
+  // plan overlaps: a poll never sees bytes another path (or another context length) left there
+  const size_t tagged_part = align256((size_t)nkv * kResMaxGroupWgs * kGqa * kHd * sizeof(unsigned long long));
+  size_t o = kSyncBytes + tagged_part;
   p.off_score = o;  o += align256((size_t)nh * p.ld * sizeof(float));
   p.off_e = o;      o += align256((size_t)nh * p.ld * sizeof(float));
   p.off_stats = o;  o += align256((size_t)nh * nq_bound * sizeof(float2));
@@ -124,34 +125,6 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
   p.off_dbg = o;    o += align256((size_t)nh * 8 * sizeof(unsigned long long));
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
   size_t total = o;
-  // the fused single-launch path: as many workgroups per KV group as stay resident
-  const int cap = fused_max_workgroups(kfmt, vfmt);
-  p.gg = 0;
-  p.rsub = 0;
-  // the sync lines of all groups and the 11 top lines must end below the running-max slots
-  const bool sync_fits = ((size_t)nkv * kGroupLines + 11) * kCounterStride * sizeof(unsigned) <= kSyncMaxOffset;
-  if (cap >= nkv && sync_fits) {
-    const int64_t pass = fused_keys_per_pass(kfmt);
-    const int64_t kpw = cdiv(n, std::min<int64_t>({cdiv(n, pass), cap / nkv, (int64_t)kFusedMaxGroupWgs}));
-    const int64_t rs = cdiv(kpw, pass);
-    const int64_t gg = cdiv(n, kpw);               // no workgroup without keys
-    if (rs <= kRMax) {
-      p.kpw = (int)kpw;
-      p.gg = (int)gg;
-      p.rsub = (int)rs;
-      size_t f = kSyncBytes;
-      p.f_stats = f;  f += align256((size_t)nh * gg * sizeof(float2));
-      p.f_sub = f;    f += align256((size_t)nkv * kMergeSub * kGqa * kHd * sizeof(float));
-      p.f_rec = f;    f += align256((size_t)nh * gg * sizeof(ChunkRec));
-      p.f_spec = f;   f += align256((size_t)nh * gg * kMaxSpecial * sizeof(Special));
-      p.f_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
-      p.f_sum = f;    f += align256((size_t)nh * sizeof(float));
-      p.f_status = f; f += align256((size_t)nh * sizeof(unsigned));
-      p.f_part = f;   f += align256((size_t)nkv * gg * kGqa * kHd * sizeof(float));
-      p.f_total = f;
-      total = std::max(total, f);
-    }
-  }
   // the resident path: one workgroup per CU, up to kResMaxG per KV group, >= 128 keys each
   // (below 16K keys fewer, longer workgroups finish sooner: 4K keys run 4 % faster at 32 per group than at 64)
   p.rG = 0;
@@ -169,12 +142,12 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
       p.rG = (int)cdiv(n, kpw);
       p.rvres = vfmt == BKV_Q8_0 && kfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
       p.rstream = p.rvres && p.rG * nkv <= stream_max_workgroups(page > 0);
-      size_t f = kSyncBytes;
+      p.r_part = kSyncBytes;
+      size_t f = kSyncBytes + tagged_part;
       p.r_spec = f;   f += align256((size_t)nh * gmax * kMaxSpecial * sizeof(Special));
       p.r_e = f;      f += align256((size_t)nh * p.ld * sizeof(float));
       p.r_sum = f;    f += align256((size_t)nh * sizeof(float));
       p.r_status = f; f += align256((size_t)nh * sizeof(unsigned));
-      p.r_part = f;   f += align256((size_t)nkv * gmax * kGqa * kHd * sizeof(unsigned long long));
       p.r_total = f;
       total = std::max(total, f);
     }
@@ -198,11 +171,10 @@ static bool keep_intermediates() {
 static int choose_path(const DecodePlan &p) {
   const int f = forced_path();
   if (f == kPathSplit) return kPathSplit;
-  if (f == kPathFused) return p.gg > 0 ? kPathFused : kPathSplit;
   if (f == kPathResident && p.rG > 0) return kPathResident;
   if (p.rstream) return kPathStream;
   if (p.rG > 0) return kPathResident;
-  return p.gg > 0 ? kPathFused : kPathSplit;
+  return kPathSplit;
 }
 
 static bool aligned16(const void *p) { return p && ((uintptr_t)p & 15u) == 0; }
@@ -310,10 +282,6 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
     ra.spec = (Special *)(w + p.r_spec);
     ra.e = (float *)(w + p.r_e);
     ra.keep_e = keep_intermediates() ? 1 : 0;
-    {
-      const char *vs = std::getenv("BKV_VSTAGE");
-      ra.vstage = vs ? std::atoi(vs) : 3;
-    }
     ra.sum = (float *)(w + p.r_sum);
     ra.status = (unsigned *)(w + p.r_status);
     ra.part = (unsigned long long *)(w + p.r_part);
@@ -324,27 +292,6 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
 #endif
     if (path == kPathStream) return hip_fail(launch_stream(ra, st));
     return hip_fail(launch_resident(ra, d->k_fmt, d->v_fmt, p.rvres, st));
-  }
-  if (path == kPathFused) {
-    FusedArgs fa{};
-    fa.L = L; fa.nkv = d->nkv; fa.nfill = nfill; fa.scale = d->scale; fa.gg = p.gg; fa.rsub = p.rsub; fa.kpw = p.kpw;
-    fa.ld = p.ld; fa.q = q; fa.qs = qs; fa.gs = gs;
-    if (fused) fa.ap = *fused;
-    fa.gate = gate; fa.out = out; fa.out_gated = out_gated;
-    fa.stats = (float2 *)(w + p.f_stats);
-    fa.mxenc = (unsigned *)(w + kSyncMaxOffset);   // fixed: the slots outlive a call
-    fa.nh = d->nh;
-    fa.subpart = (float *)(w + p.f_sub);
-    fa.rec = (ChunkRec *)(w + p.f_rec);
-    fa.spec = (Special *)(w + p.f_spec);
-    fa.e = (float *)(w + p.f_e);
-    fa.sum = (float *)(w + p.f_sum);
-    fa.status = (unsigned *)(w + p.f_status);
-    fa.part = (float *)(w + p.f_part);
-    fa.sync = (unsigned *)w;
-    const hipError_t e = launch_fused(fa, d->k_fmt, d->v_fmt, fused != nullptr, st);
-    if (e == hipSuccess) return BKV_OK;
-    (void)hipGetLastError();           // e.g. a cooperative grid the device cannot hold: split path
   }
 
   QkArgs qa{};
@@ -640,17 +587,16 @@ const char *bkv_strerror(int err) {
   }
 }
 
-// byte offsets of the resident and fused kernels' error words (see their sync-line layouts)
-static void error_word_offsets(int nkv, uint64_t out[2]) {
-  out[0] = kResSyncOffset + (uint64_t)nkv * kResGroupLines * kCounterStride * sizeof(unsigned);
-  out[1] = ((uint64_t)nkv * kGroupLines + 10) * kCounterStride * sizeof(unsigned);
+// byte offset of the single-launch kernels' error word (past their sync lines)
+static uint64_t error_word_offset(int nkv) {
+  return kResSyncOffset + (uint64_t)nkv * kResGroupLines * kCounterStride * sizeof(unsigned);
 }
 
-int bkv_error_words(const bkv_cache_desc *d, uint64_t out[2]) {
+int bkv_error_words(const bkv_cache_desc *d, uint64_t out[1]) {
   const int rc = check(d);
   if (rc) return rc;
   if (!out) return BKV_EINVAL;
-  error_word_offsets(d->nkv, out);
+  out[0] = error_word_offset(d->nkv);
   return BKV_OK;
 }
 
@@ -658,8 +604,7 @@ int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_byte
   const int rc = check(d);
   if (rc) return rc;
   if (!workspace || ws_bytes < kSyncBytes) return BKV_EWORKSPACE;
-  uint64_t off[2];
-  error_word_offsets(d->nkv, off);
+  const uint64_t off[1] = {error_word_offset(d->nkv)};
   hipError_t e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e);
   int result = BKV_OK;
@@ -667,11 +612,15 @@ int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_byte
     unsigned v = 0;
     char *p = static_cast<char *>(workspace) + o;
     if ((e = hipMemcpy(&v, p, sizeof v, hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e);
-    if (v) {
-      const unsigned zero = 0;
-      if ((e = hipMemcpy(p, &zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e);
-      result = BKV_ETIMEOUT;
-    }
+    if (v) result = BKV_ETIMEOUT;
+  }
+  if (result == BKV_ETIMEOUT) {
+    // a call that gave up left its counters and tags mid-protocol: start the workspace afresh (this
+    // also clears the error word), as bkv_workspace_init does
+    if (ws_bytes / sizeof(unsigned) > 0x7FFFFFFFull) return BKV_EINVAL;
+    if ((e = launch_workspace_init((unsigned *)workspace, (int)(ws_bytes / sizeof(unsigned)), stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(stream)) != hipSuccess)
+      return hip_fail(e);
   }
   return result;
 }
@@ -685,9 +634,9 @@ int bkv_debug_layout(const bkv_cache_desc *d, uint32_t nfill, uint64_t out[6]) {
   out[0] = (uint64_t)p.ld;
   out[1] = path == kPathSplit ? p.off_score : 0;
   const bool res = path == kPathResident || path == kPathStream;
-  out[2] = res ? p.r_e : path == kPathFused ? p.f_e : p.off_e;
-  out[3] = res ? p.r_sum : path == kPathFused ? p.f_sum : p.off_sum;
-  out[4] = res ? p.r_status : path == kPathFused ? p.f_status : p.off_status;
+  out[2] = res ? p.r_e : p.off_e;
+  out[3] = res ? p.r_sum : p.off_sum;
+  out[4] = res ? p.r_status : p.off_status;
   out[5] = p.total;
   return BKV_OK;
 }

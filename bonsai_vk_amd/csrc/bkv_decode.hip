@@ -180,19 +180,12 @@ __global__ __launch_bounds__(256) void e_kernel(EArgs a) {
     r.blast = s_bin[n - 1];
     st_rec(&a.rec[(size_t)h * a.nch + c], r);
   }
-#ifdef BKV_EXPERIMENT_NOWALK
-  return;
-#endif
   __builtin_amdgcn_s_waitcnt(0);      // this thread's write-through stores have completed
   __syncthreads();
   if (tid == 0) s_last = atomicAdd(&a.counters[h * kCounterStride], 1u) == (unsigned)(a.nch - 1) ? 1u : 0u;
   __syncthreads();
   if (!s_last) return;
   TS(0);
-#ifdef BKV_EXPERIMENT_NOWALK2
-  if (tid == 0) { a.sum[h] = 1.0f; a.status[h] = 0; }
-  return;
-#endif
 
   // ---- the walk (last workgroup of head h). Every field of a special is resolved in parallel -
   // its global key index, the global increment prefix before it, the binade of the step before
@@ -446,6 +439,29 @@ hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, co
     hipLaunchKernelGGL((pv_kernel<VF_>), dim3(pa.nch, pa.nkv), dim3(256), 0, st, pa);
   });
   hipLaunchKernelGGL(merge_kernel, dim3(ra.nh, 4), dim3(256), 0, st, ra);
+  return hipGetLastError();
+}
+
+// zero a workspace (bkv_workspace_init) and fill cache arrays (bkv_kv_fill_synthetic): kernels,
+// not memsets, so that the calls can sit inside a captured graph
+__global__ void workspace_init_kernel(unsigned *sync, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) sync[i] = 0u;
+}
+
+hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st) {
+  const int blocks = (int)std::min<long long>(1024, ((long long)nwords + 255) / 256);
+  hipLaunchKernelGGL(workspace_init_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, sync, nwords);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void fill_words_kernel(unsigned *p, size_t n, unsigned value) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = value;
+}
+
+hipError_t launch_fill_words(unsigned *p, size_t nwords, unsigned value, hipStream_t st) {
+  if (nwords == 0) return hipSuccess;
+  const int blocks = (int)std::min<size_t>(4096, (nwords + 255) / 256);
+  hipLaunchKernelGGL(fill_words_kernel, dim3(blocks), dim3(256), 0, st, p, nwords, value);
   return hipGetLastError();
 }
 

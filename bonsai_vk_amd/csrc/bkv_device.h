@@ -81,10 +81,6 @@ __device__ __forceinline__ void append_token(const AppendArgs &a, int64_t pos, i
 // d%16, so the shared operand costs no LDS or scalar traffic.
 template <int N>
 __device__ __forceinline__ void fmac_bc(float &acc, float q, float k) {
-#ifdef BKV_EXPERIMENT_NODPP
-  acc = fmaf(q, k, acc);
-  return;
-#endif
   asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
       : "+v"(acc)
       : "v"(q), "v"(k), "n"(N));
@@ -381,7 +377,6 @@ struct WalkScratchT {
   int sck[CAP];                    // binade exponent field the step must start and end in, -1: no advance
   int sdu[CAP];                    // ulps the sum advances by before the special (0: none)
 };
-using WalkScratch = WalkScratchT<kFusedMaxGroupWgs, 384>;
 
 #ifdef BKV_EXPERIMENT_TS
 #define WTS(q, i) do { if (tsp[q] && (threadIdx.x & 63) == 0) tsp[q][i] = (unsigned)wall_clock64(); } while (0)

@@ -90,41 +90,8 @@ struct RedArgs {
   float *out, *out_gated;
 };
 
-constexpr int kRMax = 2;                     // key passes per workgroup of the fused kernel
-// workgroups per KV group of the fused launch at most (the walker's LDS scratch holds this many)
-constexpr int kFusedMaxGroupWgs = 192;
-// merge sub-groups of the fused kernel (the sub-partials buffer holds kMergeSub per KV group) and the
-// 256 B sync lines each KV group uses: 3 counters, 3 flags, 8 + 8 phase sub-counters, kMergeSub
-constexpr int kMergeSub = 16;
-constexpr int kGroupLines = 22 + kMergeSub;
 constexpr size_t kSyncBytes = 256 * 1024;  // counters / flags at the start of every workspace
-constexpr size_t kSyncMaxOffset = 192 * 1024;   // the fused kernel's running-max slots [2][nh]
 
-struct FusedArgs {
-  LayerView L;
-  int nkv;
-  uint32_t nfill;
-  float scale;
-  int gg, rsub;                  // workgroups per KV group, 256-key sub-chunks per workgroup
-  int kpw;                       // keys per workgroup (the last one may hold fewer)
-  int64_t ld;
-  const float *q;                // [nh][hd], head rows qs floats apart
-  AppendArgs ap;
-  const float *gate;             // head rows gs floats apart
-  int qs, gs;
-  float *out, *out_gated;
-  float2 *stats;                 // [nh][gg]
-  unsigned *mxenc;               // [2][nh] running max (order-preserving bits), by call parity
-  int nh;
-  float *subpart;                // [nkv][kMergeSub][kGqa][hd]
-  ChunkRec *rec;                 // [nh][gg]
-  Special *spec;                 // [nh][gg][kMaxSpecial]
-  float *e;                      // [nh][ld]
-  float *sum;                    // [nh]
-  unsigned *status;              // [nh]
-  float *part;                   // [nkv][gg][kGqa][hd]
-  unsigned *sync;                // kSyncBytes
-};
 
 // ------------------------------------------------------------------ the resident decode kernel
 // One 512-thread workgroup per CU, G workgroups per KV group, every workgroup resident; a
@@ -162,7 +129,6 @@ struct ResArgs {
   unsigned *sync;                // the resident kernel's sync lines
   unsigned *ts;                  // phase timestamps (experiment builds), or null
   unsigned *tsw;                 // per-wave phase timestamps [workgroup][8 waves][8] (experiment builds)
-  int vstage;                    // stream kernel: when the V waves start their loads (tuning)
 };
 
 // ------------------------------------------------------------------ chunked prefill (MFMA)
@@ -244,9 +210,6 @@ struct DecodePlan {
   int64_t ld;
   size_t off_score, off_e, off_stats, off_rec, off_spec, off_cnt, off_sum, off_status, off_dbg, off_part,
       total;
-  // fused path (gg == 0: not available for this nfill)
-  int gg, rsub, kpw;
-  size_t f_stats, f_sub, f_rec, f_spec, f_e, f_sum, f_status, f_part, f_total;
   // resident path (rG == 0: not available for this nfill)
   int rG, rkpw;
   bool rvres, rstream;
@@ -257,9 +220,6 @@ struct DecodePlan {
 DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t nfill, int page = 0);
 int qk_keys_per_wg(int kfmt);
 
-int fused_max_workgroups(int kf, int vf);
-int fused_keys_per_pass(int kf);
-hipError_t launch_fused(const FusedArgs &a, int kf, int vf, bool fuse, hipStream_t st);
 int resident_max_workgroups(int kf, int vf);
 hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st);
 int stream_max_workgroups(bool paged);

@@ -182,18 +182,21 @@ int bkv_attn_prefill_chunk_qg(const bkv_cache_desc *d, int layer, uint32_t pos0,
  * Vulkan fences abort on a device loss; for callers that check their results). The single-launch
  * decode kernels synchronise their workgroups with bounded polls. A poll that runs out (the grid
  * was not co-resident, e.g. another kernel held CUs) sets an error word in the workspace, and that
- * call's output is not valid. This synchronises `stream`, returns BKV_ETIMEOUT if any error word
- * is set (and clears them), else BKV_OK. */
+ * call's output is not valid. This synchronises `stream`, returns BKV_ETIMEOUT if the error word
+ * is set, else BKV_OK. After a timeout it re-initialises the whole workspace (ws_bytes bytes, as
+ * bkv_workspace_init does; this clears the word), because the call that gave up left the
+ * workspace's counters mid-protocol; later calls then run normally. */
 int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_bytes, hipStream_t stream);
 
-/* Diagnostics: byte offsets in the workspace of the error words bkv_workspace_error reads
- * (out[0]: resident kernel, out[1]: fused kernel). */
-int bkv_error_words(const bkv_cache_desc *d, uint64_t out[2]);
+/* Diagnostics: byte offset in the workspace of the error word bkv_workspace_error reads (out[0];
+ * the stream and resident kernels share it). */
+int bkv_error_words(const bkv_cache_desc *d, uint64_t out[1]);
 
-/* Which decode implementation a call with nfill keys takes on the current device: 2 = the resident
- * single launch (one workgroup per CU, the default), 1 = the older fused single launch, 0 = the
- * four-launch split path; -1 = bad arguments. The environment variable BKV_DECODE = split | fused |
- * resident forces one (read on every call). */
+/* Which decode implementation a call with nfill keys takes on the current device: 3 = the stream
+ * single launch (q8_0 K and V, up to 528 keys per workgroup: the default where it applies), 2 = the
+ * resident single launch (every format, up to 2048 keys per workgroup), 0 = the four-launch split
+ * path (everything else); -1 = bad arguments. The environment variable BKV_DECODE = split |
+ * resident | stream forces one where its plan fits (read on every call). */
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill);
 
 /* Workspace needed by op (enum bkv_op) for contexts up to max_ctx positions (prefill: max_ctx is

@@ -9,7 +9,7 @@ import torch
 
 import oracle
 from bonsai_vk_amd import BKV_F16, BKV_Q8_0
-from tests.gpu_util import fill, pair, qg, report, say
+from tests.gpu_util import fill, pair, qg, report, same_bytes, say
 
 TOL = 1e-4
 pytestmark = pytest.mark.gpu
@@ -130,10 +130,35 @@ def test_config5_full_layer():
     out, og = dev.prefill_step(0, pos0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
                                torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
     torch.cuda.synchronize()
-    from tests.gpu_util import same_bytes
     assert not any(same_bytes(dev, host))
     assert report("config5 all rows", out.cpu().numpy(), want) <= TOL
     assert report("config5 all rows, gated", og.cpu().numpy(), wg) <= TOL
+
+
+def test_config5_8_layers():
+    """BASELINE config 5 on all 8 layers: per layer its own 8192 cached tokens and 512-token chunk
+    (q8_0 K+V, seed 4, layer-dependent draws), prefill_step on each layer into one 8-layer cache.
+    Every cache byte of every layer, and every one of the 512 x 16 output rows (and gated rows) of
+    every layer, against the oracle."""
+    pos0, n_q, layers = 8192, 512, 8
+    dev, host = pair(layers, pos0 + n_q, BKV_Q8_0, BKV_Q8_0)
+    worst = 0.0
+    for layer in range(layers):
+        say(f"config5 layer {layer}")
+        fill(dev, host, layer, pos0, seed=4 + layer, outliers=0)
+        k, v = oracle.synth_kv(n_q, 4, 256, 4, layer, outliers=0, stream_base=70000)
+        q, g = qg(4, layer, n=n_q)
+        host.append(layer, pos0, k, v)
+        want, wg = host.prefill(layer, pos0, q, g, nthreads=16)
+        out, og = dev.prefill_step(layer, pos0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                   torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+        torch.cuda.synchronize()
+        worst = max(worst, report(f"config5 layer {layer}", out.cpu().numpy(), want),
+                    report(f"config5 layer {layer}, gated", og.cpu().numpy(), wg))
+    diffs = same_bytes(dev, host)
+    say(f"config5 8 layers: cache byte diffs {diffs}")
+    assert diffs == [0] * len(diffs)
+    assert worst <= TOL
 
 
 def test_prefill_errors():
