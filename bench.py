@@ -10,7 +10,8 @@ A second object on the same line, "prefill", times BASELINE config 5: 512 new q8
 onto an 8192-token cache, then causal GQA attention for the 512 queries over 8 layers
 (bkv_attn_prefill_chunk), on the exact path (the default) and on the MFMA-order variant.
 A third, "other_configs", gives us/token and roofline fractions of BASELINE configs 2 (8 layers at
-4096 keys) and 4 (65536 keys, 256-token pages of a 320-page pool, f16 and q8_0).
+4096 keys) and 4 (65536 keys, 256-token pages of a 320-page pool, f16 and q8_0), and of config 3's
+shape with fp16 K + q8_0 V and with the gate read and the gated output written.
 
     python bench.py [--steps 48] [--warmup 4] [--ctx 32768] [--no-cpu] [--no-prefill] [--no-configs]
 """
@@ -40,9 +41,16 @@ def algorithmic_bytes_f16(n):
     return 4096 * n + 45056
 
 
-def time_decode(cache, layers, n0, steps, warmup, seed):
+def algorithmic_bytes_f16k_q8v(n, gated=False):
+    """As algorithmic_bytes for f16 K (2048 B/key) and q8_0 V (1088 B/key): read 3136 B/key, append
+    write 3136 B, K/V input 8192 B, Q 16384 B, out 16384 B (+ gate 32768 B)."""
+    return 3136 * n + 44096 + (32768 if gated else 0)
+
+
+def time_decode(cache, layers, n0, steps, warmup, seed, gated=False):
     """Mean us/token of `steps` decode_steps x `layers` layers over keys n0 + 1 .. (after `warmup`
-    untimed ones, which the caller counts into n0), with HIP events around the timed region."""
+    untimed ones, which the caller counts into n0), with HIP events around the timed region.
+    gated: each call also reads a gate and writes the gated output."""
     import torch
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -50,13 +58,16 @@ def time_decode(cache, layers, n0, steps, warmup, seed):
     knew = torch.randn(tot, layers, 1, 4, 256, generator=g, device="cuda")
     vnew = torch.randn(tot, layers, 1, 4, 256, generator=g, device="cuda") * 0.5
     q = torch.randn(tot, layers, 16, 256, generator=g, device="cuda")
+    gate = torch.randn(tot, layers, 16, 256, generator=g, device="cuda") if gated else None
     out = torch.empty(layers, 16, 256, device="cuda")
+    og = torch.empty(layers, 16, 256, device="cuda") if gated else None
     base = n0 - warmup
 
     def step(i):
         for layer in range(layers):
-            cache.decode_step(layer, base + i, knew[i, layer], vnew[i, layer], q[i, layer], None,
-                              out[layer])
+            cache.decode_step(layer, base + i, knew[i, layer], vnew[i, layer], q[i, layer],
+                              None if gate is None else gate[i, layer], out[layer],
+                              None if og is None else og[layer])
 
     for i in range(warmup):
         step(i)
@@ -95,6 +106,17 @@ def other_configs(steps=16, warmup=2):
         us = time_decode(cache, L, 65536, steps, warmup, seed=13)
         b = sum(L * fb(65537 + i) for i in range(steps)) / steps
         res[name] = {"us_per_token": round(us, 2), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del cache
+    # config 3's shape with fp16 K and q8_0 V, and with the gate (q8_0 K+V)
+    for name, kf, fb, gated in (("config3_f16k_q8v_32k", BKV_F16, algorithmic_bytes_f16k_q8v, False),
+                                ("config3_q8_32k_gated", BKV_Q8_0, algorithmic_bytes, True)):
+        torch.cuda.empty_cache()
+        cache = KvCache(n_layers=L, cap=32768 + steps + 1, k_fmt=kf, v_fmt=BKV_Q8_0)
+        gen_cache(cache, 32768 - warmup, seed=2, layers=L)
+        us = time_decode(cache, L, 32768, steps, warmup, seed=17, gated=gated)
+        b = sum(L * fb(32769 + i, gated) for i in range(steps)) / steps
+        res[name] = {"us_per_token": round(us, 2), "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "path": {3: "stream", 2: "resident", 0: "split"}[cache.decode_path(32769)]}
         del cache
     torch.cuda.empty_cache()
     return res
@@ -138,33 +160,69 @@ def measured_traffic(cache, n):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def cpu_baseline(ctx, seed=2):
-    """The CPU oracle (serial per head row, OpenMP over the 16 rows of a layer) on a bounded sample:
-    one layer's decode step at ctx+1 keys, scaled to 8 layers. Returns the baseline object."""
+def host_threads():
+    """(threads this process may run on, the machine's logical CPU count)"""
+    n = os.cpu_count() or 1
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else n
+    return max(1, aff), n
+
+
+def cpu_baseline(ctx, seed=2, budget_s=12.0):
+    """The reference's own CPU path on the host cores: its compiled mirror (oracle/_ref
+    ref_decode_rows: attn_vk.h:156-212 score / softmax / P16 / PV / gate per head row) over the 128
+    (layer, head) rows of one decode token at ctx+1 keys, OpenMP over every core this process may
+    use. The mirror's arenas are fp16 (the reference's CPU twin has no q8_0 path), one distinct arena
+    per layer. Beside it: the same rows single-threaded (one row x 128) and this build's CPU oracle
+    on the q8_0 cache (one layer x 8). Returns the baseline object."""
+    import ctypes
     import numpy as np
     import oracle
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
+    cores, nproc = host_threads()
     n = ctx + 1
+    res = {"unit": "us/token", "cores": cores, "nproc": nproc}
+    R = oracle.ref()
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    if R is not None:
+        rng = np.random.default_rng(seed)
+        L, words = 8, n * 4 * 128
+        kc = np.empty((L, words), np.uint32)
+        vc = np.empty((L, words), np.uint32)
+        for l in range(L):
+            kc[l] = rng.standard_normal(2 * words, np.float32).astype(np.float16).view(np.uint32)
+            vc[l] = (rng.standard_normal(2 * words, np.float32) * 0.5).astype(np.float16).view(np.uint32)
+        q16 = rng.standard_normal((L * 16, 256), np.float32).astype(np.float16).view(np.uint32).copy()
+        gate = rng.standard_normal((L * 16, 256), np.float32)
+        out = np.empty((L * 16, 256), np.float32)
+        args = lambda layers, thr: (256, 16, 4, ctypes.c_float(0.0625), layers, P(q16), P(kc), P(vc), words, n,
+                                    P(gate), P(out), thr)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < 100):
+            R.ref_decode_rows(*args(L, cores))
+            reps += 1
+        per_token = (time.perf_counter() - t0) / reps
+        t1 = time.perf_counter()
+        R.ref_decode_rows(*args(1, 1))             # one layer's 16 rows on one thread
+        single = (time.perf_counter() - t1) * 8
+        res.update({"value": per_token * 1e6, "kind": "reference",
+                    "sample": f"reference mirror (oracle/_ref ref_decode_rows) over 8 layers x 16 heads "
+                              f"at {n} fp16 keys, {reps} tokens on {cores} threads",
+                    "single_thread_us_per_token": single * 1e6})
+        del kc, vc
+    # this build's oracle on the q8_0 workload itself
     host = oracle.HostCache(n_layers=1, cap=n, k_fmt=oracle.Q8_0, v_fmt=oracle.Q8_0)
     k, v = oracle.synth_kv(n, 4, 256, seed, 0, outliers=3)
     host.append(0, 0, k, v)
     q = oracle.normal(16 * 256, seed, 5).reshape(16, 256)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < budget_s / 2 and reps < 100):
         host.decode(0, n, q, nthreads=cores)
         reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 1000:
-            break
     per_layer = (time.perf_counter() - t0) / reps
-    t1 = time.perf_counter()
-    host.decode_heads(0, n, q, 0, 1)          # one head row single-threaded, x16 rows
-    single = (time.perf_counter() - t1) * 16
-    return {"value": per_layer * 8 * 1e6, "unit": "us/token", "cores": cores, "kind": "port",
-            "sample": f"oracle decode of 1 layer (16 heads) at {n} q8_0 keys, {reps} reps, x8 layers",
-            "single_thread_us_per_token": single * 8 * 1e6,
-            "host_gbs": algorithmic_bytes(n) / per_layer / 1e9}
+    res["port_q8_us_per_token"] = per_layer * 8 * 1e6
+    res["port_sample"] = f"CPU oracle decode of 1 layer (16 heads) at {n} q8_0 keys, {reps} reps, x8 layers"
+    if "value" not in res:                     # the reference checkout was absent where oracle/_ref was built
+        res.update({"value": res["port_q8_us_per_token"], "kind": "port", "sample": res["port_sample"]})
+    return res
 
 
 VALU_FMA_PEAK = 256 * 64 * 2.4e9     # fp32 FMA lane-ops/s without packed math (256 CUs, 64 lanes, 2.4 GHz)
@@ -227,7 +285,7 @@ def prefill_leg(cpu=True, reps=5):
     if cpu:
         import numpy as np
         import oracle
-        cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+        cores = host_threads()[0]
         host = oracle.HostCache(n_layers=1, cap=n, k_fmt=oracle.Q8_0, v_fmt=oracle.Q8_0)
         kk, vv = oracle.synth_kv(n, 4, 256, 4, 0, outliers=0)
         host.append(0, 0, kk, vv)

@@ -90,6 +90,9 @@ def ref():
         L.ref_decode_row.restype = None
         L.ref_decode_row.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, P, P, P,
                                      ctypes.c_int, ctypes.c_int, P, P, P, P, P, P]
+        L.ref_decode_rows.restype = None
+        L.ref_decode_rows.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, P,
+                                      P, P, ctypes.c_size_t, ctypes.c_int, P, P, ctypes.c_int]
         L.ref_norm_rope_row.restype = None
         L.ref_norm_rope_row.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, P, P,
                                         ctypes.c_int, P]

@@ -34,6 +34,28 @@ void ref_decode_row(int hd, int nh, int nkv, float scale, const uint32_t *q16, c
   attn_gate_row(pregate, gate, hd, gated);
 }
 
+// The decode step of rows = n_layers * nh head rows through ref_decode_row, nthreads OpenMP threads
+// over the rows (a CPU decode of every layer's heads, for timing the reference's own path): row r is
+// layer r / nh, head r % nh of that layer; layer l's arenas start layer_words words past the previous
+// layer's (0: every layer reads the same arenas). q16 [rows][hd/2], out [rows][hd].
+void ref_decode_rows(int hd, int nh, int nkv, float scale, int n_layers, const uint32_t *q16,
+                     const uint32_t *kc, const uint32_t *vc, size_t layer_words, int nfill,
+                     const float *gate, float *out, int nthreads) {
+  const int rows = n_layers * nh, hw = hd / 2;
+#pragma omp parallel num_threads(nthreads)
+  {
+    std::vector<float> s(nfill), p(nfill), g(hd);
+    std::vector<uint16_t> p16(nfill);
+#pragma omp for schedule(dynamic, 1)
+    for (int r = 0; r < rows; ++r) {
+      const int l = r / nh, h = r % nh;
+      ref_decode_row(hd, nh, nkv, scale, q16 + (size_t)r * hw, kc + (size_t)l * layer_words,
+                     vc + (size_t)l * layer_words, h / (nh / nkv), nfill, gate + (size_t)r * hd,
+                     s.data(), p.data(), p16.data(), out + (size_t)r * hd, g.data());
+    }
+  }
+}
+
 // One row through the reference's attn_rms_norm then attn_rope (attn_vk.h:102-122), as attn_forward
 // calls them for a Q or K row (attn_vk.h:268-276), into a separate output (the alias-safe form).
 void ref_norm_rope_row(int hd, int nrot, float eps, float freq_base, const float *x, const float *w,

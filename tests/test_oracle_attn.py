@@ -52,6 +52,30 @@ def test_config1_matches_reference_mirror_bitwise():
         assert oracle.bit_diff(og[h], rg) == 0
 
 
+def test_reference_rows_driver_matches_rows():
+    """ref_decode_rows (the reference's rows under OpenMP, timed as the CPU baseline) gives, for 2
+    layers x 16 heads, the oracle's pre-gate output of each layer's rows, bit for bit."""
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    nfill = 300
+    c, _, _ = make_cache(nfill, F16, F16, seed=3)
+    c2, _, _ = make_cache(nfill, F16, F16, seed=4)
+    q = np.stack([q_gate(3)[0], q_gate(4)[0]])
+    g = np.zeros_like(q)
+    kc = np.ascontiguousarray(np.stack([c.k_data[0], c2.k_data[0]])).view(np.uint32)
+    vc = np.ascontiguousarray(np.stack([c.v_data[0], c2.v_data[0]])).view(np.uint32)
+    q16 = np.ascontiguousarray(oracle.f32_to_f16(q).view(np.uint32))
+    out = np.empty((2, 16, 256), np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    R.ref_decode_rows(256, 16, 4, ctypes.c_float(0.0625), 2, P(q16), P(kc), P(vc), kc[0].size, nfill,
+                      P(g), P(out), 4)
+    with oracle.exp_mode(1):
+        for i, cc in enumerate((c, c2)):
+            want, _ = cc.decode(0, nfill, q[i])
+            assert oracle.bit_diff(out[i], want) == 0
+
+
 def test_single_key_probability_is_one():
     c, _, v = make_cache(1, Q8_0, Q8_0, seed=5)
     q, _ = q_gate(5)
