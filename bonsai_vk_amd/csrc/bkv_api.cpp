@@ -153,8 +153,8 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
     }
   }
 #ifdef BKV_EXPERIMENT_TS
-  total = align256(total) + 131072;
-  p.ts_off = total - 131072;
+  total = align256(total) + 262144;
+  p.ts_off = total - 262144;
 #endif
   p.total = total;
   return p;

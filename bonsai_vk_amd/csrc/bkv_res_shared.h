@@ -18,8 +18,11 @@ constexpr int8_t kNoBin8 = -128;     // kNoBinade in the int8 binade map
 #ifdef BKV_EXPERIMENT_TS
 #define RTS(i) do { if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
 #define RTSW(i, wv) do { if (threadIdx.x == 64 * (wv) && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
-#define RTSV(i) do { if ((threadIdx.x & 63) == 0 && a.tsw) a.tsw[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 8 + (i)] = (unsigned)wall_clock64(); } while (0)
+#define RTSV(i) do { if ((threadIdx.x & 63) == 0 && a.tsw) a.tsw[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
+// the same slot with the shader clock (cycles, for the clock rate of a phase)
+#define RTSC(i) do { if ((threadIdx.x & 63) == 0 && a.tsw) a.tsw[(blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + (i)] = (unsigned)__builtin_readcyclecounter(); } while (0)
 #else
+#define RTSC(i) do { } while (0)
 #define RTSV(i) do { } while (0)
 #define RTSW(i, wv) do { } while (0)
 #define RTS(i) do { } while (0)
@@ -169,6 +172,7 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
   ok = ok && !__any(over) && T0 <= kWalkCap;
   const int T = ok ? T0 : 0;
   __builtin_amdgcn_wave_barrier();
+  if (tsw && lane == 0) tsw[0] = (unsigned)wall_clock64();
   // 2. the specials, resolved to global key index, increment prefix and starting binade
   for (int o = lane; o < T; o += 64) {
     int l = 0, hi = gg - 1;
@@ -184,7 +188,7 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
     w.sck[o] = bf == 255 ? w.wg_bp[l] : (bf == 0 ? kNoBinade : bf - 128);
   }
   __builtin_amdgcn_wave_barrier();
-  if (tsw && threadIdx.x == 0) *tsw = (unsigned)wall_clock64();   // (instrumented builds)
+  if (tsw && lane == 0) tsw[1] = (unsigned)wall_clock64();   // (instrumented builds: the wave's clocks)
   // 3. per special: the ulps of the segment before it in its binade
   bool bad = false;
   for (int o = lane; o < T; o += 64) {
@@ -208,6 +212,7 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
   ok = ok && !__any(bad);
   const int Tc = ok ? T : 0;
   __builtin_amdgcn_wave_barrier();
+  if (tsw && lane == 0) tsw[2] = (unsigned)wall_clock64();
   // 4. the chain, 16 steps per unrolled block; entries past Tc are du 0, e 0 (no change)
   float s = 0.0f;
   bool bad2 = false;
@@ -232,6 +237,7 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
     if (ck_l >= 0) bad2 |= (int)(pre >> 23) != ck_l || (int)((pre + (uint32_t)du_l) >> 23) != ck_l;
   }
   bool good = ok && !__any(bad2);
+  if (tsw && lane == 0) { tsw[3] = (unsigned)wall_clock64(); tsw[4] = (unsigned)T; }
   const long long k_last = Tc > 0 ? w.sk[Tc - 1] : -1, i_last = Tc > 0 ? w.si[Tc - 1] : 0;
   if (good && nfill - 1 - k_last > 0) good = advance(s, blast_last, itot - i_last);
   s_out = s;

@@ -329,29 +329,13 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     if (lane < 2 * kUPR)
       asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(tb) : "memory", "m0");
   }
-  // K first: a wave requests its V rows once its K tile and tail rows have landed, so the K
-  // stream (which the scores wait for) is not shared with the V stream (which only the PV needs)
+  // q (and x) are read by every wave: wave 0 waits for them (the K loads it issued after them may
+  // still be in flight), then the workgroup syncs once; each wave then waits for its own K rows only
+  // and scores them while the other waves' tiles are still landing
+  if (wave == 0) wait_vm_n((t0 ? kUPR : 0) + (tr > 0 ? 1 : 0));
+  __syncthreads();                             // s_q (and s_x) visible to every wave
   wait_vm<0>();
   RTSV(0);
-  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
-  uint32_t xs = 0u;                            // the tail slot's scale word
-  {
-    const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
-    const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
-                 "s"(sb) : "memory", "m0");
-  }
-  if (vt) {
-    const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
-    xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-  }
-#pragma unroll
-  for (int s = 0; s < kSwSlots; ++s) {
-    const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
-    const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
-    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-  }
-  __syncthreads();                             // s_q (and s_x) visible to every wave
 
   // ---------------------------------------------------------------- scores
   // Each lane: key 64 w + lane against the group's 4 heads (attn_vk.h:156-170). The tail keys 2 w,
@@ -397,6 +381,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       wave_lds_sync();
     };
     asm volatile("s_nop 4");
+    RTSV(5);
+    RTSC(6);
     if (t0) {
       RTS(14);
       if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
@@ -445,6 +431,28 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       }
     }
   }
+  RTSC(7);
+  // V after the scores: a wave requests its V rows once it has scored its K rows, so the K stream
+  // (which the scores wait for) is not shared with the V stream (which only the PV needs)
+  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
+  uint32_t xs = 0u;                            // the tail slot's scale word
+  {
+    const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
+    const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
+                 "s"(sb) : "memory", "m0");
+  }
+  if (vt) {
+    const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
+    xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+  }
+#pragma unroll
+  for (int s = 0; s < kSwSlots; ++s) {
+    const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
+    const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
+    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+  }
+
   RTS(1);
   RTSV(2);
   // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
@@ -716,27 +724,37 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     uint2 pn = s_ps[min(slot_key(0), KS - 1)];
     int rn = s_ridx[min(slot_key(0), KS - 1)];
     float vn = slot_scale(0);
-#pragma unroll
-    for (int s = 0; s < kSwSlots; ++s) {
+    auto pv_slot = [&](int s, const uint4 &vrow, uint2 pw, int ri, float vs) {
       const int k = slot_key(s);
       const bool live = (s < kSwSlots - 1 ? k < np : (vt && k < nk));
-      uint2 pw = pn;
-      const int ri = rn;
-      const float vs = vn;
-      if (s + 1 < kSwSlots) {
-        pn = s_ps[min(slot_key(s + 1), KS - 1)];
-        rn = s_ridx[min(slot_key(s + 1), KS - 1)];
-        vn = slot_scale(s + 1);
-      }
       pw.x = live ? pw.x : 0u;
       pw.y = live ? pw.y : 0u;
       float p[kGqa];
       p4(pw, p);
-      v_accum<BKV_Q8_0>(vd[s], live && !patched(s) ? vs : 0.0f, p, acc);
+      v_accum<BKV_Q8_0>(vrow, live && !patched(s) ? vs : 0.0f, p, acc);
       // (stored unconditionally, rows not at risk into spare rows: no branch per slot)
-      s_rrow[(live && ri >= 0 ? ri : kSwRisk + wave) * 16 + vsub] = vd[s];
+      s_rrow[(live && ri >= 0 ? ri : kSwRisk + wave) * 16 + vsub] = vrow;
+    };
+    // the pass slots that hold keys of this wave (slot s: keys 32 s + 4 w ..), then the tail slot
+    const int nsl = min(kSwSlots - 1, max(0, (np - 4 * wave + 31) / 32));
+#pragma unroll
+    for (int s = 0; s < kSwSlots - 1; ++s) {
+      if (s < nsl) {                           // (uniform)
+        const uint2 pw = pn;
+        const int ri = rn;
+        const float vs = vn;
+        if (s + 1 < kSwSlots - 1) {
+          pn = s_ps[min(slot_key(s + 1), KS - 1)];
+          rn = s_ridx[min(slot_key(s + 1), KS - 1)];
+          vn = slot_scale(s + 1);
+        }
+        pv_slot(s, vd[s], pw, ri, vs);
+      }
       asm volatile("" ::: "memory");
     }
+    if (vt && tn > 0)
+      pv_slot(kSwSlots - 1, vd[kSwSlots - 1], s_ps[min(slot_key(kSwSlots - 1), KS - 1)], s_ridx[min(slot_key(kSwSlots - 1), KS - 1)],
+              slot_scale(kSwSlots - 1));
     if (vt && (vsub & 3) == 0) s_tsw[(4 * wave + vkk) * 4 + (vsub >> 2)] = xs;
     if (wave == sp_w) {                        // the appended row, by the lanes of its slot
       uint2 pw = s_ps[kp];
@@ -760,7 +778,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       float sres;
       bool gres;
       walk_one<WS>(x, a.spec + (size_t)(g * kGqa + h) * G * kMaxSpecial, G, (int64_t)a.kpw, (int64_t)a.nfill,
-                   s_walk[h], sres, gres);
+                   s_walk[h], sres, gres,
+                   a.tsw ? a.tsw + (blockIdx.x * 8 + wave) * 16 + 8 : nullptr);
       if (lane == 0) {
         s_S[h] = sres;
         s_ok[h] = gres ? 1 : 0;

@@ -59,10 +59,10 @@ def probe(ctx=32768, paged=False, calls=6):
         ts = cache.workspace.view(torch.int32)[TS_WORD:TS_WORD + nwg * 16].cpu().numpy()
         out = (ctypes.c_uint64 * 6)()
         lib().bkv_debug_layout(ctypes.byref(cache.desc), ctx + i + 1, out)
-        o = (int(out[5]) - 131072) // 4
-        tw = cache.workspace.view(torch.int32)[o:o + nwg * 64].cpu().numpy()
+        o = (int(out[5]) - 262144) // 4
+        tw = cache.workspace.view(torch.int32)[o:o + nwg * 128].cpu().numpy()
     ts = ts.astype(np.int64).reshape(nwg, 16)
-    probe.per_wave = tw.astype(np.int64).reshape(nwg, 8, 8)[ts[:, 0] != 0]
+    probe.per_wave = tw.astype(np.int64).reshape(nwg, 8, 16)[ts[:, 0] != 0]
     if not ts[:, 8].any():
         raise RuntimeError("no timestamps written: load the instrumented build "
                            "(BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so after build --timestamps)")
@@ -88,7 +88,17 @@ def main(argv):
             for j in range(len(names)):
                 col = pw[:, wv, j]
                 cells.append(f"{(np.median(col) - t0) / 100.0:7.2f}" if col.any() else "      -")
-            print(f"    wave {wv}: " + " ".join(cells))
+            # slots 5 (wall) and 6 / 7 (shader cycles): the clock rate over the scoring phase
+            dw = (pw[:, wv, 2] - pw[:, wv, 5]).astype(np.float64)
+            dc = ((pw[:, wv, 7] - pw[:, wv, 6]) & 0xFFFFFFFF).astype(np.float64)
+            ok = dw > 0
+            ghz = f"   score clock {np.median(dc[ok] / dw[ok]) / 10.0:5.2f} GHz over {np.median(dw[ok]) / 100.0:5.2f} us" if ok.any() else ""
+            print(f"    wave {wv}: " + " ".join(cells) + ghz)
+        print("  the walk (waves 0-3, median): records scanned, specials loaded, segments checked, "
+              "chain done; specials walked")
+        for wv in range(4):
+            cells = [f"{(np.median(pw[:, wv, 8 + j]) - t0) / 100.0:7.2f}" for j in range(4)]
+            print(f"    wave {wv}: " + " ".join(cells) + f"   {int(np.median(pw[:, wv, 12]))}")
 
 
 if __name__ == "__main__":
