@@ -141,8 +141,8 @@ def gen_cache(cache, n, seed, layers):
 
 def kernel_name(cache, n):
     """The launch(es) one decode_step call makes at n keys."""
-    return {3: "stream_kernel (one launch per layer, one workgroup per CU, K and V waves: append, QK, "
-               "exact sum, PV, merge)",
+    return {3: "stream_kernel (one launch per layer, one workgroup per CU: append, QK, exact sum, PV, "
+               "merge)",
             2: "resident_kernel (one launch per layer, one workgroup per CU: append, QK, exact sum, "
                "PV, merge)",
             0: "qk_kernel + e_kernel + pv_kernel + merge_kernel (four launches per layer)"}[cache.decode_path(n)]

@@ -196,7 +196,9 @@ int bkv_error_words(const bkv_cache_desc *d, uint64_t out[1]);
  * single launch (q8_0 K and V, up to 528 keys per workgroup: the default where it applies), 2 = the
  * resident single launch (every format, up to 2048 keys per workgroup), 0 = the four-launch split
  * path (everything else); -1 = bad arguments. The environment variable BKV_DECODE = split |
- * resident | stream forces one where its plan fits (read on every call). */
+ * resident | stream forces one where its plan fits (read on every call). BKV_COOP=1 (read once)
+ * launches the stream kernel cooperatively: the runtime then refuses a grid that cannot be
+ * co-resident, at about 18 us more per call. */
 int bkv_decode_path(const bkv_cache_desc *d, uint32_t nfill);
 
 /* Workspace needed by op (enum bkv_op) for contexts up to max_ctx positions (prefill: max_ctx is
