@@ -20,6 +20,7 @@
 //     gate.
 // Barriers count arrivals on per-group counters (two sets, alternating by call parity; each call
 // clears the set the next one uses). Every wait is bounded and records an error word on timeout.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -854,19 +855,37 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   RTS(8);
 }
 
+// workgroups of one variant resident at once on the current device
+template <typename K>
+static int occupancy_of(K kernel, int dev) {
+  int per = 0;
+  hipDeviceProp_t pr;
+  if (hipGetDeviceProperties(&pr, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, kResNT, 0) != hipSuccess)
+    return 0;
+  return per * pr.multiProcessorCount;
+}
+
+// the grid the launches may use on the current device: the smallest occupancy over every variant
+// of this format pair that launch_resident can launch (register V or not, paged or not), queried
+// once per device
 template <int KF, int VF>
 static int resident_capacity() {
-  static int cap = -1;
-  if (cap < 0) {
-    int dev = 0, per = 0;
-    hipDeviceProp_t pr;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, resident_kernel<KF, VF, false, false>, kResNT, 0) != hipSuccess)
-      cap = 0;
-    else
-      cap = per * pr.multiProcessorCount;
+  constexpr int kMaxDev = 64;
+  static int cap[kMaxDev];
+  static bool done[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  if (!done[dev]) {
+    int c = std::min(occupancy_of(resident_kernel<KF, VF, false, false>, dev),
+                     occupancy_of(resident_kernel<KF, VF, false, true>, dev));
+    if constexpr (KF == BKV_Q8_0 && VF == BKV_Q8_0)
+      c = std::min({c, occupancy_of(resident_kernel<KF, VF, true, false>, dev),
+                     occupancy_of(resident_kernel<KF, VF, true, true>, dev)});
+    cap[dev] = c;
+    done[dev] = true;
   }
-  return cap;
+  return cap[dev];
 }
 
 int resident_max_workgroups(int kf, int vf) {

@@ -303,6 +303,34 @@ def test_workspace_error_flag(path):
     dev.check_workspace()
 
 
+def test_paths_switch_on_one_workspace(monkeypatch):
+    """The path a call takes follows its context on one workspace: split past 131,072 keys, the
+    stream kernel for a window of 3,000 of them, the resident kernel for 40,000, and back. Every
+    call matches the oracle: no path reads what another left in the workspace."""
+    monkeypatch.delenv("BKV_DECODE", raising=False)
+    n = 140000
+    dev, _ = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    k, v = oracle.synth_kv(n, 4, 256, 61, 0, outliers=3)
+    for s0 in range(0, n, 16384):
+        dev.append(0, s0, torch.from_numpy(k[s0:s0 + 16384]).cuda(), torch.from_numpy(v[s0:s0 + 16384]).cuda())
+    q, _ = qg(61, 0)
+    qd = torch.from_numpy(q).cuda()
+    wants = {}
+    for kstart in (0, n - 3000, n - 40000):                 # the oracle of each window: its keys alone
+        _, host = pair(1, n - kstart, BKV_Q8_0, BKV_Q8_0)
+        host.append(0, 0, k[kstart:], v[kstart:])
+        wants[kstart] = host.decode(0, n - kstart, q, nthreads=16)[0]
+        del host
+    for kstart, want_path in [(0, 0), (n - 3000, 3), (n - 40000, 2), (0, 0), (n - 3000, 3), (n - 40000, 2),
+                              (n - 3000, 3)]:
+        say(f"window [{kstart}, {n}) path {want_path}")
+        assert dev.decode_path(n - kstart) == want_path
+        out, _ = dev.decode_window(0, kstart, n, qd)
+        torch.cuda.synchronize()
+        assert report(f"window [{kstart}, {n})", out.cpu().numpy(), wants[kstart]) <= TOL
+    dev.check_workspace()
+
+
 def test_consecutive_decode_steps(path):
     """BASELINE config 3's pattern at a smaller context: consecutive decode_steps on one workspace
     (each call appends one token and attends over all of them), every step checked against the
