@@ -24,6 +24,7 @@
 // softmax sum and PV), hence a tolerance rather than bit-exact parity for prefill.
 
 #include "bkv_device.h"
+#include "bkv_exp.h"
 #include "bkv_internal.h"
 
 namespace bkv {
@@ -547,6 +548,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 
   __shared__ float s_red[4][kPxRows];
   __shared__ float s_m[kPxRows], s_sum[kPxRows];
+  __shared__ double s_t2[32];               // the exp table
   constexpr int ES = kPxRows + 1;          // LDS row stride (floats) of the exp tile
   constexpr int NT = kPxRows / 16;         // MFMA row tiles
   constexpr int PR = kPxRows / 4;          // probabilities per thread per 64-key tile
@@ -560,6 +562,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   // ---------------------------------------------------------------- sweep 1: exact scores
   // the rows' q16 in LDS: s_q[r][d], row r = query q0 + r/4 (clamped into the chunk), head 4g + r%4
   float *s_q = reinterpret_cast<float *>(s_big);
+  if (tid < 32) s_t2[tid] = kExp2Tab[tid];
   {
     const int qlast = a.q_base + a.n_q - 1;
     for (int i = tid; i < kPxRows * kHd / 4; i += 256) {
@@ -693,10 +696,10 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
       const float4 v = vc[r4];
       float4 e;
-      e.x = exp_cr(v.x - s_m[4 * r4]);
-      e.y = exp_cr(v.y - s_m[4 * r4 + 1]);
-      e.z = exp_cr(v.z - s_m[4 * r4 + 2]);
-      e.w = exp_cr(v.w - s_m[4 * r4 + 3]);
+      e.x = exp_cr_t(v.x - s_m[4 * r4], s_t2);
+      e.y = exp_cr_t(v.y - s_m[4 * r4 + 1], s_t2);
+      e.z = exp_cr_t(v.z - s_m[4 * r4 + 2], s_t2);
+      e.w = exp_cr_t(v.w - s_m[4 * r4 + 3], s_t2);
       *reinterpret_cast<float4 *>(src + 4 * r4) = e;
       eb[4 * r4] = e.x;
       eb[4 * r4 + 1] = e.y;
@@ -704,13 +707,13 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       eb[4 * r4 + 3] = e.w;
     }
     __syncthreads();
-    if (tid < kPxRows) {
-      const float *col = et + (t & 1) * 256 * ES + tid;
+    if (lane < kPxRows / 4) {                  // wave w adds rows 4 w .. 4 w + 3, one lane each
+      const float *col = et + (t & 1) * 256 * ES + 4 * w + lane;
 #pragma unroll 16
       for (int k = 0; k < kPxTile; ++k) sum = sum + col[k * ES];
     }
   }
-  if (tid < kPxRows) s_sum[tid] = (tid >> 2) < nqv ? sum : 1.0f;
+  if (lane < kPxRows / 4) s_sum[4 * w + lane] = (w < nqv) ? sum : 1.0f;   // row 4 w + l: query w
   __syncthreads();
 
   PXTS(2);

@@ -31,8 +31,10 @@ PHASES = [(0, "start"), (1, "scores done (wave 0)"), (2, "barrier A passed"), (1
 TS_WORD = 131072 // 4
 
 
-def probe(ctx=32768, paged=False, calls=6):
-    """Timestamps [workgroups][16] (raw 100 MHz clocks) of the last of `calls` decode_steps."""
+def probe(ctx=32768, paged=False, calls=6, b2b=False):
+    """Timestamps [workgroups][16] (raw 100 MHz clocks) of the last of `calls` decode_steps; b2b:
+    the calls run back to back as in the bench (one synchronisation at the end), otherwise each
+    call starts on an idle GPU."""
     if paged:
         npg = (ctx + calls + 255) // 256
         bt = np.random.default_rng(3).permutation(npg).astype(np.int32)[None]
@@ -55,6 +57,8 @@ def probe(ctx=32768, paged=False, calls=6):
     from bonsai_vk_amd._lib import lib
     for i in range(calls):
         cache.decode_step(0, ctx + i, k, v, q)
+        if b2b and i < calls - 1:
+            continue
         torch.cuda.synchronize()
         ts = cache.workspace.view(torch.int32)[TS_WORD:TS_WORD + nwg * 16].cpu().numpy()
         out = (ctypes.c_uint64 * 6)()
@@ -71,10 +75,10 @@ def probe(ctx=32768, paged=False, calls=6):
 
 def main(argv):
     ctx = int(next((a for a in argv if not a.startswith("-")), 32768))
-    ts = probe(ctx, "--paged" in argv)
+    ts = probe(ctx, "--paged" in argv, b2b="--b2b" in argv)
     phases = PHASES if os.environ.get("BKV_DECODE") == "resident" else PHASES_STREAM
     t0 = ts[:, 0].min()
-    print(f"ctx {ctx}{' paged' if '--paged' in argv else ''}: phase clocks in us from the first "
+    print(f"ctx {ctx}{' paged' if '--paged' in argv else ''}{' back to back' if '--b2b' in argv else ''}: phase clocks in us from the first "
           f"workgroup's start, min / median / max over {len(ts)} workgroups")
     for slot, name in phases:
         col = (ts[:, slot] - t0) / 100.0

@@ -1,4 +1,4 @@
-"""The decode kernel's table-driven exp (exp_cr_t in bonsai_vk_amd/csrc/bkv_stream.hip) restated in C
+"""The decode kernel's table-driven exp (exp_cr_t in bonsai_vk_amd/csrc/bkv_exp.h) restated in C
 with the same fp64 steps, and checked against the correctly rounded value (float)exp((double)x) that
 the oracle's e_j uses: every float of [-104, 89] in the full run (BKV_EXP_FULL=1, about a minute on 8
 cores), every 97th float by default. The arithmetic: x = (k/32) ln2 + r, exp(r) by a degree-5 Taylor
