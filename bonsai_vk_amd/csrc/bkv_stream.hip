@@ -107,6 +107,22 @@ __device__ __forceinline__ void classify_i(float abefore, float aafter, float e,
   inc = ok ? (int)r : 0;
 }
 
+// inner[h] = sum of q16[h][32 b + i] * x[i], i ascending (one fma per product: every product is
+// exact), for the block b of the lane's 16-lane row; q16[h][32 b + 16 c + j] sits in lane j of
+// the row, register q[h][c], and reaches the other lanes by row_newbcast
+template <int I>
+struct BlockChain {
+  static __device__ __forceinline__ void run(float (&inner)[kGqa], const float (&q)[kGqa][2], const float (&x)[32]) {
+    BlockChain<I - 1>::run(inner, q, x);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) fmac_bc<(I - 1) % 16>(inner[h], q[h][(I - 1) / 16], x[I - 1]);
+  }
+};
+template <>
+struct BlockChain<0> {
+  static __device__ __forceinline__ void run(float (&)[kGqa], const float (&)[kGqa][2], const float (&)[32]) {}
+};
+
 // s_waitcnt vmcnt(n) for a runtime n (a branch per value; an n the compiler knows folds away)
 __device__ __forceinline__ void wait_vm_n(int n) {
   switch (n) {
@@ -302,9 +318,10 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) { mloc[h] = -INFINITY; sc[h] = 0.0f; }
   const int kl = 64 * wave + lane;             // this lane's pass key
+  const bool bsplit = np <= 2 * 64 && tn == 0; // short workgroups: all 8 waves score
   {
     float qv[kGqa][kHd / 16];
-    {
+    if (!bsplit) {
       const float *qf = reinterpret_cast<const float *>(s_q) + (lane & 15);
 #pragma unroll
       for (int h = 0; h < kGqa; ++h)
@@ -339,7 +356,63 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     asm volatile("s_nop 4");
     RTSV(5);
     RTSC(6);
-    if (t0) {
+    if (bsplit) {
+      // at most 2 x 64 keys: every wave scores blocks of keys instead of whole keys. Wave w, row r
+      // of 16 lanes: block b = 4 (w & 1) + r of keys 64 p + 16 (w >> 1) + (lane & 15); each block's
+      // term f16(scale) * inner goes to LDS, and waves 0-1 add a key's 8 terms in block order (the
+      // same arithmetic as the lane-per-key chain)
+      RTS(14);
+      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
+      __syncthreads();                         // both tiles (and the patched row) are in LDS
+      const int i16 = lane & 15, b = 4 * (wave & 1) + (lane >> 4);
+      float qb[kGqa][2];
+      {
+        const float *qf = reinterpret_cast<const float *>(s_q) + 32 * b + i16;
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          qb[h][0] = round_f16(qf[h * kHd]);
+          qb[h][1] = round_f16(qf[h * kHd + 16]);
+        }
+      }
+      float4 *s_terms = reinterpret_cast<float4 *>(kt + 2 * 64 * kUPR);   // [key][block] x 4 heads
+#pragma unroll 1
+      for (int p = 0; p < 2; ++p) {
+        const int k0 = 64 * p + 16 * (wave >> 1);
+        if (k0 >= np) break;                   // (uniform)
+        const int key = min(k0 + i16, np - 1);
+        const uint4 *row = kt + key * kUPR;
+        const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
+        const uint32_t sw = reinterpret_cast<const uint32_t *>(&row[16])[b >> 1];
+        const float dsc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+        const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float x[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = sbyte(u[i >> 2], i & 3);
+        float inner[kGqa] = {0.f, 0.f, 0.f, 0.f};
+        BlockChain<32>::run(inner, qb, x);
+        if (k0 + i16 < np)
+          s_terms[key * 8 + b] = make_float4(__fmul_rn(dsc, inner[0]), __fmul_rn(dsc, inner[1]),
+                                             __fmul_rn(dsc, inner[2]), __fmul_rn(dsc, inner[3]));
+      }
+      __syncthreads();
+      if (kl < np) {
+        float acc1[kGqa] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int bb = 0; bb < 8; ++bb) {
+          const float4 t = s_terms[kl * 8 + bb];
+          acc1[0] = __fadd_rn(acc1[0], t.x);
+          acc1[1] = __fadd_rn(acc1[1], t.y);
+          acc1[2] = __fadd_rn(acc1[2], t.z);
+          acc1[3] = __fadd_rn(acc1[3], t.w);
+        }
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          sc[h] = acc1[h];
+          mloc[h] = fmaxf(mloc[h], acc1[h] * a.scale);
+        }
+      }
+      RTSV(1);
+    } else if (t0) {
       RTS(14);
       if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
       float acc1[kGqa];
