@@ -37,9 +37,10 @@ constexpr int kSwKeys = kSwNP + kResTail;
 constexpr int kSwTailLoads = (kResTail * kUPR + 63) / 64;   // direct-to-LDS loads of the tail rows
 constexpr int kSwBlocks = kSwNP / 64 + 1;                  // e-pass blocks: 8 of 64 keys, the tail
 constexpr int kSwRisk = 128;             // at-risk V rows the LDS keeps (more: re-read from the cache)
-// relative distance from S_a inside which the exact sum is expected (it changes ~2e-6 relative on
-// these shapes); a key is at risk when p16' would round differently anywhere inside it
-constexpr float kSwRiskBand = 0x1p-17f;
+// relative distance from S_a inside which the exact sum is expected: the serial fp32 sum departs
+// from the exact one by up to ~7e-6 relative at 32K keys (2e-6 median), and S_a adds its own ~1e-6;
+// a key is at risk when p16' would round differently anywhere within twice this distance of it
+constexpr float kSwRiskBand = 0x1p-16f;
 
 // rows [0, n) of the tail (keys k0 ..) into tt (kUPR uint4 per row), lanes past the rows masked
 template <bool PG>
@@ -189,6 +190,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ double s_bu[kSwBlocks * kGqa]; // block totals of the increments (units of 2^-40)
   __shared__ int s_bc[kSwBlocks * kGqa];    // block counts of specials
   __shared__ int s_nrisk;
+  __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
@@ -262,9 +264,11 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   WS *s_walk = reinterpret_cast<WS *>(xb + 24576 + kGqa * kMaxSpecial * sizeof(Special));
   uint4 *s_rrow = reinterpret_cast<uint4 *>(xb + 53248);              // [kSwRisk + 8][16] at-risk V rows
   float *s_red = reinterpret_cast<float *>(xb + 53248 + (kSwRisk + 8) * 256);  // [wave][head][EPL][LPR]
+  int16_t *s_rl = reinterpret_cast<int16_t *>(xb + 53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4);  // [K wave][KS]
   static_assert(kGqa * KS * 4 + 2 * KS * 8 + kGqa * KS + 2 * KS <= 24576, "e, p16', p16, binade map, risk index");
   static_assert(24576 + kGqa * kMaxSpecial * sizeof(Special) + kGqa * sizeof(WS) <= 53248, "specials, walk scratch");
-  static_assert(53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4 <= sizeof(kt), "at-risk rows, PV reduction");
+  static_assert(53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4 + kSwKW * KS * 2 <= sizeof(kt),
+                "at-risk rows, PV reduction, at-risk key lists");
   const int th = lane >> 4, tt = lane & 15;   // tail e pass: lane 16 h + t takes tail key t, head h
   const int vsub = lane & 15, vkk = lane >> 4;
 
@@ -661,6 +665,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       const _Float16 a = (_Float16)(p * (1.0f - 2.0f * kSwRiskBand)), b = (_Float16)(p * (1.0f + 2.0f * kSwRiskBand));
       return __builtin_bit_cast(uint16_t, a) != __builtin_bit_cast(uint16_t, b);
     };
+    bool rk = false;
     if (valid) {
       _Float16 pk[kGqa];
       bool r = false;
@@ -673,6 +678,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       s_ps[kl] = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, pk[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[1]) << 16),
                             (uint32_t)__builtin_bit_cast(uint16_t, pk[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, pk[3]) << 16));
       int ri = -1;
+      rk = r;
       if (r) {
         ri = atomicAdd(&s_nrisk, 1);
         if (ri >= kSwRisk) ri = -1;
@@ -682,6 +688,11 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       s_ridx[kl] = -1;
     }
     if (wave == 1 && lane < kResTail) s_ridx[NP + lane] = -1;
+    {
+      const unsigned long long rbw = __ballot(rk);
+      if (lane == 0) s_rb[wave] = rbw;
+      if (wave == 0 && lane == 1 && tn == 0) s_rb[kSwBlocks - 1] = 0ull;
+    }
     __syncthreads();
     if (tl) {                                  // the tail: one head per lane
       const float p = evt * pick4(rSa, th);
@@ -692,6 +703,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         const int ri = atomicAdd(&s_nrisk, 1);
         s_ridx[NP + tt] = (int16_t)(ri < kSwRisk ? ri : -1);
       }
+      const unsigned long long rbt = __ballot(th == 0 && tt < tn && r);
+      if (lane == 0) s_rb[kSwBlocks - 1] = rbt;
     }
   }
   wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
@@ -766,6 +779,26 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     };
     // the pass slots that hold keys of this wave (slot s: keys 32 s + 4 w ..), then the tail slot
     const int nsl = min(kSwSlots - 1, max(0, (np - 4 * wave + 31) / 32));
+    auto scale_bits = [&](int s) -> uint32_t { return vsc16[(4 * s + vkk) * 8 + (vsub >> 1)]; };
+    if (nsl == kSwSlots - 1) {
+      // every pass slot holds keys: straight-line code, each slot's LDS operands requested at the
+      // start of the slot before and waited for at the start of the next
+      uint32_t vr = scale_bits(0);
+#pragma unroll
+      for (int s = 0; s < kSwSlots - 1; ++s) {
+        const uint2 pw = pn;
+        const int ri = rn;
+        const uint32_t vsr = vr;
+        if (s + 1 < kSwSlots - 1) {
+          pn = s_ps[min(slot_key(s + 1), KS - 1)];
+          rn = s_ridx[min(slot_key(s + 1), KS - 1)];
+          vr = scale_bits(s + 1);
+        }
+        asm volatile("" ::: "memory");
+        pv_slot(s, vd[s], pw, ri, f16_to_f32(vsr));
+        asm volatile("" ::: "memory");
+      }
+    } else
 #pragma unroll
     for (int s = 0; s < kSwSlots - 1; ++s) {
       if (s < nsl) {                           // (uniform)
@@ -777,6 +810,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
           rn = s_ridx[min(slot_key(s + 1), KS - 1)];
           vn = slot_scale(s + 1);
         }
+        asm volatile("" ::: "memory");
         pv_slot(s, vd[s], pw, ri, vs);
       }
       asm volatile("" ::: "memory");
@@ -854,57 +888,116 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       a.sum[g * kGqa + h] = S;
       a.status[g * kGqa + h] = s_ok[h] ? 0u : 1u;
     }
-    // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296) of head h
-    _Float16 *p16h = reinterpret_cast<_Float16 *>(s_p16);
-    for (int i = lane; i < KS; i += 64) {
-      const bool live = i < np || (i >= NP && i < NP + tn);
-      p16h[i * kGqa + h] = (_Float16)(live ? s_e[h * KS + i] / S : 0.0f);
-    }
-    kwave_sync(&s_kctr, kc += kSwKW);
-    RTS(12);
-    // (p16 - p16') * v for the keys whose rounding the exact sum changed: K wave w checks keys
-    // 64 (w + 4 i) + lane and takes its changed ones in order, 4 at a time (row group vkk takes one):
-    // the at-risk row from LDS, the appended row from s_x, or (a changed key not at risk) the cache
-#pragma unroll 1
-    for (int i = 0; i < 3; ++i) {
-      const int k0 = 64 * (wave + 4 * i), k = k0 + lane;
-      const bool live = k < np || (k >= NP && k < NP + tn);
-      const int kk = min(k, KS - 1);
-      const uint2 pw = s_p16[kk], qw = s_ps[kk];
-      unsigned long long m = __ballot(live && (pw.x != qw.x || pw.y != qw.y));
-      while (m) {
-        int kq[4];
+    // (p16 - p16') * v for up to 4 keys whose rounding the exact sum changed (row group vkk takes
+    // kq[vkk]; -1: none): the at-risk row from LDS, the appended row from s_x, or (a changed key not
+    // at risk) the cache
+    auto correct4 = [&](const int (&kq)[4]) {
+      const int kc4 = kq[vkk];
+      uint4 d = make_uint4(0u, 0u, 0u, 0u);
+      float vs = 0.0f, p[kGqa] = {0.f, 0.f, 0.f, 0.f};
+      if (kc4 >= 0) {
+        float q[kGqa];
+        p4(s_p16[kc4], p);
+        p4(s_ps[kc4], q);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          kq[j] = __builtin_amdgcn_readfirstlane(m ? k0 + (int)__builtin_ctzll(m) : -1);
-          m &= m - 1;
-        }
-        const int kc4 = kq[vkk];
-        uint4 d = make_uint4(0u, 0u, 0u, 0u);
-        float vs = 0.0f, p[kGqa] = {0.f, 0.f, 0.f, 0.f};
-        if (kc4 >= 0) {
-          float q[kGqa];
-          p4(s_p16[kc4], p);
-          p4(s_ps[kc4], q);
-#pragma unroll
-          for (int hh = 0; hh < kGqa; ++hh) p[hh] -= q[hh];
-          if (kc4 == kp) {
-            d = pd;
-            vs = pscale;
+        for (int hh = 0; hh < kGqa; ++hh) p[hh] -= q[hh];
+        if (kc4 == kp) {
+          d = pd;
+          vs = pscale;
+        } else {
+          const int ri = s_ridx[kc4];
+          const uint32_t sw = kc4 < NP ? reinterpret_cast<const uint32_t *>(vsc + ((kc4 % 32) / 4) * 64 + 4 * (kc4 / 32) + kc4 % 4)[vsub >> 2]
+                                       : s_tsw[(kc4 - NP) * 4 + (vsub >> 2)];
+          vs = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+          if (ri >= 0) {
+            d = s_rrow[ri * 16 + vsub];
           } else {
-            const int ri = s_ridx[kc4];
-            const uint32_t sw = kc4 < NP ? reinterpret_cast<const uint32_t *>(vsc + ((kc4 % 32) / 4) * 64 + 4 * (kc4 / 32) + kc4 % 4)[vsub >> 2]
-                                         : s_tsw[(kc4 - NP) * 4 + (vsub >> 2)];
-            vs = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-            if (ri >= 0) {
-              d = s_rrow[ri * 16 + vsub];
-            } else {
-              const int64_t sl = slot_k<PG>(sm, kc4);
-              d = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-            }
+            const int64_t sl = slot_k<PG>(sm, kc4);
+            d = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
           }
         }
-        v_accum<BKV_Q8_0>(d, vs, p, acc);
+      }
+      v_accum<BKV_Q8_0>(d, vs, p, acc);
+    };
+    // When every head's exact sum lies within kSwRiskBand of S_a (relative), a key whose p16' rounds
+    // the same anywhere within 2 kSwRiskBand of it (not at risk) has p16 = p16' (the fp32 roundings
+    // of e / sum and e * (1 / S_a) move the quotient by a few 2^-24 at most), so only the at-risk keys
+    // need the exact p16. Otherwise every key's p16 is formed and compared.
+    bool fast = true;
+#pragma unroll
+    for (int hh = 0; hh < kGqa; ++hh)
+      fast = fast && s_ok[hh] && fabsf(s_S[hh] - s_Sa[hh]) <= kSwRiskBand * fminf(s_S[hh], s_Sa[hh]);
+    if (fast) {
+      // the at-risk keys in key order (each K wave lists them all); then 16 keys per step, lane
+      // 16 h + i: key i of the step, head h; K wave w takes steps w, w + 4, ..., so the corrections
+      // of every key are added by one fixed wave in key order
+      int16_t *lst = s_rl + wave * KS;
+      unsigned long long rbw[kSwBlocks];
+#pragma unroll
+      for (int wd = 0; wd < kSwBlocks; ++wd) rbw[wd] = s_rb[wd];
+      int n = 0;
+#pragma unroll
+      for (int wd = 0; wd < kSwBlocks; ++wd) {
+        const unsigned long long b = rbw[wd];
+        const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
+        if ((b >> lane) & 1ull) lst[pos] = (int16_t)(wd < kSwBlocks - 1 ? 64 * wd + lane : NP + lane);
+        n += __popcll(b);
+      }
+      wave_lds_sync();
+      RTS(12);
+      const int hh = lane >> 4;
+      const float Sh = s_S[hh];
+      _Float16 *p16h = reinterpret_cast<_Float16 *>(s_p16);
+      const _Float16 *psh = reinterpret_cast<const _Float16 *>(s_ps);
+      for (int j0 = 16 * wave; j0 < n; j0 += 16 * kSwKW) {
+        const int e = j0 + (lane & 15);
+        const int k = e < n ? (int)lst[e] : -1;
+        bool ch = false;
+        if (k >= 0) {
+          // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296)
+          const _Float16 x = (_Float16)(s_e[hh * KS + k] / Sh);
+          p16h[k * kGqa + hh] = x;
+          ch = __builtin_bit_cast(uint16_t, x) != __builtin_bit_cast(uint16_t, psh[k * kGqa + hh]);
+        }
+        const unsigned long long cm = __ballot(ch);
+        unsigned m = (unsigned)((cm | (cm >> 16) | (cm >> 32) | (cm >> 48)) & 0xFFFFull);
+        wave_lds_sync();
+        while (m) {
+          int kq[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            kq[j] = m ? __builtin_amdgcn_readlane(k, (int)__builtin_ctz(m)) : -1;
+            m &= m - 1;
+          }
+          correct4(kq);
+        }
+      }
+    } else {
+      // p16 = f16_rne(e / sum) (attn_vk.h:188 and the fp16 operand cast, :295-296) of head h
+      _Float16 *p16h = reinterpret_cast<_Float16 *>(s_p16);
+      for (int i = lane; i < KS; i += 64) {
+        const bool live = i < np || (i >= NP && i < NP + tn);
+        p16h[i * kGqa + h] = (_Float16)(live ? s_e[h * KS + i] / S : 0.0f);
+      }
+      kwave_sync(&s_kctr, kc += kSwKW);
+      RTS(12);
+      // K wave w checks keys 64 (w + 4 i) + lane and takes its changed ones in order, 4 at a time
+#pragma unroll 1
+      for (int i = 0; i < 3; ++i) {
+        const int k0 = 64 * (wave + 4 * i), k = k0 + lane;
+        const bool live = k < np || (k >= NP && k < NP + tn);
+        const int kk = min(k, KS - 1);
+        const uint2 pw = s_p16[kk], qw = s_ps[kk];
+        unsigned long long m = __ballot(live && (pw.x != qw.x || pw.y != qw.y));
+        while (m) {
+          int kq[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            kq[j] = __builtin_amdgcn_readfirstlane(m ? k0 + (int)__builtin_ctzll(m) : -1);
+            m &= m - 1;
+          }
+          correct4(kq);
+        }
       }
     }
     RTS(15);
