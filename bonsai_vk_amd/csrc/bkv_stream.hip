@@ -231,6 +231,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
   if (tid == 0) { s_kctr = 0u; s_nrisk = 0; }
+  if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
     s_bc[(kSwBlocks - 1) * kGqa + tid] = 0;
@@ -413,6 +414,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         for (int h = 0; h < kGqa; ++h) {
           sc[h] = acc1[h];
           mloc[h] = fmaxf(mloc[h], acc1[h] * a.scale);
+          s_e[h * KS + kl] = acc1[h];          // for the e pass, which reads them by (key, head)
         }
       }
       RTSV(1);
@@ -543,6 +545,67 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   float Mh[kGqa], rSa[kGqa], P0f[kGqa], ev[kGqa], fin[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) { Mh[h] = s_M[h]; rSa[h] = 1.0f / s_Sa[h]; P0f[h] = (float)s_P0[h]; }
+  // p16' = f16(e * (1/S_a)) (a speculative value: any rounding of it serves, the corrections
+  // subtract exactly what the PV added); at risk: p16' would round differently somewhere within
+  // 2 kSwRiskBand of it
+  auto risky = [](float p) {
+    const _Float16 a = (_Float16)(p * (1.0f - 2.0f * kSwRiskBand)), b = (_Float16)(p * (1.0f + 2.0f * kSwRiskBand));
+    return __builtin_bit_cast(uint16_t, a) != __builtin_bit_cast(uint16_t, b);
+  };
+  if (bsplit) {
+    // At most 128 keys: the e pass on all eight waves with the tail's mapping, lane 16 h + i: key
+    // 16 w + i, head h. Block w = keys 16 w .. 16 w + 15, positions by row scans; the score of
+    // (key, head) sits in s_e, where the block-split scores left it, and e replaces it.
+    const int hh = lane >> 4, i16 = lane & 15, kk = 16 * wave + i16;
+    const bool sv = kk < np;
+    for (int i = tid; i < KS; i += NT) s_ridx[i] = -1;
+    const float evs = sv ? exp_cr_t(s_e[hh * KS + kk] * a.scale - pick4(Mh, hh), s_t2) : 0.0f;
+    const float fins = row_incl_scan_dpp(evs);
+    if (sv) s_e[hh * KS + kk] = evs;
+    if (i16 == 15) reinterpret_cast<float *>(&s_bt[wave])[hh] = fins;
+    if (a.keep_e && sv) a.e[(size_t)(g * kGqa + hh) * a.ld + kb + kk] = evs;
+    __syncthreads();
+    float fb = 0.0f;
+    for (int b = 0; b < wave; ++b) fb += reinterpret_cast<const float *>(&s_bt[b])[hh];
+    const float ab = pick4(P0f, hh) + (fb + (fins - evs));
+    int bin, inc;
+    bool sps;
+    classify_i(ab, ab + evs, evs, sps, bin, inc);
+    sps = sps && sv;
+    const double dincs = (sv && !sps) ? ldexp((double)inc, bin + 17) : 0.0;
+    if (sv) s_bin[hh * KS + kk] = sps ? kNoBin8 : (int8_t)bin;
+    const unsigned rowms = (unsigned)(__ballot(sps) >> (16 * hh)) & 0xFFFFu;
+    const double dins = row_incl_scan_dpp(dincs);
+    if (i16 == 15) {
+      s_bu[wave * kGqa + hh] = dins;
+      s_bc[wave * kGqa + hh] = __popc(rowms);
+    }
+    __syncthreads();                           // block totals, the binade map
+    if (sps) {
+      int cb = 0;
+      double ib = 0.0;
+      for (int b = 0; b < wave; ++b) { cb += s_bc[b * kGqa + hh]; ib += s_bu[b * kGqa + hh]; }
+      const int id = cb + __popc(rowms & ((1u << i16) - 1u));
+      if (id < kMaxSpecial) {
+        const int8_t bp8 = kk > 0 ? s_bin[hh * KS + kk - 1] : (int8_t)0;
+        const int bprev = kk > 0 ? (bp8 == kNoBin8 ? kNoBinade : bp8) : 127;
+        Special x;
+        x.ipre = (long long)(ib + (dins - dincs));
+        x.e = evs;
+        x.meta = kk | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+        s_spec[hh * kMaxSpecial + id] = x;
+      }
+    }
+    const float p = evs * pick4(rSa, hh);
+    if (sv) reinterpret_cast<_Float16 *>(s_ps + kk)[hh] = (_Float16)p;
+    const unsigned long long rm = __ballot(sv && risky(p));
+    const bool r = ((rm >> i16) | (rm >> (i16 + 16)) | (rm >> (i16 + 32)) | (rm >> (i16 + 48))) & 1ull;
+    if (hh == 0 && sv && r) {
+      const int ri = atomicAdd(&s_nrisk, 1);
+      s_ridx[kk] = (int16_t)(ri < kSwRisk ? ri : -1);
+      atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
+    }
+  } else {
   const bool valid = kl < np;
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
@@ -658,13 +721,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
   }
   {
-    // p16' = f16(e * (1/S_a)) (a speculative value: any rounding of it serves, the corrections
-    // subtract exactly what the PV added); at risk: p16' would round differently somewhere within
-    // kSwRiskBand of it
-    auto risky = [](float p) {
-      const _Float16 a = (_Float16)(p * (1.0f - 2.0f * kSwRiskBand)), b = (_Float16)(p * (1.0f + 2.0f * kSwRiskBand));
-      return __builtin_bit_cast(uint16_t, a) != __builtin_bit_cast(uint16_t, b);
-    };
     bool rk = false;
     if (valid) {
       _Float16 pk[kGqa];
@@ -706,6 +762,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       const unsigned long long rbt = __ballot(th == 0 && tt < tn && r);
       if (lane == 0) s_rb[kSwBlocks - 1] = rbt;
     }
+  }
   }
   wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
