@@ -192,7 +192,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ int s_nrisk;
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
-  __shared__ unsigned s_vdone;              // block-split plans: waves 4-7 done with the PV
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
   // of one key range share an XCD (each 64 B scale line holds all groups' scales of a slot)
@@ -231,7 +230,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2, 0ull);
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
-  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; s_vdone = 0u; }
+  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; }
   if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
@@ -478,32 +477,15 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
                  "s"(sb) : "memory", "m0");
   }
-  int nvr = 0;                                 // loads issued after the scale rows (their wait below)
   if (vt) {
     const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
     xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-    ++nvr;
   }
-  if (bsplit) {
-    // at most 128 keys: waves 4-7 hold the V rows of every key (slot j < 4: their own slot j; slot
-    // j = 4..7: slot j - 4 of wave w - 4) and run the whole PV while waves 0-3 walk
-    if (!kwave) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int k = 32 * (j & 3) + 4 * (j < 4 ? wave : wave - 4) + vkk;
-        const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
-        vd[j] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-      }
-      nvr += 8;
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < kSwSlots; ++s) {
-      const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
-      const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
-      vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-    }
-    nvr += kSwSlots;
+  for (int s = 0; s < kSwSlots; ++s) {
+    const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
+    const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
+    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
   }
 
   RTS(1);
@@ -782,7 +764,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
   }
   }
-  wait_vm_n(nvr);                              // this wave's V scale rows are in LDS (for every wave)
+  wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
   RTS(3);
 
@@ -835,36 +817,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   const uint4 pd = s_x[vsub];
   const uint32_t pws = reinterpret_cast<const uint32_t *>(&s_x[16])[vsub >> 2];
   const float pscale = f16_to_f32(((vsub >> 1) & 1) ? (pws >> 16) : (pws & 0xFFFFu));
-  if (bsplit) {
-    if (!kwave) {
-      // waves 4-7: slot j of wave w holds keys 32 (j & 3) + 4 src + vkk, src = w (j < 4) or w - 4
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int src = j < 4 ? wave : wave - 4, s = j & 3, k0 = 32 * s + 4 * src, k = k0 + vkk;
-        if (k0 < np) {                         // (uniform)
-          const bool live = k < np;
-          uint2 pw = s_ps[min(k, KS - 1)];
-          pw.x = live ? pw.x : 0u;
-          pw.y = live ? pw.y : 0u;
-          const int ri = s_ridx[min(k, KS - 1)];
-          const float vs = f16_to_f32(reinterpret_cast<const uint16_t *>(vsc + src * 64)[(4 * s + vkk) * 8 + (vsub >> 1)]);
-          float p[kGqa];
-          p4(pw, p);
-          v_accum<BKV_Q8_0>(vd[j], live && k != kp ? vs : 0.0f, p, acc);
-          s_rrow[(live && ri >= 0 ? ri : kSwRisk + wave) * 16 + vsub] = vd[j];
-        }
-      }
-      // the appended row, by the row group of its slot on the wave that ran that slot
-      if (kp >= 0 && (sp_w < 4 ? sp_w + 4 : sp_w) == wave) {
-        uint2 pw = s_ps[kp];
-        if (vkk != sp_kk) pw = make_uint2(0u, 0u);
-        float p[kGqa];
-        p4(pw, p);
-        v_accum<BKV_Q8_0>(pd, vkk == sp_kk ? pscale : 0.0f, p, acc);
-      }
-      lds_arrive(&s_vdone);                    // the at-risk rows are in LDS
-    }
-  } else
   {
     // each slot's LDS operands are read one slot ahead, and no further (held back by the compiler
     // barrier at the end of a slot, they would all be read up front into registers)
@@ -1028,7 +980,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     // the same anywhere within 2 kSwRiskBand of it (not at risk) has p16 = p16' (the fp32 roundings
     // of e / sum and e * (1 / S_a) move the quotient by a few 2^-24 at most), so only the at-risk keys
     // need the exact p16. Otherwise every key's p16 is formed and compared.
-    if (bsplit) lds_wait(&s_vdone, kResNW - kSwKW);   // waves 4-7 have stored the at-risk rows
     bool fast = true;
 #pragma unroll
     for (int hh = 0; hh < kGqa; ++hh)
