@@ -23,6 +23,7 @@
 //     p16 = f16(e / sum) and add (p16 - p16') * v for the keys whose rounding changed.
 //  5. The workgroup's [4][256] partial goes out as tagged words, and workgroup i sums slice i of
 //     the group's partials in workgroup order (+ gate).
+#include <algorithm>
 #include <cstdlib>
 
 #include "bkv_exp.h"
@@ -165,7 +166,9 @@ __device__ __forceinline__ float wave_max64(float v) { return rd_lane(wave_max_l
 __device__ __forceinline__ float wave_sum64(float v) { return rd_lane(wave_sum_l63(v), 63); }
 __device__ __forceinline__ int wave_sum64_i(int v) { return __builtin_amdgcn_readlane(wave_scan_i32(v), 63); }
 
-template <bool PG>
+// SHORT: a plan of at most 128 keys per workgroup (every workgroup then has no tail keys); its own
+// instantiation, so that the block-split scores and e pass leave the full-pass code as it is
+template <bool PG, bool SHORT>
 __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   constexpr int NT = kResNT, NW = kResNW, NP = kSwNP, KS = kSwKeys;
   using WS = WalkScratchT<kResMaxGroupWgs, 192>;
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) { mloc[h] = -INFINITY; sc[h] = 0.0f; }
   const int kl = 64 * wave + lane;             // this lane's pass key
-  const bool bsplit = np <= 2 * 64 && tn == 0; // short workgroups: all 8 waves score
+  constexpr bool bsplit = SHORT;               // short workgroups: all 8 waves score and run the e pass
   {
     float qv[kGqa][kHd / 16];
     if (!bsplit) {
@@ -552,60 +555,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     const _Float16 a = (_Float16)(p * (1.0f - 2.0f * kSwRiskBand)), b = (_Float16)(p * (1.0f + 2.0f * kSwRiskBand));
     return __builtin_bit_cast(uint16_t, a) != __builtin_bit_cast(uint16_t, b);
   };
-  if (bsplit) {
-    // At most 128 keys: the e pass on all eight waves with the tail's mapping, lane 16 h + i: key
-    // 16 w + i, head h. Block w = keys 16 w .. 16 w + 15, positions by row scans; the score of
-    // (key, head) sits in s_e, where the block-split scores left it, and e replaces it.
-    const int hh = lane >> 4, i16 = lane & 15, kk = 16 * wave + i16;
-    const bool sv = kk < np;
-    for (int i = tid; i < KS; i += NT) s_ridx[i] = -1;
-    const float evs = sv ? exp_cr_t(s_e[hh * KS + kk] * a.scale - pick4(Mh, hh), s_t2) : 0.0f;
-    const float fins = row_incl_scan_dpp(evs);
-    if (sv) s_e[hh * KS + kk] = evs;
-    if (i16 == 15) reinterpret_cast<float *>(&s_bt[wave])[hh] = fins;
-    if (a.keep_e && sv) a.e[(size_t)(g * kGqa + hh) * a.ld + kb + kk] = evs;
-    __syncthreads();
-    float fb = 0.0f;
-    for (int b = 0; b < wave; ++b) fb += reinterpret_cast<const float *>(&s_bt[b])[hh];
-    const float ab = pick4(P0f, hh) + (fb + (fins - evs));
-    int bin, inc;
-    bool sps;
-    classify_i(ab, ab + evs, evs, sps, bin, inc);
-    sps = sps && sv;
-    const double dincs = (sv && !sps) ? ldexp((double)inc, bin + 17) : 0.0;
-    if (sv) s_bin[hh * KS + kk] = sps ? kNoBin8 : (int8_t)bin;
-    const unsigned rowms = (unsigned)(__ballot(sps) >> (16 * hh)) & 0xFFFFu;
-    const double dins = row_incl_scan_dpp(dincs);
-    if (i16 == 15) {
-      s_bu[wave * kGqa + hh] = dins;
-      s_bc[wave * kGqa + hh] = __popc(rowms);
-    }
-    __syncthreads();                           // block totals, the binade map
-    if (sps) {
-      int cb = 0;
-      double ib = 0.0;
-      for (int b = 0; b < wave; ++b) { cb += s_bc[b * kGqa + hh]; ib += s_bu[b * kGqa + hh]; }
-      const int id = cb + __popc(rowms & ((1u << i16) - 1u));
-      if (id < kMaxSpecial) {
-        const int8_t bp8 = kk > 0 ? s_bin[hh * KS + kk - 1] : (int8_t)0;
-        const int bprev = kk > 0 ? (bp8 == kNoBin8 ? kNoBinade : bp8) : 127;
-        Special x;
-        x.ipre = (long long)(ib + (dins - dincs));
-        x.e = evs;
-        x.meta = kk | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
-        s_spec[hh * kMaxSpecial + id] = x;
-      }
-    }
-    const float p = evs * pick4(rSa, hh);
-    if (sv) reinterpret_cast<_Float16 *>(s_ps + kk)[hh] = (_Float16)p;
-    const unsigned long long rm = __ballot(sv && risky(p));
-    const bool r = ((rm >> i16) | (rm >> (i16 + 16)) | (rm >> (i16 + 32)) | (rm >> (i16 + 48))) & 1ull;
-    if (hh == 0 && sv && r) {
-      const int ri = atomicAdd(&s_nrisk, 1);
-      s_ridx[kk] = (int16_t)(ri < kSwRisk ? ri : -1);
-      atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
-    }
-  } else {
+  if (!bsplit) {
   const bool valid = kl < np;
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
@@ -763,6 +713,59 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       if (lane == 0) s_rb[kSwBlocks - 1] = rbt;
     }
   }
+  } else {
+    // At most 128 keys: the e pass on all eight waves with the tail's mapping, lane 16 h + i: key
+    // 16 w + i, head h. Block w = keys 16 w .. 16 w + 15, positions by row scans; the score of
+    // (key, head) sits in s_e, where the block-split scores left it, and e replaces it.
+    const int hh = lane >> 4, i16 = lane & 15, kk = 16 * wave + i16;
+    const bool sv = kk < np;
+    for (int i = tid; i < KS; i += NT) s_ridx[i] = -1;
+    const float evs = sv ? exp_cr_t(s_e[hh * KS + kk] * a.scale - pick4(Mh, hh), s_t2) : 0.0f;
+    const float fins = row_incl_scan_dpp(evs);
+    if (sv) s_e[hh * KS + kk] = evs;
+    if (i16 == 15) reinterpret_cast<float *>(&s_bt[wave])[hh] = fins;
+    if (a.keep_e && sv) a.e[(size_t)(g * kGqa + hh) * a.ld + kb + kk] = evs;
+    __syncthreads();
+    float fb = 0.0f;
+    for (int b = 0; b < wave; ++b) fb += reinterpret_cast<const float *>(&s_bt[b])[hh];
+    const float ab = pick4(P0f, hh) + (fb + (fins - evs));
+    int bin, inc;
+    bool sps;
+    classify_i(ab, ab + evs, evs, sps, bin, inc);
+    sps = sps && sv;
+    const double dincs = (sv && !sps) ? ldexp((double)inc, bin + 17) : 0.0;
+    if (sv) s_bin[hh * KS + kk] = sps ? kNoBin8 : (int8_t)bin;
+    const unsigned rowms = (unsigned)(__ballot(sps) >> (16 * hh)) & 0xFFFFu;
+    const double dins = row_incl_scan_dpp(dincs);
+    if (i16 == 15) {
+      s_bu[wave * kGqa + hh] = dins;
+      s_bc[wave * kGqa + hh] = __popc(rowms);
+    }
+    __syncthreads();                           // block totals, the binade map
+    if (sps) {
+      int cb = 0;
+      double ib = 0.0;
+      for (int b = 0; b < wave; ++b) { cb += s_bc[b * kGqa + hh]; ib += s_bu[b * kGqa + hh]; }
+      const int id = cb + __popc(rowms & ((1u << i16) - 1u));
+      if (id < kMaxSpecial) {
+        const int8_t bp8 = kk > 0 ? s_bin[hh * KS + kk - 1] : (int8_t)0;
+        const int bprev = kk > 0 ? (bp8 == kNoBin8 ? kNoBinade : bp8) : 127;
+        Special x;
+        x.ipre = (long long)(ib + (dins - dincs));
+        x.e = evs;
+        x.meta = kk | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
+        s_spec[hh * kMaxSpecial + id] = x;
+      }
+    }
+    const float p = evs * pick4(rSa, hh);
+    if (sv) reinterpret_cast<_Float16 *>(s_ps + kk)[hh] = (_Float16)p;
+    const unsigned long long rm = __ballot(sv && risky(p));
+    const bool r = ((rm >> i16) | (rm >> (i16 + 16)) | (rm >> (i16 + 32)) | (rm >> (i16 + 48))) & 1ull;
+    if (hh == 0 && sv && r) {
+      const int ri = atomicAdd(&s_nrisk, 1);
+      s_ridx[kk] = (int16_t)(ri < kSwRisk ? ri : -1);
+      atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
+    }
   }
   wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
@@ -1150,6 +1153,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 
 template <bool PG>
 static int stream_capacity() {
+  // every instantiation launch_stream may launch (full and short plans)
   static int cap[64];
   static bool done[64];
   int dev = 0;
@@ -1158,10 +1162,16 @@ static int stream_capacity() {
     int per = 0;
     hipDeviceProp_t pr;
     if (hipGetDeviceProperties(&pr, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG>, kResNT, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG, false>, kResNT, 0) != hipSuccess)
       cap[dev] = 0;
     else
       cap[dev] = per * pr.multiProcessorCount;
+    int per2 = 0;
+    if (cap[dev] > 0 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per2, stream_kernel<PG, true>, kResNT, 0) == hipSuccess)
+      cap[dev] = std::min(cap[dev], per2 * pr.multiProcessorCount);
+    else
+      cap[dev] = 0;
     done[dev] = true;
   }
   return cap[dev];
@@ -1174,15 +1184,13 @@ int stream_max_workgroups(bool paged) { return paged ? stream_capacity<true>() :
 hipError_t launch_stream(const ResArgs &a, hipStream_t st) {
   const dim3 grid(a.G * a.nkv), block(kResNT);
   static const bool coop = [] { const char *e = std::getenv("BKV_COOP"); return e && e[0] == '1'; }();
-  if (coop) {
-    ResArgs args = a;
-    void *kp[] = {&args};
-    if (a.L.page) return hipLaunchCooperativeKernel((const void *)stream_kernel<true>, grid, block, kp, 0, st);
-    return hipLaunchCooperativeKernel((const void *)stream_kernel<false>, grid, block, kp, 0, st);
-  }
-  if (a.L.page) hipLaunchKernelGGL((stream_kernel<true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((stream_kernel<false>), grid, block, 0, st, a);
-  return hipGetLastError();
+  const bool shrt = a.kpw <= 2 * 64;
+  const void *fn = a.L.page ? (shrt ? (const void *)stream_kernel<true, true> : (const void *)stream_kernel<true, false>)
+                            : (shrt ? (const void *)stream_kernel<false, true> : (const void *)stream_kernel<false, false>);
+  ResArgs args = a;
+  void *kp[] = {&args};
+  if (coop) return hipLaunchCooperativeKernel(fn, grid, block, kp, 0, st);
+  return hipLaunchKernel(fn, grid, block, kp, 0, st);
 }
 
 }  // namespace bkv
