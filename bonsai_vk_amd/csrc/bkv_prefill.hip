@@ -532,6 +532,91 @@ struct ScoreBlocksQ8<B0, 0> {
   static __device__ __forceinline__ void run(const uint4 (&)[8], const uint4 &, const float *, float (&)[kPxRows]) {}
 };
 
+// ---------------------------------------------------------------- q8_0 scores on the matrix cores
+// v_mfma_f32_16x16x1_4b_f32 computes, for 4 independent blocks b, D_b[i][j] += A_b[i] * B_b[j] with
+// one rounding per element: A_b[i] comes from lane 16b + i, B_b[j] from lane 16b + j, and lane l
+// holds D_b[4(l/16) + k][l%16] in accumulator register 4b + k. With K = 1 each step is exactly one
+// fp32 fma per element (the product of an fp16 q and an int8 is exact in fp32), so a chain of
+// steps in ascending dimension is the reference's serial inner sum of a q8_0 block, bit for bit.
+// Here block b of the instruction is the K block 4h + b (h = half row), row i is the workgroup's
+// row i (query i/4, head i%4), column j is key 16g + j of the wave's 64 keys (4 key groups g).
+typedef float fv16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ fv16 mfma_k1(float a, float b, fv16 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+// the raw bytes of one quarter of the wave's tile for the lane: K block 4h + l/16 (32 B) of keys
+// 16(2p + u) + l%16, u = 0, 1 (half row h, key pair p)
+struct KQuarter {
+  uint4 d[2][2];
+};
+
+template <bool PG>
+__device__ __forceinline__ void load_kquarter(const PrefillXArgs &a, int g, uint32_t key0, uint32_t kend,
+                                              int unit, int lane, KQuarter &r) {
+  constexpr int RB = row_bytes(BKV_Q8_0);
+  const int h = unit >> 1, p = unit & 1;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const uint32_t key = min(key0 + (uint32_t)(16 * (2 * p + u) + (lane & 15)), kend - 1);
+    const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+    const uint4 *src = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB + 32 * (4 * h + (lane >> 4)));
+    r.d[u][0] = src[0];
+    r.d[u][1] = src[1];
+  }
+}
+
+template <bool PG>
+__device__ __forceinline__ void load_kscales(const PrefillXArgs &a, int g, uint32_t key0, uint32_t kend,
+                                             int lane, uint4 (&sc)[4]) {
+#pragma unroll
+  for (int kg = 0; kg < 4; ++kg) {
+    const uint32_t key = min(key0 + (uint32_t)(16 * kg + (lane & 15)), kend - 1);
+    const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+    sc[kg] = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
+  }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// one unit (half row h, key pair p) of the wave's 64-key tile: the inner sums of K blocks 4h .. 4h+3
+// for key groups 2p, 2p+1 (two independent MFMA chains), then the outer steps
+// acc = acc + f16(scale) * inner in block order. qm: the lane's q16 operands for half h (s_qm[h]);
+// acc[kg][k]: key 16kg + l%16, row 4(l/16) + k.
+template <int UNIT>
+__device__ __forceinline__ void score_unit_mfma(const KQuarter &kr, const uint4 (&sc)[4], const float4 *qm,
+                                                int lane, float (&acc)[4][4]) {
+  constexpr int H = UNIT >> 1, P = UNIT & 1;
+  fv16 d[2] = {fv16{}, fv16{}};
+#pragma unroll
+  for (int i4 = 0; i4 < 8; ++i4) {
+    const float4 q4 = qm[i4 * 64 + lane];
+    const float qa[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * i4 + e;   // dimension within the block
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        d[u] = mfma_k1(qa[e], sbyte(word_of(kr.d[u][i >> 4], (i >> 2) & 3), i & 3), d[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int kg = 2 * P + u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int blk = 4 * H + b;
+      const uint32_t sw = word_of(sc[kg], blk >> 1);
+      const float s = f16_to_f32((blk & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[kg][k] = acc[kg][k] + s * d[u][4 * b + k];
+    }
+  }
+}
+
 template <int KF, int VF, bool PG>
 __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   const int n = gridDim.x, b = blockIdx.x;
@@ -561,8 +646,79 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 #endif
   // ---------------------------------------------------------------- sweep 1: exact scores
   // the rows' q16 in LDS: s_q[r][d], row r = query q0 + r/4 (clamped into the chunk), head 4g + r%4
-  float *s_q = reinterpret_cast<float *>(s_big);
   if (tid < 32) s_t2[tid] = kExp2Tab[tid];
+  if constexpr (KF) {
+    // q8_0 K on the matrix cores. s_qm[h][i4][lane] = q16 of row l%16, dims 32(4h + l/16) + 4 i4
+    // .. + 4: the lane's A operands for half h, read as one float4 per four steps.
+    float4 *s_qm = reinterpret_cast<float4 *>(s_big);
+    {
+      const int qlast = a.q_base + a.n_q - 1;
+      for (int i = tid; i < 2 * 8 * 64; i += 256) {
+        const int l = i & 63, i4 = (i >> 6) & 7, h = i >> 9;
+        const int r = l & 15;
+        const int qi = min(q0 + (r >> 2), qlast);
+        const float4 x = *reinterpret_cast<const float4 *>(
+            a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * a.qs + 32 * (4 * h + (l >> 4)) + 4 * i4);
+        s_qm[i] = make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
+      }
+    }
+    __syncthreads();
+    // the lane's rows are 4(l/16) + k: query l/16, heads 0..3
+    const int ql = lane >> 4;
+    const bool qlive = ql < nqv;
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    KQuarter k0, k1;
+    uint4 scc[4], scn[4];
+    load_kquarter<PG>(a, g, (uint32_t)(64 * w), kend, 0, lane, k0);
+    load_kscales<PG>(a, g, (uint32_t)(64 * w), kend, lane, scc);
+    for (int t = 0; t < ntile; ++t) {
+      const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
+      const uint32_t nkey0 = (uint32_t)(min(t + 1, ntile - 1) * kPxTile + 64 * w);
+      float acc[4][4];
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[kg][k] = 0.f;
+      // each unit's bytes are requested one unit ahead
+      // (the scheduling barriers keep each request ahead of the unit it overlaps: without them the
+      // compiler sinks the loads next to their first use and every unit waits on memory)
+      load_kquarter<PG>(a, g, key0, kend, 1, lane, k1);
+      __builtin_amdgcn_sched_barrier(0);
+      score_unit_mfma<0>(k0, scc, s_qm, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_kquarter<PG>(a, g, key0, kend, 2, lane, k0);
+      __builtin_amdgcn_sched_barrier(0);
+      score_unit_mfma<1>(k1, scc, s_qm, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_kquarter<PG>(a, g, key0, kend, 3, lane, k1);
+      load_kscales<PG>(a, g, nkey0, kend, lane, scn);
+      __builtin_amdgcn_sched_barrier(0);
+      score_unit_mfma<2>(k0, scc, s_qm + 8 * 64, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_kquarter<PG>(a, g, nkey0, kend, 0, lane, k0);
+      __builtin_amdgcn_sched_barrier(0);
+      score_unit_mfma<3>(k1, scc, s_qm + 8 * 64, lane, acc);
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg) {
+        scc[kg] = scn[kg];
+        const uint32_t j = key0 + (uint32_t)(16 * kg + (lane & 15));
+        const bool live = qlive && (int)j <= lim0 + ql;
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[k] = live ? acc[kg][k] * a.scale : -INFINITY;
+          mx[k] = v[k] > mx[k] ? v[k] : mx[k];
+        }
+        *reinterpret_cast<float4 *>(sc + (size_t)j * kPxRows + 4 * ql) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float m = row16_max(mx[k]);
+      if ((lane & 15) == 0) s_red[w][4 * ql + k] = m;
+    }
+  } else {
+  float *s_q = reinterpret_cast<float *>(s_big);
   {
     const int qlast = a.q_base + a.n_q - 1;
     for (int i = tid; i < kPxRows * kHd / 4; i += 256) {
@@ -578,39 +734,18 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   float mx[kPxRows];
 #pragma unroll
   for (int r = 0; r < kPxRows; ++r) mx[r] = -INFINITY;
-  constexpr int RB = row_bytes(KF ? BKV_Q8_0 : BKV_F16);
+  constexpr int RB = row_bytes(BKV_F16);
   const float *qlane = s_q + l16;
   auto kaddr = [&](int t) -> int64_t {
     return slot_t<PG>(a.L, min((uint32_t)(t * kPxTile + tid), kend - 1)) * a.nkv + g;
   };
-  // q8_0: each half of the K row (128 B) is fetched for the next tile as soon as this tile has
-  // used it, so a load has half a tile to land; fp16: two 64 B blocks ahead
-  uint4 ra[8], rb[8];
-  uint4 swn = make_uint4(0, 0, 0, 0);
-  if constexpr (KF) {
-    const int64_t ro = kaddr(0);
-    const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) { ra[c] = kp[c]; rb[c] = kp[8 + c]; }
-    swn = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
-  }
+  // fp16: two 64 B blocks ahead
   for (int t = 0; t < ntile; ++t) {
     const uint32_t j = (uint32_t)(t * kPxTile + tid);
     float acc[kPxRows];
 #pragma unroll
     for (int r = 0; r < kPxRows; ++r) acc[r] = 0.f;
-    if constexpr (KF) {
-      const uint4 sw4 = swn;
-      const int64_t ro = kaddr(min(t + 1, ntile - 1));
-      const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB);
-      ScoreBlocksQ8<0, 4>::run(ra, sw4, qlane, acc);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) ra[c] = kp[c];
-      swn = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
-      ScoreBlocksQ8<4, 4>::run(rb, sw4, qlane, acc);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) rb[c] = kp[8 + c];
-    } else {
+    {
       const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + kaddr(t) * RB);
       uint4 b0[4], b1[4];
 #pragma unroll
@@ -661,6 +796,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   for (int r = 0; r < kPxRows; ++r) {
     const float m = wave_max(mx[r]);
     if (lane == 0) s_red[w][r] = m;
+  }
   }
   __syncthreads();
   if (tid < kPxRows) {
