@@ -82,7 +82,7 @@ PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q, size_t base) {
 // the [keys][rows] score / exp scratch
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base) {
   (void)nh;
-  const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile;
+  const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile + kPxTile;   // + the exp sweep's overhang
   const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
   return base + align256(wgs * (size_t)ld * kPxRows * sizeof(float));
 }
@@ -467,7 +467,7 @@ static int prefill_common(const bkv_cache_desc *d, int layer, uint32_t pos0, int
   const size_t base = prefill_base(d);
   if (!prefill_mfma_requested() && n_q >= kPxMinQ) {
     // the exact kernel, in slices of at most kPxSlice queries
-    const int64_t ld = cdiv((int64_t)pos0 + n_q, kPxTile) * kPxTile;
+    const int64_t ld = cdiv((int64_t)pos0 + n_q, kPxTile) * kPxTile + kPxTile;
     if (ws_bytes < prefill_exact_workspace(d->nh, d->nkv, (int64_t)pos0 + n_q, base)) return BKV_EWORKSPACE;
     char *w = (char *)workspace;
     PrefillXArgs a{};

@@ -51,4 +51,28 @@ __device__ __forceinline__ float exp_cr_t(float xf, const double *t2) {
   return res;
 }
 
+// The same value in two steps, for callers that form many exps at once: exp_t_fast is the table
+// path alone, branch-free (so independent calls interleave and their table reads overlap), and
+// sets `slow` where exp_cr_t would let the library decide; exp_t_slow is that decision (x <= -104
+// rounds to +0 without the library: exp(-104) < 2^-150).
+__device__ __forceinline__ float exp_t_fast(float xf, const double *t2, bool &slow) {
+  const float kf = __builtin_rintf(xf * 46.16624130844683f);
+  const int k = (int)kf;
+  const double x = xf, kd = kf;
+  double r = fma(-kd, 0x1.62e42fefa3800p-6, x);
+  r = fma(-kd, 0x1.ef35793c76730p-50, r);
+  double p = fma_sc(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);
+  p = fma_sc(p, r, 0x1.5555555555555p-3);
+  p = fma_sc(p, r, 0.5);
+  p = fma_sc(p, r, 1.0);
+  p = fma_sc(p, r, 1.0);
+  const double y = ldexp(p * t2[k & 31], k >> 5);
+  const long long low = (long long)(__double_as_longlong(y) & 0x1FFFFFFFll) - 0x10000000ll;
+  slow = !(xf > -87.0f && xf < 88.0f) || (low >= -64 && low <= 64);
+  return (float)y;
+}
+__device__ __forceinline__ float exp_t_slow(float xf) {
+  return xf <= -104.0f ? 0.0f : (float)exp((double)xf);
+}
+
 }  // namespace bkv

@@ -173,7 +173,8 @@ struct PrefillXArgs {
   int chunk_q;                   // queries in the whole chunk (row stride of q / out)
   float scale;
   int nqb;
-  int64_t ld;                    // keys per workgroup scratch region (multiple of kPxTile)
+  int64_t ld;                    // keys per workgroup scratch region (multiple of kPxTile, one
+                                 // tile past the last key)
   const float *q;                // [chunk_q][nh] rows of hd fp32, qs floats apart
   const float *gate;             // rows gs floats apart
   int qs, gs;

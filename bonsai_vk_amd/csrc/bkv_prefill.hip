@@ -532,6 +532,11 @@ struct ScoreBlocksQ8<B0, 0> {
   static __device__ __forceinline__ void run(const uint4 (&)[8], const uint4 &, const float *, float (&)[kPxRows]) {}
 };
 
+// scratch accesses (plain loads and stores: the scratch round trips are served largely by the
+// memory-side cache, which non-temporal accesses bypass)
+__device__ __forceinline__ void st_sc4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+__device__ __forceinline__ float4 ld_sc4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
 // ---------------------------------------------------------------- q8_0 scores on the matrix cores
 // v_mfma_f32_16x16x1_4b_f32 computes, for 4 independent blocks b, D_b[i][j] += A_b[i] * B_b[j] with
 // one rounding per element: A_b[i] comes from lane 16b + i, B_b[j] from lane 16b + j, and lane l
@@ -583,14 +588,12 @@ __device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) {
 }
 
 // one unit (half row h, key pair p) of the wave's 64-key tile: the inner sums of K blocks 4h .. 4h+3
-// for key groups 2p, 2p+1 (two independent MFMA chains), then the outer steps
-// acc = acc + f16(scale) * inner in block order. qm: the lane's q16 operands for half h (s_qm[h]);
-// acc[kg][k]: key 16kg + l%16, row 4(l/16) + k.
+// for key groups 2p, 2p+1, as two independent MFMA chains. qm: the lane's q16 operands for half h
+// (s_qm[h]).
 template <int UNIT>
-__device__ __forceinline__ void score_unit_mfma(const KQuarter &kr, const uint4 (&sc)[4], const float4 *qm,
-                                                int lane, float (&acc)[4][4]) {
-  constexpr int H = UNIT >> 1, P = UNIT & 1;
-  fv16 d[2] = {fv16{}, fv16{}};
+__device__ __forceinline__ void chain_unit_mfma(const KQuarter &kr, const float4 *qm, int lane, fv16 (&d)[2]) {
+  d[0] = fv16{};
+  d[1] = fv16{};
 #pragma unroll
   for (int i4 = 0; i4 < 8; ++i4) {
     const float4 q4 = qm[i4 * 64 + lane];
@@ -603,6 +606,13 @@ __device__ __forceinline__ void score_unit_mfma(const KQuarter &kr, const uint4 
         d[u] = mfma_k1(qa[e], sbyte(word_of(kr.d[u][i >> 4], (i >> 2) & 3), i & 3), d[u]);
     }
   }
+}
+
+// the unit's outer steps acc = acc + f16(scale) * inner, in block order; acc[kg][k]: key
+// 16kg + l%16, row 4(l/16) + k
+template <int UNIT>
+__device__ __forceinline__ void outer_unit(const fv16 (&d)[2], const uint4 (&sc)[4], float (&acc)[4][4]) {
+  constexpr int H = UNIT >> 1, P = UNIT & 1;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int kg = 2 * P + u;
@@ -637,7 +647,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   constexpr int ES = kPxRows + 1;          // LDS row stride (floats) of the exp tile
   constexpr int NT = kPxRows / 16;         // MFMA row tiles
   constexpr int PR = kPxRows / 4;          // probabilities per thread per 64-key tile
-  constexpr int kBig2 = 2 * 256 * ES * 4, kBig3 = 2 * kPxRows * kPfRS + 4 * (VF ? 2 : 1) * 64 * kPfRS;
+  constexpr int kBig2 = 2 * 256 * ES * 4, kBig3 = 2 * kPxRows * kPfRS + (VF ? 0 : 4 * 64 * kPfRS);
   __shared__ __attribute__((aligned(16))) char s_big[kBig2 > kBig3 ? kBig2 : kBig3];
 
   PXTS(0);
@@ -669,11 +679,13 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     KQuarter k0, k1;
     uint4 scc[4], scn[4];
-    load_kquarter<PG>(a, g, (uint32_t)(64 * w), kend, 0, lane, k0);
-    load_kscales<PG>(a, g, (uint32_t)(64 * w), kend, lane, scc);
-    for (int t = 0; t < ntile; ++t) {
+    // tiles in descending key order: sweep 2 reads them ascending, so its first reads find the
+    // most recently written scores still in the memory-side cache
+    load_kquarter<PG>(a, g, (uint32_t)((ntile - 1) * kPxTile + 64 * w), kend, 0, lane, k0);
+    load_kscales<PG>(a, g, (uint32_t)((ntile - 1) * kPxTile + 64 * w), kend, lane, scc);
+    for (int t = ntile - 1; t >= 0; --t) {
       const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
-      const uint32_t nkey0 = (uint32_t)(min(t + 1, ntile - 1) * kPxTile + 64 * w);
+      const uint32_t nkey0 = (uint32_t)(max(t - 1, 0) * kPxTile + 64 * w);
       float acc[4][4];
 #pragma unroll
       for (int kg = 0; kg < 4; ++kg)
@@ -682,22 +694,28 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       // each unit's bytes are requested one unit ahead
       // (the scheduling barriers keep each request ahead of the unit it overlaps: without them the
       // compiler sinks the loads next to their first use and every unit waits on memory)
+      // each unit's outer steps run inside the next unit's chain
+      fv16 da[2], db[2];
       load_kquarter<PG>(a, g, key0, kend, 1, lane, k1);
       __builtin_amdgcn_sched_barrier(0);
-      score_unit_mfma<0>(k0, scc, s_qm, lane, acc);
+      chain_unit_mfma<0>(k0, s_qm, lane, da);
       __builtin_amdgcn_sched_barrier(0);
       load_kquarter<PG>(a, g, key0, kend, 2, lane, k0);
       __builtin_amdgcn_sched_barrier(0);
-      score_unit_mfma<1>(k1, scc, s_qm, lane, acc);
+      chain_unit_mfma<1>(k1, s_qm, lane, db);
+      outer_unit<0>(da, scc, acc);
       __builtin_amdgcn_sched_barrier(0);
       load_kquarter<PG>(a, g, key0, kend, 3, lane, k1);
       load_kscales<PG>(a, g, nkey0, kend, lane, scn);
       __builtin_amdgcn_sched_barrier(0);
-      score_unit_mfma<2>(k0, scc, s_qm + 8 * 64, lane, acc);
+      chain_unit_mfma<2>(k0, s_qm + 8 * 64, lane, da);
+      outer_unit<1>(db, scc, acc);
       __builtin_amdgcn_sched_barrier(0);
       load_kquarter<PG>(a, g, nkey0, kend, 0, lane, k0);
       __builtin_amdgcn_sched_barrier(0);
-      score_unit_mfma<3>(k1, scc, s_qm + 8 * 64, lane, acc);
+      chain_unit_mfma<3>(k1, s_qm + 8 * 64, lane, db);
+      outer_unit<2>(da, scc, acc);
+      outer_unit<3>(db, scc, acc);
 #pragma unroll
       for (int kg = 0; kg < 4; ++kg) {
         scc[kg] = scn[kg];
@@ -709,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
           v[k] = live ? acc[kg][k] * a.scale : -INFINITY;
           mx[k] = v[k] > mx[k] ? v[k] : mx[k];
         }
-        *reinterpret_cast<float4 *>(sc + (size_t)j * kPxRows + 4 * ql) = make_float4(v[0], v[1], v[2], v[3]);
+        st_sc4(sc + (size_t)j * kPxRows + 4 * ql, make_float4(v[0], v[1], v[2], v[3]));
       }
     }
 #pragma unroll
@@ -789,7 +807,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
         v[i] = (int)j <= lim0 + (r >> 2) && (r >> 2) < nqv ? acc[r] * a.scale : -INFINITY;
         mx[r] = v[i] > mx[r] ? v[i] : mx[r];
       }
-      *reinterpret_cast<float4 *>(dst + 4 * r4) = make_float4(v[0], v[1], v[2], v[3]);
+      st_sc4(dst + 4 * r4, make_float4(v[0], v[1], v[2], v[3]));
     }
   }
 #pragma unroll
@@ -807,53 +825,192 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 
   PXTS(1);
   // ---------------------------------------------------------------- sweep 2: exp and serial sum
-  float *et = reinterpret_cast<float *>(s_big);   // [2][256][ES]
+  // Waves 0..2 form e for 192 keys per step (one key per thread, its 16 rows) while wave 3 adds
+  // the previous step's e values of each row in key order (lane r: row r), so the serial chains
+  // run beside the exps instead of after them.
+  constexpr int kEK = 192;                        // keys per step
+  float *et = reinterpret_cast<float *>(s_big);   // [2][kEK][ES]
+  const int nstep = (int)((kend + kEK - 1) / kEK);
+  const uint32_t kscr = (uint32_t)(ntile * kPxTile);   // this workgroup's scratch keys
   float sum = 0.f;
-  float4 vn[kPxRows / 4];
-  {
-    const float *src = sc + (size_t)tid * kPxRows;
+  if (w < 3) {
+    float4 vn[kPxRows / 4];
+    auto fetch = [&](int t) {
+      const uint32_t j = min((uint32_t)(t * kEK + tid), kscr - 1);
+      const float *src = sc + (size_t)j * kPxRows;
 #pragma unroll
-    for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = *reinterpret_cast<const float4 *>(src + 4 * r4);
-  }
-  for (int t = 0; t < ntile; ++t) {
-    const uint32_t j = (uint32_t)(t * kPxTile + tid);
-    float *src = sc + (size_t)j * kPxRows;
-    float *eb = et + (t & 1) * 256 * ES + tid * ES;
-    float4 vc[kPxRows / 4];
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = ld_sc4(src + 4 * r4);
+    };
+    float mrow[kPxRows];
 #pragma unroll
-    for (int r4 = 0; r4 < kPxRows / 4; ++r4) vc[r4] = vn[r4];
-    {
-      // the next tile's scores are in flight while this tile's exp runs
-      const float *nx = sc + (size_t)(min(t + 1, ntile - 1) * kPxTile + tid) * kPxRows;
+    for (int r = 0; r < kPxRows; ++r) mrow[r] = s_m[r];
+    fetch(0);
+    for (int t = 0; t < nstep; ++t) {
+      const uint32_t j = (uint32_t)(t * kEK + tid);
+      float *src = sc + (size_t)j * kPxRows;
+      float *eb = et + (t & 1) * kEK * ES + tid * ES;
+      float4 vc[kPxRows / 4];
 #pragma unroll
-      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = *reinterpret_cast<const float4 *>(nx + 4 * r4);
-    }
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vc[r4] = vn[r4];
+      fetch(min(t + 1, nstep - 1));                // the next step's scores are in flight
+      __builtin_amdgcn_sched_barrier(0);
+      const bool in = j < kscr;                    // keys past the scores: e = 0 (none are live)
+      // all 16 exps first, then the stores: independent exps interleave (their table reads in
+      // flight together) instead of each waiting out an LDS round trip behind the stores before it
+      float ev[kPxRows], xv[kPxRows];
+      bool slow[kPxRows], any = false;
 #pragma unroll
-    for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
-      const float4 v = vc[r4];
-      float4 e;
-      e.x = exp_cr_t(v.x - s_m[4 * r4], s_t2);
-      e.y = exp_cr_t(v.y - s_m[4 * r4 + 1], s_t2);
-      e.z = exp_cr_t(v.z - s_m[4 * r4 + 2], s_t2);
-      e.w = exp_cr_t(v.w - s_m[4 * r4 + 3], s_t2);
-      *reinterpret_cast<float4 *>(src + 4 * r4) = e;
-      eb[4 * r4] = e.x;
-      eb[4 * r4 + 1] = e.y;
-      eb[4 * r4 + 2] = e.z;
-      eb[4 * r4 + 3] = e.w;
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
+        xv[4 * r4] = vc[r4].x - mrow[4 * r4];
+        xv[4 * r4 + 1] = vc[r4].y - mrow[4 * r4 + 1];
+        xv[4 * r4 + 2] = vc[r4].z - mrow[4 * r4 + 2];
+        xv[4 * r4 + 3] = vc[r4].w - mrow[4 * r4 + 3];
+      }
+#pragma unroll
+      for (int r = 0; r < kPxRows; ++r) {
+        ev[r] = exp_t_fast(xv[r], s_t2, slow[r]);
+        any = any || slow[r];
+      }
+      if (any) {
+#pragma unroll
+        for (int r = 0; r < kPxRows; ++r)
+          if (slow[r]) ev[r] = exp_t_slow(xv[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < kPxRows; ++r) ev[r] = in ? ev[r] : 0.f;
+      // (stored unconditionally: a step's keys end within the region's last tile, which is spare)
+#pragma unroll
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4)
+        st_sc4(src + 4 * r4, make_float4(ev[4 * r4], ev[4 * r4 + 1], ev[4 * r4 + 2], ev[4 * r4 + 3]));
+#pragma unroll
+      for (int r = 0; r < kPxRows; ++r) eb[r] = ev[r];
+      __syncthreads();
     }
     __syncthreads();
-    if (lane < kPxRows / 4) {                  // wave w adds rows 4 w .. 4 w + 3, one lane each
-      const float *col = et + (t & 1) * 256 * ES + 4 * w + lane;
+  } else {
+    const int r = lane & 15;
+    for (int t = 0; t <= nstep; ++t) {
+      if (t > 0 && lane < kPxRows) {
+        const float *col = et + ((t - 1) & 1) * kEK * ES + r;
 #pragma unroll 16
-      for (int k = 0; k < kPxTile; ++k) sum = sum + col[k * ES];
+        for (int k = 0; k < kEK; ++k) sum = sum + col[k * ES];
+      }
+      __syncthreads();
     }
+    if (lane < kPxRows) s_sum[r] = (r >> 2) < nqv ? sum : 1.0f;
   }
-  if (lane < kPxRows / 4) s_sum[4 * w + lane] = (w < nqv) ? sum : 1.0f;   // row 4 w + l: query w
   __syncthreads();
 
   PXTS(2);
   // ---------------------------------------------------------------- sweep 3: p16 and PV
+  if constexpr (VF) {
+    // q8_0 V straight from memory into the A operand (no LDS tile): out^T = V^T . P^T on
+    // v_mfma_f32_16x16x32_f16, wave w owning dims 64 w .. + 63. Lane l supplies row i = l%16 of
+    // dimension tile mt as dim 64 w + 4 i + mt, and keys 8(l/16) .. + 7 of each 32-key half, so one
+    // 4-byte load per key brings the lane's bytes of all four dimension tiles; a byte transpose in
+    // registers and the exact fp16 split of d*b (hi = f16(d*b), lo = d*b - hi) form the operands.
+    // P^T (p16 = f16(e / sum), all 16 rows) goes through a double-buffered LDS tile.
+    const int lr = lane & 15, lq = lane >> 4;
+    char *s_p = s_big;                                              // [2][kPxRows][kPfRS]
+    f4 o[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] = f4{0.f, 0.f, 0.f, 0.f};
+    const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
+    const int pk = tid >> 2, pr0 = PR * (tid & 3);   // this thread's probabilities: key pk, rows pr0..+PR
+    float sinv[PR];
+#pragma unroll
+    for (int i = 0; i < PR; ++i) sinv[i] = s_sum[pr0 + i];
+    const int dcol = 64 * w + 4 * lr;                 // the lane's 4 dims
+    const int sblk = dcol >> 5;                       // their q8_0 block
+    struct PvIn {
+      float4 en;                                      // e of key pk, rows pr0 .. + 3
+      uint32_t vw[16], vs[16];                        // [ks * 8 + c]: key 32 ks + 8 lq + c of the tile
+    };
+    auto load_tile = [&](int t, PvIn &in) {
+      in.en = ld_sc4(sc + ((size_t)t * kPfTile + pk) * kPxRows + pr0);
+#pragma unroll
+      for (int kc = 0; kc < 16; ++kc) {
+        const uint32_t key = min((uint32_t)(t * kPfTile + 32 * (kc >> 3) + 8 * lq + (kc & 7)), kend - 1);
+        const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+        in.vw[kc] = *reinterpret_cast<const uint32_t *>(a.L.vd + ro * kHd + dcol);
+        in.vs[kc] = *reinterpret_cast<const uint16_t *>(a.L.vs + ro * kScaleRowBytes + 2 * sblk);
+      }
+    };
+    auto tile = [&](int t, const PvIn &in) {
+      char *pb = s_p + (t & 1) * kPxRows * kPfRS;
+      const float ev[PR] = {in.en.x, in.en.y, in.en.z, in.en.w};
+#pragma unroll
+      for (int i = 0; i < PR; ++i) {
+        const _Float16 h = (_Float16)(ev[i] / sinv[i]);
+        *reinterpret_cast<_Float16 *>(pb + (pr0 + i) * kPfRS + 2 * pk) = h;
+      }
+      // the A operands (registers only): pair p of key half ks holds keys 2p, 2p+1
+      h8 ah[2][4], al[2][4];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          constexpr uint32_t kSel[4] = {0x0C040C00u, 0x0C050C01u, 0x0C060C02u, 0x0C070C03u};
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            const uint32_t bw = __builtin_amdgcn_perm(in.vw[8 * ks + 2 * pp + 1], in.vw[8 * ks + 2 * pp], kSel[mt]) ^ 0x64806480u;
+            const h2 x = as_h2(bw) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+            h2 hi, lo;
+            split_prod(x, as_h2(in.vs[8 * ks + 2 * pp] | (in.vs[8 * ks + 2 * pp + 1] << 16)), hi, lo);
+            hw[pp] = as_u(hi);
+            lw[pp] = as_u(lo);
+          }
+          ah[ks][mt] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          al[ks][mt] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const h8 bp = *reinterpret_cast<const h8 *>(pb + lr * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          o[mt] = mfma16(ah[ks][mt], bp, o[mt]);
+          o[mt] = mfma16(al[ks][mt], bp, o[mt]);
+        }
+      }
+    };
+    // tiles in descending key order (the PV sum's order is free), the last-written exp values
+    // first; two register sets, each tile's operands requested one tile ahead
+    PvIn ia, ib;
+    load_tile(nt64 - 1, ia);
+    for (int t = nt64 - 1; t >= 0; t -= 2) {
+      if (t >= 1) load_tile(t - 1, ib);
+      __builtin_amdgcn_sched_barrier(0);
+      tile(t, ia);
+      if (t < 1) break;
+      if (t >= 2) load_tile(t - 2, ia);
+      __builtin_amdgcn_sched_barrier(0);
+      tile(t - 1, ib);
+    }
+    PXTS(3);
+    // lane l holds out^T[dim 64 w + 4 m + mt][row l%16] in o[mt][r], m = 4(l/16) + r
+    const int r = lr;
+    if ((r >> 2) < nqv) {
+      const size_t row = (size_t)(q0 + (r >> 2)) * a.nh + g * kGqa + (r & 3);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d = 64 * w + 4 * (4 * lq + rr);
+        const float4 v = make_float4(o[0][rr], o[1][rr], o[2][rr], o[3][rr]);
+        *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
+        if (a.gate) {
+          const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * a.gs + d);
+          float4 og;
+          og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
+          og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
+          og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
+          og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
+          *reinterpret_cast<float4 *>(a.out_gated + row * kHd + d) = og;
+        }
+      }
+    }
+  } else {
   const int lr = lane & 15, lq = lane >> 4, kp = lane & 31, vh = lane >> 5;
   char *s_p = s_big;                                              // [2][kPxRows][kPfRS]
   char *vt_hi = s_big + 2 * kPxRows * kPfRS + w * (VF ? 2 : 1) * 64 * kPfRS;
@@ -870,13 +1027,14 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   auto load_tile = [&](int t) {
     const float *src = sc + ((size_t)t * kPfTile + pk) * kPxRows + pr0;
 #pragma unroll
-    for (int i = 0; i < PR / 4; ++i) en[i] = *reinterpret_cast<const float4 *>(src + 4 * i);
+    for (int i = 0; i < PR / 4; ++i) en[i] = ld_sc4(src + 4 * i);
     const uint32_t ka = min((uint32_t)(t * kPfTile + 2 * kp), kend - 1);
     const uint32_t kb = min((uint32_t)(t * kPfTile + 2 * kp + 1), kend - 1);
     load_v<VF, PG>(a.L, a.nkv, g, ka, kb, w, vh, vrn);
   };
-  load_tile(0);
-  for (int t = 0; t < nt64; ++t) {
+  // tiles in descending key order (the PV sum's order is free): the last-written exp values first
+  load_tile(nt64 - 1);
+  for (int t = nt64 - 1; t >= 0; --t) {
     char *pb = s_p + (t & 1) * kPxRows * kPfRS;
     float ev[PR];
 #pragma unroll
@@ -884,7 +1042,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       ev[4 * i] = en[i].x; ev[4 * i + 1] = en[i].y; ev[4 * i + 2] = en[i].z; ev[4 * i + 3] = en[i].w;
     }
     const VRaw<VF> vr = vrn;
-    load_tile(min(t + 1, nt64 - 1));   // in flight during this tile
+    load_tile(max(t - 1, 0));   // in flight during this tile
 #pragma unroll
     for (int i = 0; i < PR; ++i) {
       const _Float16 h = (_Float16)(ev[i] / s_sum[pr0 + i]);
@@ -932,6 +1090,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
         *reinterpret_cast<float4 *>(a.out_gated + row * kHd + d) = og;
       }
     }
+  }
   }
 }
 
