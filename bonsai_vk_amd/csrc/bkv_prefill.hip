@@ -677,12 +677,20 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     const int ql = lane >> 4;
     const bool qlive = ql < nqv;
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    KQuarter k0, k1;
-    uint4 scc[4], scn[4];
     // tiles in descending key order: sweep 2 reads them ascending, so its first reads find the
-    // most recently written scores still in the memory-side cache
-    load_kquarter<PG>(a, g, (uint32_t)((ntile - 1) * kPxTile + 64 * w), kend, 0, lane, k0);
-    load_kscales<PG>(a, g, (uint32_t)((ntile - 1) * kPxTile + 64 * w), kend, lane, scc);
+    // most recently written scores still in the memory-side cache.
+    // One register set per unit: each unit's bytes for the next tile are requested right after
+    // its chain for this tile, so a request has a whole tile to land (the K rows come from HBM the
+    // first time any workgroup of the XCD reads them, and the workgroups run nearly in step)
+    KQuarter kq[4];
+    uint4 scc[4];
+    {
+      const uint32_t k0 = (uint32_t)((ntile - 1) * kPxTile + 64 * w);
+      load_kquarter<PG>(a, g, k0, kend, 0, lane, kq[0]);
+      load_kquarter<PG>(a, g, k0, kend, 1, lane, kq[1]);
+      load_kquarter<PG>(a, g, k0, kend, 2, lane, kq[2]);
+      load_kquarter<PG>(a, g, k0, kend, 3, lane, kq[3]);
+    }
     for (int t = ntile - 1; t >= 0; --t) {
       const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
       const uint32_t nkey0 = (uint32_t)(max(t - 1, 0) * kPxTile + 64 * w);
@@ -691,34 +699,30 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[kg][k] = 0.f;
-      // each unit's bytes are requested one unit ahead
-      // (the scheduling barriers keep each request ahead of the unit it overlaps: without them the
-      // compiler sinks the loads next to their first use and every unit waits on memory)
-      // each unit's outer steps run inside the next unit's chain
-      fv16 da[2], db[2];
-      load_kquarter<PG>(a, g, key0, kend, 1, lane, k1);
+      load_kscales<PG>(a, g, key0, kend, lane, scc);   // (small and shared: L2 hits; used after unit 0)
+      fv16 d[2];
+      chain_unit_mfma<0>(kq[0], s_qm, lane, d);
       __builtin_amdgcn_sched_barrier(0);
-      chain_unit_mfma<0>(k0, s_qm, lane, da);
+      load_kquarter<PG>(a, g, nkey0, kend, 0, lane, kq[0]);
       __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, key0, kend, 2, lane, k0);
+      outer_unit<0>(d, scc, acc);
+      chain_unit_mfma<1>(kq[1], s_qm, lane, d);
       __builtin_amdgcn_sched_barrier(0);
-      chain_unit_mfma<1>(k1, s_qm, lane, db);
-      outer_unit<0>(da, scc, acc);
+      load_kquarter<PG>(a, g, nkey0, kend, 1, lane, kq[1]);
       __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, key0, kend, 3, lane, k1);
-      load_kscales<PG>(a, g, nkey0, kend, lane, scn);
+      outer_unit<1>(d, scc, acc);
+      chain_unit_mfma<2>(kq[2], s_qm + 8 * 64, lane, d);
       __builtin_amdgcn_sched_barrier(0);
-      chain_unit_mfma<2>(k0, s_qm + 8 * 64, lane, da);
-      outer_unit<1>(db, scc, acc);
+      load_kquarter<PG>(a, g, nkey0, kend, 2, lane, kq[2]);
       __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, nkey0, kend, 0, lane, k0);
+      outer_unit<2>(d, scc, acc);
+      chain_unit_mfma<3>(kq[3], s_qm + 8 * 64, lane, d);
       __builtin_amdgcn_sched_barrier(0);
-      chain_unit_mfma<3>(k1, s_qm + 8 * 64, lane, db);
-      outer_unit<2>(da, scc, acc);
-      outer_unit<3>(db, scc, acc);
+      load_kquarter<PG>(a, g, nkey0, kend, 3, lane, kq[3]);
+      __builtin_amdgcn_sched_barrier(0);
+      outer_unit<3>(d, scc, acc);
 #pragma unroll
       for (int kg = 0; kg < 4; ++kg) {
-        scc[kg] = scn[kg];
         const uint32_t j = key0 + (uint32_t)(16 * kg + (lane & 15));
         const bool live = qlive && (int)j <= lim0 + ql;
         float v[4];
