@@ -476,61 +476,22 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 // The default prefill: every (query, head) row reproduces the serial reference bit for bit up to
 // the PV contraction. A workgroup owns 4 queries x 4 heads = 16 rows of one KV group and all of
 // their keys, in three sweeps:
-//   1  scores on the vector ALUs in the reference's order (fp16 K: acc = acc + q16*k ascending;
-//      q8_0 K: inner = sum of q16*int8 over a block ascending, acc = acc + f16(scale)*inner; every
-//      product is exact, so each step is one fma), times the softmax scale, masked causally; the
-//      row max. Scores go to a scratch region [key][row].
+//   1  scores in the reference's order (q8_0 K: inner = sum of q16*int8 over a block ascending,
+//      as exact fp32 fma chains on the matrix cores, then acc = acc + f16(scale)*inner on the
+//      VALU; fp16 K: acc = acc + q16*k ascending on the VALU; every product is exact, so each step
+//      is one fma), times the softmax scale, masked causally; the row max. Scores go to a scratch
+//      region [key][row].
 //   2  e = exp(v - max) correctly rounded, written back over the scores; one lane per row adds
 //      them in key order (the reference's serial fp32 sum, attn_vk.h:175-189).
 //   3  p16 = f16(e / sum) (correctly rounded division, then round to nearest even), and
 //      out = sum p16 * v on the matrix cores with V as its exact fp16 hi/lo pair.
 // Only the PV sum runs in another order than the reference (fp32 accumulation of exact products).
 
-
 #ifdef BKV_EXPERIMENT_TS
 #define PXTS(i) do { if (threadIdx.x == 0 && a.ts) a.ts[blockIdx.x * 16 + (i)] = (unsigned)wall_clock64(); } while (0)
 #else
 #define PXTS(i) do { } while (0)
 #endif
-
-// one q8_0 K block (32 elements, blk) of the lane's key against every row: the reference's
-// block-factored order, inner = sum of q16*int8 ascending, acc = acc + f16(scale)*inner
-template <int BLK>
-__device__ __forceinline__ void score_block_q8(const uint4 (&rc)[8], const uint4 &sw4, const float *qlane,
-                                               float (&acc)[kPxRows]) {
-  constexpr int H = BLK & 3;   // block within the half row held in rc
-  const uint32_t kw[8] = {rc[2 * H].x, rc[2 * H].y, rc[2 * H].z, rc[2 * H].w,
-                          rc[2 * H + 1].x, rc[2 * H + 1].y, rc[2 * H + 1].z, rc[2 * H + 1].w};
-  float k0[16], k1[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    k0[e] = sbyte(kw[e >> 2], e & 3);
-    k1[e] = sbyte(kw[4 + (e >> 2)], e & 3);
-  }
-  const uint32_t sw = BLK < 2 ? sw4.x : BLK < 4 ? sw4.y : BLK < 6 ? sw4.z : sw4.w;
-  const float scl = f16_to_f32((BLK & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-  const float *qb = qlane + 32 * BLK;
-#pragma unroll
-  for (int r = 0; r < kPxRows; ++r) {
-    float inner = 0.f;
-    Dot16<16>::run(inner, qb[r * kHd], k0);
-    Dot16<16>::run(inner, qb[r * kHd + 16], k1);
-    acc[r] = acc[r] + scl * inner;
-  }
-}
-// blocks B0 .. B0+N-1 (all in one half row)
-template <int B0, int N>
-struct ScoreBlocksQ8 {
-  static __device__ __forceinline__ void run(const uint4 (&rc)[8], const uint4 &sw4, const float *qlane,
-                                             float (&acc)[kPxRows]) {
-    ScoreBlocksQ8<B0, N - 1>::run(rc, sw4, qlane, acc);
-    score_block_q8<B0 + N - 1>(rc, sw4, qlane, acc);
-  }
-};
-template <int B0>
-struct ScoreBlocksQ8<B0, 0> {
-  static __device__ __forceinline__ void run(const uint4 (&)[8], const uint4 &, const float *, float (&)[kPxRows]) {}
-};
 
 // scratch accesses (plain loads and stores: the scratch round trips are served largely by the
 // memory-side cache, which non-temporal accesses bypass)
