@@ -701,85 +701,92 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       if ((lane & 15) == 0) s_red[w][4 * ql + k] = m;
     }
   } else {
-  float *s_q = reinterpret_cast<float *>(s_big);
-  {
-    const int qlast = a.q_base + a.n_q - 1;
-    for (int i = tid; i < kPxRows * kHd / 4; i += 256) {
-      const int r = i / (kHd / 4), d4 = i % (kHd / 4);
-      const int qi = min(q0 + (r >> 2), qlast);
-      const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * a.qs + 4 * d4);
-      *reinterpret_cast<float4 *>(s_q + r * kHd + 4 * d4) =
-          make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
-    }
-  }
-  __syncthreads();
-  const int l16 = lane & 15;
-  float mx[kPxRows];
-#pragma unroll
-  for (int r = 0; r < kPxRows; ++r) mx[r] = -INFINITY;
-  constexpr int RB = row_bytes(BKV_F16);
-  const float *qlane = s_q + l16;
-  auto kaddr = [&](int t) -> int64_t {
-    return slot_t<PG>(a.L, min((uint32_t)(t * kPxTile + tid), kend - 1)) * a.nkv + g;
-  };
-  // fp16: two 64 B blocks ahead
-  for (int t = 0; t < ntile; ++t) {
-    const uint32_t j = (uint32_t)(t * kPxTile + tid);
-    float acc[kPxRows];
-#pragma unroll
-    for (int r = 0; r < kPxRows; ++r) acc[r] = 0.f;
+    // fp16 K on the matrix cores: one chain of 256 steps per (row, key), acc = acc + q16*k in
+    // ascending dimension (each product exact in fp32, each step one fma). Block b of the
+    // instruction is key group b (keys 16b .. + 15 of a 64-key set), so one MFMA advances 64 keys x
+    // 16 rows; a wave runs two sets (keys 64w .. of the two halves of a 512-key super tile) as two
+    // independent chains, streaming each key's row 32 dimensions (64 B) at a time, one chunk ahead.
+    // s_qh[d4][i] = q16 of row i, dims 4 d4 .. + 3 (the lanes of one row read the same float4).
+    float4 *s_qh = reinterpret_cast<float4 *>(s_big);
     {
-      const uint4 *kp = reinterpret_cast<const uint4 *>(a.L.kd + kaddr(t) * RB);
-      uint4 b0[4], b1[4];
+      const int qlast = a.q_base + a.n_q - 1;
+      for (int i = tid; i < (kHd / 4) * kPxRows; i += 256) {
+        const int r = i & 15, d4 = i >> 4;
+        const int qi = min(q0 + (r >> 2), qlast);
+        const float4 x = *reinterpret_cast<const float4 *>(a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * a.qs + 4 * d4);
+        s_qh[i] = make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
+      }
+    }
+    __syncthreads();
+    const int ql = lane >> 4;
+    const bool qlive = ql < nqv;
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    const int nsup = (int)((kend + 2 * kPxTile - 1) / (2 * kPxTile));
+    constexpr int RB = row_bytes(BKV_F16);
+    struct KChunk { uint4 d[2][4]; };          // [set][16 B]: dims 32c .. + 31 of the lane's key
+    auto load_chunk = [&](int T, int c, KChunk &k) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) { b0[c] = kp[c]; b1[c] = kp[4 + c]; }
+      for (int st = 0; st < 2; ++st) {
+        const uint32_t key = min((uint32_t)(T * 2 * kPxTile + st * kPxTile + 64 * w + lane), kend - 1);
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.L.kd + (slot_t<PG>(a.L, key) * a.nkv + g) * RB + 64 * c);
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        uint4 b2[4];
-        const int bn = min(blk + 2, 7);
+        for (int q = 0; q < 4; ++q) k.d[st][q] = src[q];
+      }
+    };
+    auto chunk = [&](const KChunk &k, int c, fv16 (&d)[2]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) b2[c] = kp[4 * bn + c];
-        float k0[16], k1[16];
+      for (int i4 = 0; i4 < 8; ++i4) {
+        const float4 q4 = s_qh[(8 * c + i4) * kPxRows + (lane & 15)];
+        const float qa[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t kw[4] = {b0[c].x, b0[c].y, b0[c].z, b0[c].w};
-          float *kk = c < 2 ? k0 : k1;
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * i4 + e;      // dimension within the chunk: 16-bit half i of the 64 B
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            kk[8 * (c & 1) + 2 * i] = f16_to_f32(kw[i] & 0xFFFFu);
-            kk[8 * (c & 1) + 2 * i + 1] = f16_to_f32(kw[i] >> 16);
+          for (int st = 0; st < 2; ++st) {
+            const uint32_t wv = word_of(k.d[st][i >> 3], (i >> 1) & 3);
+            d[st] = mfma_k1(qa[e], f16_to_f32((i & 1) ? (wv >> 16) : (wv & 0xFFFFu)), d[st]);
           }
         }
-        const float *qb = qlane + 32 * blk;
+      }
+    };
+    KChunk ka, kb;
+    load_chunk(nsup - 1, 0, ka);
+    // super tiles in descending key order (sweep 2 reads them ascending)
+    for (int T = nsup - 1; T >= 0; --T) {
+      fv16 d[2] = {fv16{}, fv16{}};
 #pragma unroll
-        for (int r = 0; r < kPxRows; ++r) {
-          float x = acc[r];
-          Dot16<16>::run(x, qb[r * kHd], k0);
-          Dot16<16>::run(x, qb[r * kHd + 16], k1);
-          acc[r] = x;
+      for (int c = 0; c < kHd / 32; c += 2) {
+        load_chunk(T, c + 1, kb);
+        __builtin_amdgcn_sched_barrier(0);
+        chunk(ka, c, d);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 2 < kHd / 32) load_chunk(T, c + 2, ka);
+        else load_chunk(max(T - 1, 0), 0, ka);
+        __builtin_amdgcn_sched_barrier(0);
+        chunk(kb, c + 1, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int bq = 0; bq < 4; ++bq) {
+          const uint32_t j = (uint32_t)(T * 2 * kPxTile + st * kPxTile + 64 * w + 16 * bq + (lane & 15));
+          const bool live = qlive && (int)j <= lim0 + ql;
+          float v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            v[k] = live ? d[st][4 * bq + k] * a.scale : -INFINITY;
+            mx[k] = v[k] > mx[k] ? v[k] : mx[k];
+          }
+          st_sc4(sc + (size_t)j * kPxRows + 4 * ql, make_float4(v[0], v[1], v[2], v[3]));
         }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) { b0[c] = b1[c]; b1[c] = b2[c]; }
       }
     }
-    float *dst = sc + (size_t)j * kPxRows;
 #pragma unroll
-    for (int r4 = 0; r4 < kPxRows / 4; ++r4) {
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * r4 + i;
-        v[i] = (int)j <= lim0 + (r >> 2) && (r >> 2) < nqv ? acc[r] * a.scale : -INFINITY;
-        mx[r] = v[i] > mx[r] ? v[i] : mx[r];
-      }
-      st_sc4(dst + 4 * r4, make_float4(v[0], v[1], v[2], v[3]));
+    for (int k = 0; k < 4; ++k) {
+      const float m = row16_max(mx[k]);
+      if ((lane & 15) == 0) s_red[w][4 * ql + k] = m;
     }
-  }
-#pragma unroll
-  for (int r = 0; r < kPxRows; ++r) {
-    const float m = wave_max(mx[r]);
-    if (lane == 0) s_red[w][r] = m;
-  }
   }
   __syncthreads();
   if (tid < kPxRows) {
