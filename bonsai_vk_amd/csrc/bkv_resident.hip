@@ -26,6 +26,7 @@
 
 #include "bkv_common.h"
 #include "bkv_device.h"
+#include "bkv_exp.h"
 #include "bkv_internal.h"
 #include "bkv_res_shared.h"
 
@@ -171,6 +172,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   __shared__ int s_ok[kGqa];
   __shared__ long long s_tt[kGqa];
   __shared__ int s_tc[kGqa];
+  __shared__ double s_t2[32];               // 2^(j/32), the table exp's
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
   // of one key range share an XCD, so the cache lines they split (each 64 B scale line holds all
@@ -186,6 +188,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     wi = w / nkv;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < 32) s_t2[tid] = kExp2Tab[tid];     // (read after the barriers before the e pass)
   const int64_t kb = (int64_t)wi * a.kpw;
   const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
   const int nk = (int)max((int64_t)0, ke - kb);
@@ -406,9 +409,26 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       const int64_t j = kb + kl;
       // the key's position on the running sum: the fp64 start of this workgroup plus an fp32
       // exclusive scan inside it (relative error ~1e-7, far inside the classification margin)
+      {
+        // the 4 heads' exps together, branch-free (table reads in flight at once); the rare cases
+        // the table path leaves to the library afterwards
+        float xh[kGqa];
+        bool slow[kGqa], any = false;
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) {
+          xh[h] = sc[r][h] * a.scale - Mh[h];
+          ev[r][h] = exp_t_fast(xh[h], s_t2, slow[h]);
+          any = any || (valid && slow[h]);
+        }
+        if (any) {
+#pragma unroll
+          for (int h = 0; h < kGqa; ++h)
+            if (slow[h]) ev[r][h] = exp_t_slow(xh[h]);
+        }
+      }
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
-        ev[r][h] = valid ? exp_cr(sc[r][h] * a.scale - Mh[h]) : 0.0f;
+        ev[r][h] = valid ? ev[r][h] : 0.0f;
         if (valid && a.keep_e) a.e[(size_t)(g * kGqa + h) * a.ld + j] = ev[r][h];
       }
       float fin[kGqa];
@@ -493,7 +513,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
 #pragma unroll
         for (int h = 1; h < kGqa; ++h)
           if (th == h) { Mt = Mh[h]; ct = carry[h]; it = itot[h]; ns = nspc[h]; }
-        evt = valid ? exp_cr(sct * a.scale - Mt) : 0.0f;
+        evt = valid ? exp_cr_t(sct * a.scale - Mt, s_t2) : 0.0f;
         if (valid && a.keep_e) a.e[(size_t)(g * kGqa + th) * a.ld + kb + tb + tt] = evt;
         const float fin = row_incl_scan_dpp(evt);
         const double ab = ct + (double)(fin - evt);

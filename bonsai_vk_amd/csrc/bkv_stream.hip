@@ -557,9 +557,27 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   };
   if (!bsplit) {
   const bool valid = kl < np;
+  {
+    // the 4 heads' exps together, branch-free (their table reads in flight at once), the rare
+    // cases the table path leaves to the library afterwards
+    float xh[kGqa];
+    bool slow[kGqa], any = false;
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      xh[h] = sc[h] * a.scale - Mh[h];
+      ev[h] = exp_t_fast(xh[h], s_t2, slow[h]);
+      any = any || (valid && slow[h]);
+    }
+    if (any) {
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h)
+        if (slow[h]) ev[h] = exp_t_slow(xh[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) ev[h] = valid ? ev[h] : 0.0f;
+  }
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
-    ev[h] = valid ? exp_cr_t(sc[h] * a.scale - Mh[h], s_t2) : 0.0f;
     fin[h] = wave_incl_scan_dpp(ev[h]);
     if (valid) s_e[h * KS + kl] = ev[h];
   }
