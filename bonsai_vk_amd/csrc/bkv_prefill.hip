@@ -493,6 +493,14 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 #define PXTS(i) do { } while (0)
 #endif
 
+// Workgroup barrier for LDS traffic only: every wave's LDS operations have completed, while its
+// global loads (prefetches a step or more ahead) stay in flight. __syncthreads() also releases
+// global memory, i.e. waits for every outstanding load and store of the wave first, which would
+// void those prefetches. Used where the waves exchange data through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // scratch accesses (plain loads and stores: the scratch round trips are served largely by the
 // memory-side cache, which non-temporal accesses bypass)
 __device__ __forceinline__ void st_sc4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
@@ -797,37 +805,30 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 
   PXTS(1);
   // ---------------------------------------------------------------- sweep 2: exp and serial sum
-  // Waves 0..2 form e for 192 keys per step (one key per thread, its 16 rows) while wave 3 adds
-  // the previous step's e values of each row in key order (lane r: row r), so the serial chains
-  // run beside the exps instead of after them.
+  // Waves 0..2 form e for 192 keys per step (one key per thread, its 16 rows) into an LDS tile
+  // while wave 3 adds the previous step's e values of each row in key order (lane r: row r), so
+  // the serial chains run beside the exps, and writes that tile over the scores (wave 3 reads no
+  // global memory, so its stores never hold up a wait for the exp waves' score loads).
   constexpr int kEK = 192;                        // keys per step
   float *et = reinterpret_cast<float *>(s_big);   // [2][kEK][ES]
-  const int nstep = (int)((kend + kEK - 1) / kEK);
+  const int nstep = (int)((kend + kEK - 1) / kEK + 1) & ~1;   // even: the exp waves run steps in pairs
   const uint32_t kscr = (uint32_t)(ntile * kPxTile);   // this workgroup's scratch keys
   float sum = 0.f;
   if (w < 3) {
-    float4 vn[kPxRows / 4];
-    auto fetch = [&](int t) {
-      const uint32_t j = min((uint32_t)(t * kEK + tid), kscr - 1);
-      const float *src = sc + (size_t)j * kPxRows;
-#pragma unroll
-      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vn[r4] = ld_sc4(src + 4 * r4);
-    };
     float mrow[kPxRows];
 #pragma unroll
     for (int r = 0; r < kPxRows; ++r) mrow[r] = s_m[r];
-    fetch(0);
-    for (int t = 0; t < nstep; ++t) {
-      const uint32_t j = (uint32_t)(t * kEK + tid);
-      float *src = sc + (size_t)j * kPxRows;
-      float *eb = et + (t & 1) * kEK * ES + tid * ES;
-      float4 vc[kPxRows / 4];
+    auto fetch = [&](int t, float4 (&v)[kPxRows / 4]) {
+      const uint32_t j = min((uint32_t)(t * kEK + tid), kscr - 1);
+      const float *src = sc + (size_t)j * kPxRows;
 #pragma unroll
-      for (int r4 = 0; r4 < kPxRows / 4; ++r4) vc[r4] = vn[r4];
-      fetch(min(t + 1, nstep - 1));                // the next step's scores are in flight
-      __builtin_amdgcn_sched_barrier(0);
+      for (int r4 = 0; r4 < kPxRows / 4; ++r4) v[r4] = ld_sc4(src + 4 * r4);
+    };
+    auto step = [&](int t, const float4 (&vc)[kPxRows / 4]) {
+      const uint32_t j = (uint32_t)(t * kEK + tid);
+      float *eb = et + (t & 1) * kEK * ES + tid * ES;
       const bool in = j < kscr;                    // keys past the scores: e = 0 (none are live)
-      // all 16 exps first, then the stores: independent exps interleave (their table reads in
+      // all 16 exps first, then the LDS stores: independent exps interleave (their table reads in
       // flight together) instead of each waiting out an LDS round trip behind the stores before it
       float ev[kPxRows], xv[kPxRows];
       bool slow[kPxRows], any = false;
@@ -849,25 +850,41 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
           if (slow[r]) ev[r] = exp_t_slow(xv[r]);
       }
 #pragma unroll
-      for (int r = 0; r < kPxRows; ++r) ev[r] = in ? ev[r] : 0.f;
-      // (stored unconditionally: a step's keys end within the region's last tile, which is spare)
-#pragma unroll
-      for (int r4 = 0; r4 < kPxRows / 4; ++r4)
-        st_sc4(src + 4 * r4, make_float4(ev[4 * r4], ev[4 * r4 + 1], ev[4 * r4 + 2], ev[4 * r4 + 3]));
-#pragma unroll
-      for (int r = 0; r < kPxRows; ++r) eb[r] = ev[r];
-      __syncthreads();
+      for (int r = 0; r < kPxRows; ++r) eb[r] = in ? ev[r] : 0.f;
+      lds_barrier();
+    };
+    // two register sets: each step's scores are requested two steps ahead
+    float4 va[kPxRows / 4], vb[kPxRows / 4];
+    fetch(0, va);
+    fetch(min(1, nstep - 1), vb);
+    for (int t = 0; t < nstep; t += 2) {
+      step(t, va);
+      fetch(min(t + 2, nstep - 1), va);
+      step(t + 1, vb);
+      fetch(min(t + 3, nstep - 1), vb);
     }
     __syncthreads();
   } else {
     const int r = lane & 15;
     for (int t = 0; t <= nstep; ++t) {
-      if (t > 0 && lane < kPxRows) {
-        const float *col = et + ((t - 1) & 1) * kEK * ES + r;
+      if (t > 0) {
+        const float *tile = et + ((t - 1) & 1) * kEK * ES;
+        if (lane < kPxRows) {
+          const float *col = tile + r;
 #pragma unroll 16
-        for (int k = 0; k < kEK; ++k) sum = sum + col[k * ES];
+          for (int k = 0; k < kEK; ++k) sum = sum + col[k * ES];
+        }
+        // the tile over the scores: key k's 16 rows as 4 float4, within the region's ld keys
+        float *dst = sc + (size_t)(t - 1) * kEK * kPxRows;
+        const int kmax = (int)min((int64_t)kEK, a.ld - (int64_t)(t - 1) * kEK);
+#pragma unroll
+        for (int i = 0; i < kEK * kPxRows / 4 / 64; ++i) {
+          const int f = lane + 64 * i, k = f >> 2, r4 = f & 3;
+          const float *e4 = tile + k * ES + 4 * r4;
+          if (k < kmax) st_sc4(dst + 4 * f, make_float4(e4[0], e4[1], e4[2], e4[3]));
+        }
       }
-      __syncthreads();
+      lds_barrier();
     }
     if (lane < kPxRows) s_sum[r] = (r >> 2) < nqv ? sum : 1.0f;
   }
@@ -937,7 +954,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
           al[ks][mt] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
         }
       }
-      __syncthreads();
+      lds_barrier();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const h8 bp = *reinterpret_cast<const h8 *>(pb + lr * kPfRS + 2 * (32 * ks + 8 * lq));
