@@ -335,6 +335,23 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h)
         if (th == h) mloc[h] = fmaxf(mloc[h], sct * a.scale);
   }
+  // fp16 K with q8_0 V (no register V form): this wave's V rows 32 i + 4 wave + vkk of the first
+  // pass (i < 16) and their block-pair scale words, requested once the scores are done, so that
+  // they stream in during barrier A, the e pass and the walk instead of after them (requested
+  // after barrier A instead, they hold up the e pass: 377 against 364 us per token)
+  constexpr bool VPF = !VRES && KF == BKV_F16 && VF == BKV_Q8_0;
+  constexpr int kPfRows = NT / 32;
+  uint4 pv_w[VPF ? kPfRows : 1];
+  uint32_t pv_s[VPF ? kPfRows : 1];
+  if constexpr (VPF) {
+#pragma unroll
+    for (int i = 0; i < kPfRows; ++i) {
+      const int kl = 32 * i + wave * VR::KPW + vkk;
+      const int64_t slot = slot_k<PG>(sm, min(kl, nk - 1));
+      pv_w[i] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+      pv_s[i] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+    }
+  }
   RTS(1);
 
   // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
@@ -558,7 +575,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // VRES: p16' = f16(e / S_a), the probabilities with the sum barrier A already gives, into the
   // (now free) K tile area, for the speculative PV of waves kGqa.. during the walk
   uint2 *s_ps = reinterpret_cast<uint2 *>(lds);
-  if constexpr (VRES) {
+  if constexpr (VRES || VPF) {
+    static_assert(2048 * 4 >= NT * sizeof(uint2), "s_ps (one pass) must end before s_acc");
     if (tid < nk) {
       _Float16 pk[kGqa];
 #pragma unroll
@@ -592,8 +610,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // rows with p16', and park the partial in the K tile area; after the walk they add
   // (p16 - p16') only for the keys whose rounding the exact sum changes
   float *s_acc = reinterpret_cast<float *>(lds) + 2048;   // [kGqa*EPL][NW-kGqa][64], past s_ps
-  if constexpr (VRES) {
-    static_assert(2048 * 4 >= SB * sizeof(uint2), "s_ps must end before s_acc");
+  if constexpr (VRES || VPF) {
     static_assert((2048 + kGqa * VR::EPL * (NW - kGqa) * 64) * 4 <= sizeof(lds), "s_acc must fit");
     if (wave >= kGqa) {
       float sacc[kGqa][VR::EPL];
@@ -601,7 +618,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h)
 #pragma unroll
         for (int i = 0; i < VR::EPL; ++i) sacc[h][i] = 0.0f;
-      pv_res_slots<false>(vd, vsw, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
+      if constexpr (VRES) pv_res_slots<false>(vd, vsw, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
+      else pv_res_slots<false>(pv_w, pv_s, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
 #pragma unroll
       for (int h = 0; h < kGqa; ++h)
 #pragma unroll
@@ -729,7 +747,24 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     constexpr int RS = NW * VR::KPW;        // rows per workgroup step
     constexpr int U = 4;                    // row loads in flight per lane
     constexpr int RB = row_bytes(VF);
-    for (int base = 0; base < nk; base += RS * U) {
+    int base0 = 0;
+    if constexpr (VPF) {
+      // the first pass's rows are in registers (requested after the scores): waves 0..3 add them
+      // with the exact p16; waves 4..7 added them with p16' during the walk and now add
+      // (p16 - p16') for the keys whose rounding the exact sum changed
+      static_assert(RS * U * (kPfRows / U) == NT && kPfRows == kResVTiles, "prefetched rows cover one pass");
+      if (wave < kGqa) {
+        pv_res_slots<false>(pv_w, pv_s, s_p16, nullptr, nk, wave, vkk, vsub, acc);
+      } else {
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+          for (int i = 0; i < VR::EPL; ++i) acc[h][i] = s_acc[((h * VR::EPL + i) * (NW - kGqa) + wave - kGqa) * 64 + lane];
+        pv_res_slots<true>(pv_w, pv_s, s_p16, s_ps, nk, wave, vkk, vsub, acc);
+      }
+      base0 = NT;
+    }
+    for (int base = base0; base < nk; base += RS * U) {
       uint4 wv[U];
       uint32_t sw[U];
       int kl[U];
