@@ -40,12 +40,12 @@ def test_prefill_matches_oracle(kf, vf, pos0, n_q):
     assert run_pair(dev, host, 0, pos0, n_q, seed=pos0 + 1) <= TOL
 
 
-@pytest.mark.parametrize("kf,vf", [(BKV_Q8_0, BKV_Q8_0), (BKV_Q8_0, BKV_F16)])
-@pytest.mark.parametrize("pos0,n_q", [(240, 16), (752, 16), (1520, 16), (0, 600)])
+@pytest.mark.parametrize("kf,vf", [(BKV_Q8_0, BKV_Q8_0), (BKV_Q8_0, BKV_F16), (BKV_F16, BKV_Q8_0)])
+@pytest.mark.parametrize("pos0,n_q", [(240, 16), (496, 16), (752, 16), (1008, 16), (1520, 16), (0, 600)])
 def test_prefill_tile_edges(kf, vf, pos0, n_q):
     """Chunks whose workgroups end exactly on the exact kernel's tile edges (256-key score tiles,
-    192-key exp steps, 64-key PV tiles: 256, 768 and 1536 keys), and a chunk of two 512-query
-    slices."""
+    512-key fp16-K super tiles, 192-key exp steps, 64-key PV tiles: 256, 512, 768, 1024 and 1536
+    keys), and a chunk of two 512-query slices."""
     say(f"prefill tile edges kf={kf} vf={vf} pos0={pos0} n_q={n_q}")
     n = pos0 + n_q
     dev, host = pair(1, n, kf, vf)
