@@ -335,11 +335,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h)
         if (th == h) mloc[h] = fmaxf(mloc[h], sct * a.scale);
   }
-  // fp16 K with q8_0 V (no register V form): this wave's V rows 32 i + 4 wave + vkk of the first
-  // pass (i < 16) and their block-pair scale words, requested once the scores are done, so that
-  // they stream in during barrier A, the e pass and the walk instead of after them (requested
-  // after barrier A instead, they hold up the e pass: 377 against 364 us per token)
-  constexpr bool VPF = !VRES && KF == BKV_F16 && VF == BKV_Q8_0;
+  // q8_0 V without the register V form (fp16 K, or more than one pass): this wave's V rows
+  // 32 i + 4 wave + vkk of the first pass (i < 16) and their block-pair scale words, requested once
+  // the scores are done, so that they stream in during barrier A, the e pass and the walk instead
+  // of after them (requested after barrier A instead, they hold up the e pass: 377 against 364 us
+  // per token for fp16 K at 32K)
+  constexpr bool VPF = !VRES && VF == BKV_Q8_0;
   constexpr int kPfRows = NT / 32;
   uint4 pv_w[VPF ? kPfRows : 1];
   uint32_t pv_s[VPF ? kPfRows : 1];
