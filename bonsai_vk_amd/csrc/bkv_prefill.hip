@@ -51,6 +51,23 @@ __device__ __forceinline__ h2 bytes_h2(uint32_t wb) {
   return x - h2{(_Float16)1152.0f, (_Float16)1152.0f};
 }
 
+// e / s correctly rounded to fp32, from rs = fp32(1/s) correctly rounded, without a division:
+// q0 = e*rs is within 1.5 ulps of e/s; one correction q1 = q0 + (e - s*q0)*rs (the remainder exact
+// by fma) brings it within one ulp, and a second is then the correctly rounded quotient (Markstein's
+// theorem: y within half an ulp of 1/s, q within one ulp of e/s, r = e - s*q exact => RN(q + r*y)
+// = RN(e/s)). Valid for 0 <= e <= s, s >= 1 (a softmax sum includes the maximum's e = 1): the
+// remainders stay normal while the quotient is above 2^-60, and below that the quotient rounds to
+// an fp16 zero whatever its last bits.
+__device__ __forceinline__ float div_by_sum(float e, float s, float rs) {
+  const float q0 = e * rs;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-s, q0, e), rs, q0);
+  float q2 = __builtin_fmaf(__builtin_fmaf(-s, q1, e), rs, q1);
+  // the fp32 result itself: a conversion to fp16 of the fma would otherwise be folded into one
+  // mixed-precision fma rounding once, straight to fp16 (a different result at fp16 ties)
+  asm volatile("" : "+v"(q2));
+  return q2;
+}
+
 // exact fp16 split of s*b: hi = f16(s*b) (rounded fp16 product), lo = the product's rounding error
 __device__ __forceinline__ void split_prod(h2 b, h2 s, h2 &hi, h2 &lo) {
   hi = b * s;
@@ -483,8 +500,9 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 //      region [key][row].
 //   2  e = exp(v - max) correctly rounded, written back over the scores; one lane per row adds
 //      them in key order (the reference's serial fp32 sum, attn_vk.h:175-189).
-//   3  p16 = f16(e / sum) (correctly rounded division, then round to nearest even), and
-//      out = sum p16 * v on the matrix cores with V as its exact fp16 hi/lo pair.
+//   3  p16 = f16(e / sum) (the correctly rounded fp32 quotient, from e * (1/sum) by two remainder
+//      corrections, then round to nearest even), and out = sum p16 * v on the matrix cores with V
+//      as its exact fp16 hi/lo pair.
 // Only the PV sum runs in another order than the reference (fp32 accumulation of exact products).
 
 #ifdef BKV_EXPERIMENT_TS
@@ -906,9 +924,12 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     for (int mt = 0; mt < 4; ++mt) o[mt] = f4{0.f, 0.f, 0.f, 0.f};
     const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
     const int pk = tid >> 2, pr0 = PR * (tid & 3);   // this thread's probabilities: key pk, rows pr0..+PR
-    float sinv[PR];
+    float ssum[PR], srcp[PR];
 #pragma unroll
-    for (int i = 0; i < PR; ++i) sinv[i] = s_sum[pr0 + i];
+    for (int i = 0; i < PR; ++i) {
+      ssum[i] = s_sum[pr0 + i];
+      srcp[i] = 1.0f / ssum[i];
+    }
     const int dcol = 64 * w + 4 * lr;                 // the lane's 4 dims
     const int sblk = dcol >> 5;                       // their q8_0 block
     struct PvIn {
@@ -930,7 +951,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
       const float ev[PR] = {in.en.x, in.en.y, in.en.z, in.en.w};
 #pragma unroll
       for (int i = 0; i < PR; ++i) {
-        const _Float16 h = (_Float16)(ev[i] / sinv[i]);
+        const _Float16 h = (_Float16)div_by_sum(ev[i], ssum[i], srcp[i]);
         *reinterpret_cast<_Float16 *>(pb + (pr0 + i) * kPfRS + 2 * pk) = h;
       }
       // the A operands (registers only): pair p of key half ks holds keys 2p, 2p+1
@@ -1011,6 +1032,12 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     for (int nt = 0; nt < NT; ++nt) o[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
   const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
   const int pk = tid >> 2, pr0 = PR * (tid & 3);   // this thread's probabilities: key pk, rows pr0..+PR
+  float ssum[PR], srcp[PR];
+#pragma unroll
+  for (int i = 0; i < PR; ++i) {
+    ssum[i] = s_sum[pr0 + i];
+    srcp[i] = 1.0f / ssum[i];
+  }
   float4 en[PR / 4];
   VRaw<VF> vrn;
   auto load_tile = [&](int t) {
@@ -1034,7 +1061,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     load_tile(max(t - 1, 0));   // in flight during this tile
 #pragma unroll
     for (int i = 0; i < PR; ++i) {
-      const _Float16 h = (_Float16)(ev[i] / s_sum[pr0 + i]);
+      const _Float16 h = (_Float16)div_by_sum(ev[i], ssum[i], srcp[i]);
       *reinterpret_cast<_Float16 *>(pb + (pr0 + i) * kPfRS + 2 * pk) = h;
     }
     put_vt<VF>(vr, kp, vh, vt_hi, vt_lo);
