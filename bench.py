@@ -277,7 +277,7 @@ def prefill_leg(cpu=True, reps=5):
            "us_per_layer": round(res["exact"] / L, 1),
            "algorithmic_tflops": round(fl / (res["exact"] * 1e-6) / 1e12, 2),
            "bound": "fp32 matrix cores (serial-order score chains, one fma per MFMA step) and the "
-                    "vector ALUs (correctly rounded exp, serial sums, p16 division)",
+                    "vector ALUs (correctly rounded exp, serial sums, the p16 quotients)",
            "score_chain_fp32_mfma_tflops_over_chunk": round(score_flops / (res["exact"] * 1e-6) / 1e12, 1),
            "fp32_mfma_peak_tflops": 157.3,
            "mfma_variant": {"value": round(res["mfma"], 1), "unit": "us/chunk",
