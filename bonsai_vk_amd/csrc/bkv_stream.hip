@@ -911,6 +911,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   if (kwave) {
     // ---------------------------------------------------------------- barrier B, the walk
     const int h = wave;
+    __builtin_amdgcn_s_setprio(2);
     {
       unsigned long long v[2];
       poll_tagged(trec + h * GM * 2, 2, 2, G, tag, v, err);
@@ -926,6 +927,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         s_ok[h] = gres ? 1 : 0;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     unsigned kc = kSwKW;                       // K-wave spin barrier target
     kwave_sync(&s_kctr, kc);
     RTS(5);
