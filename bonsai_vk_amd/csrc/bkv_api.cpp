@@ -29,8 +29,8 @@ static inline int64_t next_pow2(int64_t x) {
 }
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // the fewest keys a resident or stream workgroup takes (short contexts use fewer workgroups; at 4K
-// keys 128 beat 256 and 512 by 12 % and 30 %)
-constexpr int64_t kResMinKeysPerWg = 128;
+// keys 96 ran ~1 % faster than 64 and 128, and 4 % and more faster than 80, 176, 256 and 512)
+constexpr int64_t kResMinKeysPerWg = 96;
 
 // Partition sizes of the split path. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16
 // keys). Probability chunks: kE2Chunk keys. PV: enough workgroups to cover the chip (512 at nkv = 4)
@@ -129,7 +129,7 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
   p.off_part = o;   o += align256((size_t)np_bound * nh * kHd * sizeof(float));
   size_t total = o;
   // the resident path: one workgroup per CU, up to kResMaxG per KV group, >= 128 keys each
-  // (below 16K keys fewer, longer workgroups finish sooner: 4K keys run 4 % faster at 32 per group than at 64)
+  // (below 64 x kResMinKeysPerWg keys fewer workgroups per group, each with at least that many keys)
   p.rG = 0;
   p.rvres = p.rstream = false;
   const int rcap = resident_max_workgroups(kfmt, vfmt);
