@@ -12,6 +12,7 @@
 #include "bkv_common.h"
 #include "bkv_device.h"
 #include "bkv_internal.h"
+#include "bkv_q8dot.h"
 
 namespace bkv {
 
@@ -49,13 +50,31 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
   constexpr int RB = row_bytes(KF);
   stage_rows<NT, T::KEYS, T::DPR, T::UPR>(tile, L.kd, RB, L, a.nkv, g, j0, n);
   if (KF == BKV_Q8_0) stage_rows<NT, T::KEYS, 1, T::UPR>(tile + 16, L.ks, kScaleRowBytes, L, a.nkv, g, j0, n);
-  float qv[kGqa][kHd / 16];
-  load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
-  __syncthreads();
-  asm volatile("s_nop 4");      // DPP source registers written above: VALU-write -> DPP-read gap
-
+  const float *qg = a.q + (size_t)g * kGqa * a.qs;
   float acc[kGqa];
-  qk_row_dot<KF>(tile + tid * T::UPR, qv, acc);
+  if constexpr (KF == BKV_Q8_0) {
+    // the int8 matrix cores on the q rows' digits (bkv_q8dot.h)
+    __shared__ int8_t s_lim[kLimBytes];
+    __shared__ int s_lt[kGqa * 8];
+    __shared__ unsigned s_wide;
+    if (tid == 0) s_wide = 0u;
+    __syncthreads();
+    q8lim_build(qg, a.qs, s_lim, s_lt, &s_wide, tid, NT);
+    __syncthreads();                           // the digits and the K tile
+    if (s_wide == 0u) {
+      Q8Lim qlim;
+      q8lim_load(s_lim, s_lt, qlim);
+      q8_score64(tile + (tid & ~63) * T::UPR, T::UPR, qlim, acc);
+    } else {
+      q8_score_key_slow(tile + tid * T::UPR, qg, a.qs, acc);
+    }
+  } else {
+    float qv[kGqa][kHd / 16];
+    load_q16_rows(qg, qv, a.qs);
+    __syncthreads();
+    asm volatile("s_nop 4");      // DPP source registers written above: VALU-write -> DPP-read gap
+    qk_row_dot<KF>(tile + tid * T::UPR, qv, acc);
+  }
 
   // scores, and per head the partition's (max, sum exp) used to place each key on the running sum
   const bool valid = tid < n;

@@ -133,53 +133,17 @@ struct DotIl<C, 16> {
   static __device__ __forceinline__ void run(float (&)[C], const float (&)[C], const float (&)[C][16]) {}
 };
 
-// Scores of one cached key against the group's 4 query heads, each one accumulation chain in
-// ascending d (attn_vk.h:156-170). row: the key's LDS row - q8_0: 16 data uint4 then the scale
-// uint4; fp16: 32 data uint4. The chains of the 4 heads (and, q8_0, of two blocks, whose inner sums
-// are independent) are interleaved. The caller guarantees at least two VALU cycles between writing qv
-// and this call (DPP source hazard).
+// Scores of one cached fp16 K row against the group's 4 query heads, each one accumulation chain
+// in ascending d (attn_vk.h:156-170): acc = acc + q16_d * k_d, every product exact. row: the key's
+// 32 data uint4 in LDS. The chains of the 4 heads are interleaved. The caller guarantees at least
+// two VALU cycles between writing qv and this call (DPP source hazard). (q8_0 K: bkv_q8dot.h.)
 template <int KF>
 __device__ __forceinline__ void qk_row_dot(const uint4 *row, const float (&qv)[kGqa][kHd / 16],
                                            float (&acc)[kGqa]) {
+  static_assert(KF == BKV_F16, "q8_0 K scores: bkv_q8dot.h");
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) acc[h] = 0.0f;
-  if (KF == BKV_Q8_0) {
-    const uint4 scl = row[16];
-#pragma unroll
-    for (int bp = 0; bp < kHd / 64; ++bp) {
-      // blocks 2 bp and 2 bp + 1: their inner sums over the two 16-element halves, 8 chains
-      float inner[2 * kGqa];
-#pragma unroll
-      for (int c = 0; c < 2 * kGqa; ++c) inner[c] = 0.0f;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        float x[2 * kGqa][16], q[2 * kGqa];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-          const uint4 w = row[2 * (2 * bp + bb) + half];
-          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int i = 0; i < 16; ++i) x[bb * kGqa][i] = sbyte(u[i >> 2], i & 3);
-#pragma unroll
-          for (int h = 0; h < kGqa; ++h) {
-            q[bb * kGqa + h] = qv[h][2 * (2 * bp + bb) + half];
-            if (h > 0)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) x[bb * kGqa + h][i] = x[bb * kGqa][i];
-          }
-        }
-        DotIl<2 * kGqa>::run(inner, q, x);
-      }
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int b = 2 * bp + bb;
-        const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
-        const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-#pragma unroll
-        for (int h = 0; h < kGqa; ++h) acc[h] = __fadd_rn(acc[h], __fmul_rn(sc, inner[bb * kGqa + h]));
-      }
-    }
-  } else {
+  {
 #pragma unroll
     for (int j = 0; j < kHd / 16; ++j) {
       const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];

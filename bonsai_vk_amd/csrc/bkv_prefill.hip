@@ -26,6 +26,7 @@
 #include "bkv_device.h"
 #include "bkv_exp.h"
 #include "bkv_internal.h"
+#include "bkv_q8dot.h"
 
 namespace bkv {
 
@@ -524,94 +525,20 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ void st_sc4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 __device__ __forceinline__ float4 ld_sc4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
-// ---------------------------------------------------------------- q8_0 scores on the matrix cores
+// ---------------------------------------------------------------- fp16 K scores on the matrix cores
 // v_mfma_f32_16x16x1_4b_f32 computes, for 4 independent blocks b, D_b[i][j] += A_b[i] * B_b[j] with
 // one rounding per element: A_b[i] comes from lane 16b + i, B_b[j] from lane 16b + j, and lane l
 // holds D_b[4(l/16) + k][l%16] in accumulator register 4b + k. With K = 1 each step is exactly one
-// fp32 fma per element (the product of an fp16 q and an int8 is exact in fp32), so a chain of
-// steps in ascending dimension is the reference's serial inner sum of a q8_0 block, bit for bit.
-// Here block b of the instruction is the K block 4h + b (h = half row), row i is the workgroup's
-// row i (query i/4, head i%4), column j is key 16g + j of the wave's 64 keys (4 key groups g).
+// fp32 fma per element (the product of two fp16 values is exact in fp32), so a chain of steps in
+// ascending dimension is the reference's serial score, bit for bit. (q8_0 K: bkv_q8dot.h.)
 typedef float fv16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ fv16 mfma_k1(float a, float b, fv16 c) {
   return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
 }
 
-// the raw bytes of one quarter of the wave's tile for the lane: K block 4h + l/16 (32 B) of keys
-// 16(2p + u) + l%16, u = 0, 1 (half row h, key pair p)
-struct KQuarter {
-  uint4 d[2][2];
-};
-
-template <bool PG>
-__device__ __forceinline__ void load_kquarter(const PrefillXArgs &a, int g, uint32_t key0, uint32_t kend,
-                                              int unit, int lane, KQuarter &r) {
-  constexpr int RB = row_bytes(BKV_Q8_0);
-  const int h = unit >> 1, p = unit & 1;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const uint32_t key = min(key0 + (uint32_t)(16 * (2 * p + u) + (lane & 15)), kend - 1);
-    const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
-    const uint4 *src = reinterpret_cast<const uint4 *>(a.L.kd + ro * RB + 32 * (4 * h + (lane >> 4)));
-    r.d[u][0] = src[0];
-    r.d[u][1] = src[1];
-  }
-}
-
-template <bool PG>
-__device__ __forceinline__ void load_kscales(const PrefillXArgs &a, int g, uint32_t key0, uint32_t kend,
-                                             int lane, uint4 (&sc)[4]) {
-#pragma unroll
-  for (int kg = 0; kg < 4; ++kg) {
-    const uint32_t key = min(key0 + (uint32_t)(16 * kg + (lane & 15)), kend - 1);
-    const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
-    sc[kg] = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
-  }
-}
-
 __device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
-// one unit (half row h, key pair p) of the wave's 64-key tile: the inner sums of K blocks 4h .. 4h+3
-// for key groups 2p, 2p+1, as two independent MFMA chains. qm: the lane's q16 operands for half h
-// (s_qm[h]).
-template <int UNIT>
-__device__ __forceinline__ void chain_unit_mfma(const KQuarter &kr, const float4 *qm, int lane, fv16 (&d)[2]) {
-  d[0] = fv16{};
-  d[1] = fv16{};
-#pragma unroll
-  for (int i4 = 0; i4 < 8; ++i4) {
-    const float4 q4 = qm[i4 * 64 + lane];
-    const float qa[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 4 * i4 + e;   // dimension within the block
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-        d[u] = mfma_k1(qa[e], sbyte(word_of(kr.d[u][i >> 4], (i >> 2) & 3), i & 3), d[u]);
-    }
-  }
-}
-
-// the unit's outer steps acc = acc + f16(scale) * inner, in block order; acc[kg][k]: key
-// 16kg + l%16, row 4(l/16) + k
-template <int UNIT>
-__device__ __forceinline__ void outer_unit(const fv16 (&d)[2], const uint4 (&sc)[4], float (&acc)[4][4]) {
-  constexpr int H = UNIT >> 1, P = UNIT & 1;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int kg = 2 * P + u;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int blk = 4 * H + b;
-      const uint32_t sw = word_of(sc[kg], blk >> 1);
-      const float s = f16_to_f32((blk & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc[kg][k] = acc[kg][k] + s * d[u][4 * b + k];
-    }
-  }
 }
 
 template <int KF, int VF, bool PG>
@@ -645,69 +572,84 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   // the rows' q16 in LDS: s_q[r][d], row r = query q0 + r/4 (clamped into the chunk), head 4g + r%4
   if (tid < 32) s_t2[tid] = kExp2Tab[tid];
   if constexpr (KF) {
-    // q8_0 K on the matrix cores. s_qm[h][i4][lane] = q16 of row l%16, dims 32(4h + l/16) + 4 i4
-    // .. + 4: the lane's A operands for half h, read as one float4 per four steps.
-    float4 *s_qm = reinterpret_cast<float4 *>(s_big);
+    // q8_0 K on the int8 matrix cores (bkv_q8dot.h): the digits of each of the workgroup's
+    // queries' 4 q rows in LDS, their A operands in registers. A wave scores its 64 keys of a tile
+    // as 4 key groups x 4 queries (one MFMA per block each) and transposes each key group's 4
+    // queries so that lane l holds rows 4(l/16) + k: query l/16, heads 0..3. Each key group's K
+    // bytes are requested two key groups ahead (the rows come from HBM the first time any
+    // workgroup of the XCD reads them; the workgroups run nearly in step).
+    int8_t *s_lim = reinterpret_cast<int8_t *>(s_big);                    // [query][kLimBytes]
+    int *s_lt = reinterpret_cast<int *>(s_big + kPxQ * kLimBytes);        // [query][head][block]
+    static_assert(kPxQ * (kLimBytes + kGqa * 8 * 4) <= sizeof(s_big), "digits in the big LDS area");
+    __shared__ unsigned s_wide;
+    if (tid == 0) s_wide = 0u;
+    __syncthreads();
+    const int qlast = a.q_base + a.n_q - 1;
+    auto qrows = [&](int jq) {                 // the 4 q rows of query jq (clamped into the chunk)
+      return a.q + ((size_t)min(q0 + jq, qlast) * a.nh + g * kGqa) * a.qs;
+    };
+#pragma unroll 1
+    for (int jq = 0; jq < kPxQ; ++jq)
+      q8lim_build(qrows(jq), a.qs, s_lim + jq * kLimBytes, s_lt + jq * kGqa * 8, &s_wide, tid, 256);
+    __syncthreads();
+    const bool wide = s_wide != 0u;
+    long qa[kPxQ][8];
     {
-      const int qlast = a.q_base + a.n_q - 1;
-      for (int i = tid; i < 2 * 8 * 64; i += 256) {
-        const int l = i & 63, i4 = (i >> 6) & 7, h = i >> 9;
-        const int r = l & 15;
-        const int qi = min(q0 + (r >> 2), qlast);
-        const float4 x = *reinterpret_cast<const float4 *>(
-            a.q + ((size_t)qi * a.nh + g * kGqa + (r & 3)) * a.qs + 32 * (4 * h + (l >> 4)) + 4 * i4);
-        s_qm[i] = make_float4(round_f16(x.x), round_f16(x.y), round_f16(x.z), round_f16(x.w));
+      Q8Lim t;
+#pragma unroll
+      for (int jq = 0; jq < kPxQ; ++jq) {
+        q8lim_load(s_lim + jq * kLimBytes, s_lt + jq * kGqa * 8, t);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) qa[jq][b] = t.a[b];
       }
     }
-    __syncthreads();
-    // the lane's rows are 4(l/16) + k: query l/16, heads 0..3
-    const int ql = lane >> 4;
+    const int ql = lane >> 4, n16 = lane & 15;
     const bool qlive = ql < nqv;
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    // tiles in descending key order: sweep 2 reads them ascending, so its first reads find the
-    // most recently written scores still in the memory-side cache.
-    // One register set per unit: each unit's bytes for the next tile are requested right after
-    // its chain for this tile, so a request has a whole tile to land (the K rows come from HBM the
-    // first time any workgroup of the XCD reads them, and the workgroups run nearly in step)
-    KQuarter kq[4];
-    uint4 scc[4];
-    {
-      const uint32_t k0 = (uint32_t)((ntile - 1) * kPxTile + 64 * w);
-      load_kquarter<PG>(a, g, k0, kend, 0, lane, kq[0]);
-      load_kquarter<PG>(a, g, k0, kend, 1, lane, kq[1]);
-      load_kquarter<PG>(a, g, k0, kend, 2, lane, kq[2]);
-      load_kquarter<PG>(a, g, k0, kend, 3, lane, kq[3]);
-    }
+    constexpr int RB = row_bytes(BKV_Q8_0);
+    struct KG { long b[8]; uint4 s; };        // one key group's B operands and the lane key's scales
+    auto load_kg = [&](uint32_t key0, int kg, KG &r) {
+      const uint32_t key = min(key0 + (uint32_t)(16 * kg + n16), kend - 1);
+      const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+      const uint8_t *src = a.L.kd + ro * RB + 8 * ql;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) r.b[b] = *reinterpret_cast<const long *>(src + 32 * b);
+      r.s = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
+    };
+    KG kn[2];
+#pragma unroll
+    for (int kg = 0; kg < 2; ++kg) load_kg((uint32_t)((ntile - 1) * kPxTile + 64 * w), kg, kn[kg]);
     for (int t = ntile - 1; t >= 0; --t) {
       const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
       const uint32_t nkey0 = (uint32_t)(max(t - 1, 0) * kPxTile + 64 * w);
       float acc[4][4];
 #pragma unroll
-      for (int kg = 0; kg < 4; ++kg)
+      for (int kg = 0; kg < 4; ++kg) {
+        const KG cur = kn[kg & 1];
+        __builtin_amdgcn_sched_barrier(0);
+        load_kg(kg < 2 ? key0 : nkey0, (kg + 2) & 3, kn[kg & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (!wide) {
+          float r[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[kg][k] = 0.f;
-      load_kscales<PG>(a, g, key0, kend, lane, scc);   // (small and shared: L2 hits; used after unit 0)
-      fv16 d[2];
-      chain_unit_mfma<0>(kq[0], s_qm, lane, d);
-      __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, nkey0, kend, 0, lane, kq[0]);
-      __builtin_amdgcn_sched_barrier(0);
-      outer_unit<0>(d, scc, acc);
-      chain_unit_mfma<1>(kq[1], s_qm, lane, d);
-      __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, nkey0, kend, 1, lane, kq[1]);
-      __builtin_amdgcn_sched_barrier(0);
-      outer_unit<1>(d, scc, acc);
-      chain_unit_mfma<2>(kq[2], s_qm + 8 * 64, lane, d);
-      __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, nkey0, kend, 2, lane, kq[2]);
-      __builtin_amdgcn_sched_barrier(0);
-      outer_unit<2>(d, scc, acc);
-      chain_unit_mfma<3>(kq[3], s_qm + 8 * 64, lane, d);
-      __builtin_amdgcn_sched_barrier(0);
-      load_kquarter<PG>(a, g, nkey0, kend, 3, lane, kq[3]);
-      __builtin_amdgcn_sched_barrier(0);
-      outer_unit<3>(d, scc, acc);
+          for (int jq = 0; jq < kPxQ; ++jq) {
+            int tt[8];
+            const int4 t0 = *reinterpret_cast<const int4 *>(s_lt + (jq * kGqa + ql) * 8);
+            const int4 t1 = *reinterpret_cast<const int4 *>(s_lt + (jq * kGqa + ql) * 8 + 4);
+            tt[0] = t0.x; tt[1] = t0.y; tt[2] = t0.z; tt[3] = t0.w;
+            tt[4] = t1.x; tt[5] = t1.y; tt[6] = t1.z; tt[7] = t1.w;
+            r[jq] = q8_score16r(cur.b, cur.s, qa[jq], tt);
+          }
+          transpose_rows4(r);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[kg][k] = r[k];
+        } else {                               // lane: key 16 kg + l%16 against query l/16's 4 heads
+          const uint32_t key = min(key0 + (uint32_t)(16 * kg + n16), kend - 1);
+          const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+          q8_score_key_slow(reinterpret_cast<const uint32_t *>(a.L.kd + ro * RB),
+                            reinterpret_cast<const uint32_t *>(a.L.ks + ro * kScaleRowBytes), qrows(ql), a.qs, acc[kg]);
+        }
+      }
 #pragma unroll
       for (int kg = 0; kg < 4; ++kg) {
         const uint32_t j = key0 + (uint32_t)(16 * kg + (lane & 15));

@@ -321,28 +321,8 @@ __device__ __forceinline__ T wave_incl_scan_dpp(T v) {
   v += dpp0<0x143, 0xC>(v);
   return v;
 }
-// one query head's score of one key (the tail): as qk_row_dot, with qt[j] = q16[h][16j + lane%16]
-// for the head h of the lane's DPP row
-__device__ __forceinline__ void qk_row_dot1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
-  const uint4 scl = row[16];
-#pragma unroll
-  for (int b = 0; b < kHd / 32; ++b) {
-    const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
-    float x0[16], x1[16];
-    const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x0[i] = sbyte(u0[i >> 2], i & 3);
-      x1[i] = sbyte(u1[i >> 2], i & 3);
-    }
-    const uint32_t sw = (b >> 1) == 0 ? scl.x : (b >> 1) == 1 ? scl.y : (b >> 1) == 2 ? scl.z : scl.w;
-    const float sc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-    float inner = 0.0f;
-    Dot16<16>::run(inner, qt[2 * b], x0);
-    Dot16<16>::run(inner, qt[2 * b + 1], x1);
-    acc = __fadd_rn(acc, __fmul_rn(sc, inner));
-  }
-}
+// one query head's score of one fp16 K key (the tail), half row CH: as qk_row_dot, with qt[j] =
+// q16[h][16j + lane%16] for the head h of the lane's DPP row
 template <int CH>
 __device__ __forceinline__ void qk_f16_half1(const uint4 *row, const float (&qt)[kHd / 16], float &acc) {
 #pragma unroll

@@ -27,6 +27,7 @@
 #include "bkv_common.h"
 #include "bkv_device.h"
 #include "bkv_exp.h"
+#include "bkv_q8dot.h"
 #include "bkv_internal.h"
 #include "bkv_res_shared.h"
 
@@ -173,6 +174,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   __shared__ long long s_tt[kGqa];
   __shared__ int s_tc[kGqa];
   __shared__ double s_t2[32];               // 2^(j/32), the table exp's
+  __shared__ unsigned s_wide;                // q8_0 K: the digits do not fit (fp64 score path)
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
   // of one key range share an XCD, so the cache lines they split (each 64 B scale line holds all
@@ -189,6 +191,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid < 32) s_t2[tid] = kExp2Tab[tid];     // (read after the barriers before the e pass)
+  if (tid == 0) s_wide = 0u;                   // (read after the barrier that follows the digits)
   const int64_t kb = (int64_t)wi * a.kpw;
   const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
   const int nk = (int)max((int64_t)0, ke - kb);
@@ -250,9 +253,25 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   const int tn = TAIL ? max(0, nk - tb) : 0;
   uint4 *tail_t = ldx;
   if (TAIL && tn > 0 && wave == 0) stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 0);
-  float qv[kGqa][kHd / 16];
-  load_q16_rows(a.q + (size_t)g * kGqa * a.qs, qv, a.qs);
-  asm volatile("s_nop 4");
+  // q8_0 K: the digits of the group's q rows (int8 matrix cores, bkv_q8dot.h) in the exchange area
+  // past the tail rows, free until the e phase; fp16 K: q16 in registers for the DPP chains
+  const float *qg = a.q + (size_t)g * kGqa * a.qs;
+  float qv[kGqa][kHd / (KF == BKV_Q8_0 ? 256 : 16)];
+  Q8Lim qlim;
+  bool wide = false;
+  if constexpr (KF == BKV_Q8_0) {
+    int8_t *s_lim = reinterpret_cast<int8_t *>(ldx) + kResTail * kUPR * 16;
+    int *s_lt = reinterpret_cast<int *>(s_lim + kLimBytes);
+    static_assert(kResTail * kUPR * 16 + kLimBytes + kGqa * 8 * 4 <= sizeof(ldx), "digits beside the tail rows");
+    __syncthreads();                             // s_wide cleared
+    q8lim_build(qg, a.qs, s_lim, s_lt, &s_wide, tid, NT);
+    __syncthreads();
+    q8lim_load(s_lim, s_lt, qlim);
+    wide = s_wide != 0u;
+  } else {
+    load_q16_rows(qg, qv, a.qs);
+    asm volatile("s_nop 4");
+  }
 
   // VRES: this wave's V rows 32 s + 4 wave + vkk (s < kResVTiles) and their block-pair scale words,
   // loaded right behind the first K tile so that they stream in during the scores
@@ -286,8 +305,11 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       } else {
         wait_vm<0>();
       }
-      if (KF == BKV_Q8_0) {
-        qk_row_dot<KF>(kt + lane * kUPR, qv, acc);
+      if constexpr (KF == BKV_Q8_0) {
+        if (!wide)
+          q8_score64(kt, kUPR, qlim, acc);
+        else
+          q8_score_key_slow(kt + lane * kUPR, qg, a.qs, acc);
       } else {
         qk_f16_half<0>(kt + lane * kUPR, qv, acc);
         wave_lds_sync();
@@ -312,17 +334,25 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   const int th = lane >> 4, tt = lane & 15;
   float sct = 0.0f;
   if (TAIL && tn > 0 && wave == 0) {
-    float qt[kHd / 16];
-#pragma unroll
-    for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, th, j);
-#pragma unroll
-    for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
     wait_vm<kVLoads<XE>>();
-    asm volatile("s_nop 4");
     float acc1 = 0.0f;
     if constexpr (KF == BKV_Q8_0) {
-      qk_row_dot1(tail_t + tt * kUPR, qt, acc1);
+      // the MFMA key group's lane (key tt, head th) is this lane's (key, head)
+      const uint4 *trow = tail_t + min(tt, tn - 1) * kUPR;
+      if (!wide) {
+        acc1 = q8_score16(trow, qlim);
+      } else {
+        float a4[kGqa];
+        q8_score_key_slow(trow, qg, a.qs, a4);
+        acc1 = pick4(a4, th);
+      }
     } else {                               // fp16 rows: the second half row follows the first
+      float qt[kHd / 16];
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, th, j);
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
+      asm volatile("s_nop 4");
       qk_f16_half1<0>(tail_t + tt * kUPR, qt, acc1);
       wave_lds_sync();
       stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 1);

@@ -27,6 +27,7 @@
 #include <cstdlib>
 
 #include "bkv_exp.h"
+#include "bkv_q8dot.h"
 #include "bkv_res_shared.h"
 
 namespace bkv {
@@ -195,6 +196,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ int s_nrisk;
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
+  __shared__ int s_lt[kGqa * 8];            // q8_0 K digits: the exponent of each (head, block)
+  __shared__ unsigned s_wide, s_limctr;     // the digits do not fit (fp64 path); waves done reading them
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
   // of one key range share an XCD (each 64 B scale line holds all groups' scales of a slot)
@@ -233,7 +236,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2, 0ull);
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
-  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; }
+  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; s_wide = 0u; s_limctr = 0u; }
   if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
@@ -314,32 +317,31 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   // and scores them while the other waves' tiles are still landing
   if (wave == 0) wait_vm_n((t0 ? kUPR : 0) + (tr > 0 ? 1 : 0));
   __syncthreads();                             // s_q (and s_x) visible to every wave
-  wait_vm<0>();
+  // the q8_0 K digits of the group's q rows, in the V scale rows' LDS (their loads come after the
+  // scores, once every wave has read its A operands)
+  int8_t *s_lim = reinterpret_cast<int8_t *>(vsc);
+  static_assert(kLimBytes <= (int)sizeof(vsc), "digits in the V scale rows");
+  q8lim_build(reinterpret_cast<const float *>(s_q), kHd, s_lim, s_lt, &s_wide, tid, NT);
+  __syncthreads();
+  Q8Lim qlim;
+  q8lim_load(s_lim, s_lt, qlim);
+  const bool wide = s_wide != 0u;
+  lds_arrive(&s_limctr);
+  wait_vm<0>();                                // this wave's K tile
   RTSV(0);
 
   // ---------------------------------------------------------------- scores
-  // Each lane: key 64 w + lane against the group's 4 heads (attn_vk.h:156-170). The tail keys 2 w,
-  // 2 w + 1: lane 8 p + b computes block b's inner sum of pair p (key 2 w + p / 4, head p % 4), the
-  // 8 blocks' terms are then added in order by the pair's first lane (the same arithmetic).
+  // q8_0 K on the int8 matrix cores (bkv_q8dot.h): each wave scores its 64 keys as four MFMA key
+  // groups and transposes them to one key per lane, 4 heads each; the tail keys 2 w, 2 w + 1 are
+  // one more (partly empty) key group.
   float sc[kGqa];
+  float sv_short = 0.0f;                       // SHORT: the score of key 16 w + lane % 16, head lane / 16
   float mloc[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) { mloc[h] = -INFINITY; sc[h] = 0.0f; }
   const int kl = 64 * wave + lane;             // this lane's pass key
   constexpr bool bsplit = SHORT;               // short workgroups: all 8 waves score and run the e pass
   {
-    float qv[kGqa][kHd / 16];
-    if (!bsplit) {
-      const float *qf = reinterpret_cast<const float *>(s_q) + (lane & 15);
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h)
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qf[h * kHd + 16 * j]);
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h)
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qv[h][j]));
-    }
     // decode_step: the wave that holds the new token's K row quantises the token (both rows stored
     // to the cache here), patches its K row into the tile and leaves its V row in s_x
     uint4 ad = make_uint4(0u, 0u, 0u, 0u);
@@ -365,67 +367,42 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     RTSV(5);
     RTSC(6);
     if (bsplit) {
-      // at most 2 x 64 keys: every wave scores blocks of keys instead of whole keys. Wave w, row r
-      // of 16 lanes: block b = 4 (w & 1) + r of keys 64 p + 16 (w >> 1) + (lane & 15); each block's
-      // term f16(scale) * inner goes to LDS, and waves 0-1 add a key's 8 terms in block order (the
-      // same arithmetic as the lane-per-key chain)
+      // at most 2 x 64 keys: every wave scores one MFMA key group of 16
       RTS(14);
       if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
       __syncthreads();                         // both tiles (and the patched row) are in LDS
-      const int i16 = lane & 15, b = 4 * (wave & 1) + (lane >> 4);
-      float qb[kGqa][2];
-      {
-        const float *qf = reinterpret_cast<const float *>(s_q) + 32 * b + i16;
-#pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          qb[h][0] = round_f16(qf[h * kHd]);
-          qb[h][1] = round_f16(qf[h * kHd + 16]);
+      // wave w: keys 16 w + lane % 16 against head lane / 16 (the scores go to s_e, over the K
+      // tiles, once every wave has scored)
+      const int i16 = lane & 15, hg = lane >> 4, key = 16 * wave + i16;
+      float v = 0.0f;
+      if (16 * wave < np) {                    // (uniform)
+        const uint4 *row = kt + min(key, np - 1) * kUPR;
+        if (!wide) {
+          v = q8_score16(row, qlim);
+        } else {
+          float a4[kGqa];
+          q8_score_key_slow(row, reinterpret_cast<const float *>(s_q), kHd, a4);
+          v = pick4(a4, hg);
         }
       }
-      float4 *s_terms = reinterpret_cast<float4 *>(kt + 2 * 64 * kUPR);   // [key][block] x 4 heads
-#pragma unroll 1
-      for (int p = 0; p < 2; ++p) {
-        const int k0 = 64 * p + 16 * (wave >> 1);
-        if (k0 >= np) break;                   // (uniform)
-        const int key = min(k0 + i16, np - 1);
-        const uint4 *row = kt + key * kUPR;
-        const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
-        const uint32_t sw = reinterpret_cast<const uint32_t *>(&row[16])[b >> 1];
-        const float dsc = f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu));
-        const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        float x[32];
+      const bool live = key < np;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = sbyte(u[i >> 2], i & 3);
-        float inner[kGqa] = {0.f, 0.f, 0.f, 0.f};
-        BlockChain<32>::run(inner, qb, x);
-        if (k0 + i16 < np)
-          s_terms[key * 8 + b] = make_float4(__fmul_rn(dsc, inner[0]), __fmul_rn(dsc, inner[1]),
-                                             __fmul_rn(dsc, inner[2]), __fmul_rn(dsc, inner[3]));
-      }
+      for (int h = 0; h < kGqa; ++h) mloc[h] = (live && h == hg) ? v * a.scale : -INFINITY;
+      sv_short = live ? v : 0.0f;
       __syncthreads();
-      if (kl < np) {
-        float acc1[kGqa] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int bb = 0; bb < 8; ++bb) {
-          const float4 t = s_terms[kl * 8 + bb];
-          acc1[0] = __fadd_rn(acc1[0], t.x);
-          acc1[1] = __fadd_rn(acc1[1], t.y);
-          acc1[2] = __fadd_rn(acc1[2], t.z);
-          acc1[3] = __fadd_rn(acc1[3], t.w);
-        }
-#pragma unroll
-        for (int h = 0; h < kGqa; ++h) {
-          sc[h] = acc1[h];
-          mloc[h] = fmaxf(mloc[h], acc1[h] * a.scale);
-          s_e[h * KS + kl] = acc1[h];          // for the e pass, which reads them by (key, head)
-        }
-      }
+      if (live) s_e[hg * KS + key] = v;        // for the e pass, which reads them by (key, head)
       RTSV(1);
     } else if (t0) {
       RTS(14);
       if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
       float acc1[kGqa];
-      qk_row_dot<BKV_Q8_0>(kt + kl * kUPR, qv, acc1);
+      if (!wide) {
+        // four MFMA key groups of 16 (lane: key 16 c + lane % 16, head lane / 16), then transposed
+        // to one key per lane
+        q8_score64(kt + 64 * wave * kUPR, kUPR, qlim, acc1);
+      } else {
+        q8_score_key_slow(kt + kl * kUPR, reinterpret_cast<const float *>(s_q), kHd, acc1);
+      }
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
         sc[h] = acc1[h];
@@ -435,51 +412,44 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
     if (tr > 0) {
       if (wave == aw && kp >= NP) patch_k(ttl + (kp - NP) * kUPR);
-      const int p = lane >> 3, b = lane & 7, t = 2 * wave + (p >> 2), h = p & 3;
-      const int tk = min(t, tn - 1);
-      const uint4 *row = ttl + tk * kUPR;
-      const uint4 w0 = row[2 * b], w1 = row[2 * b + 1];
-      const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-      const float4 *qh = s_q + h * (kHd / 4) + 8 * b;
-      float inner = 0.0f;
+      // the wave's tail keys 2 w, 2 w + 1 as MFMA columns 0, 1 (lane: key column lane % 16, head
+      // lane / 16)
+      const int n16 = lane & 15, hg = lane >> 4, t = 2 * wave + n16;
+      const uint4 *row = ttl + (2 * wave + min(n16, tr - 1)) * kUPR;
+      float v[kGqa];
+      if (!wide) {
+        const float x = q8_score16(row, qlim);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float4 q4 = qh[c];
-        const float qq[4] = {round_f16(q4.x), round_f16(q4.y), round_f16(q4.z), round_f16(q4.w)};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) inner = fmaf(qq[i], sbyte(u[c], i), inner);   // exact products
+        for (int h = 0; h < kGqa; ++h) v[h] = x;
+      } else {
+        q8_score_key_slow(row, reinterpret_cast<const float *>(s_q), kHd, v);
       }
-      const uint32_t sw = reinterpret_cast<const uint32_t *>(&row[16])[b >> 1];
-      const float term = __fmul_rn(f16_to_f32((b & 1) ? (sw >> 16) : (sw & 0xFFFFu)), inner);
-      // acc = ((0 + term_0) + term_1) + ... + term_7 on the pair's first lane (row_shl j brings
-      // lane + j of the same row of 16)
-      float acc1 = term;
-      acc1 = __fadd_rn(acc1, dpp<0x101>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x102>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x103>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x104>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x105>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x106>(term));
-      acc1 = __fadd_rn(acc1, dpp<0x107>(term));
-      if (b == 0 && t < tn) s_tsc[t * kGqa + h] = acc1;
+      const bool tv = n16 < tr;
+      if (!wide) {
+        if (tv) s_tsc[t * kGqa + hg] = v[0];
+      } else if (tv && hg == 0) {
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) s_tsc[t * kGqa + h] = v[h];
+      }
 #pragma unroll
       for (int hh = 0; hh < kGqa; ++hh) {      // fold the tail scores into the lane maxima
-        const float v = (b == 0 && t < tn && h == hh) ? acc1 * a.scale : -INFINITY;
-        mloc[hh] = fmaxf(mloc[hh], v);
+        const bool on = tv && (wide ? hg == 0 : hg == hh);
+        mloc[hh] = fmaxf(mloc[hh], on ? v[wide ? hh : 0] * a.scale : -INFINITY);
       }
     }
   }
   RTSC(7);
   // V after the scores: a wave requests its V rows once it has scored its K rows, so the K stream
   // (which the scores wait for) is not shared with the V stream (which only the PV needs)
-  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
-  uint32_t xs = 0u;                            // the tail slot's scale word
+  lds_wait(&s_limctr, NW);                     // every wave has read its digits (they sit in vsc)
   {
     const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
     const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
                  "s"(sb) : "memory", "m0");
   }
+  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
+  uint32_t xs = 0u;                            // the tail slot's scale word
   if (vt) {
     const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
     xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
@@ -499,7 +469,12 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   float lsum[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
-    float l = (t0 && kl < np) ? __expf(sc[h] * a.scale - mloc[h]) : 0.0f;
+    float l;
+    if constexpr (SHORT) {
+      l = (16 * wave + (lane & 15) < np && h == (lane >> 4)) ? __expf(sv_short * a.scale - mloc[h]) : 0.0f;
+    } else {
+      l = (t0 && kl < np) ? __expf(sc[h] * a.scale - mloc[h]) : 0.0f;
+    }
     if (wave == 0 && tt < tn && th == h) l += __expf(s_tsc[tt * kGqa + h] * a.scale - mloc[h]);
     lsum[h] = l;
   }

@@ -215,7 +215,8 @@ void bko_load_row(const bkv_cache_desc *d, int which, int layer, int64_t pos, in
 /* ------------------------------------------------------------------ decode (serial mirror)
  * One head row, exactly runtime_vk/attn_vk.h:156-212 in order:
  *   score_j = sum over d ascending of q16_d * k_d, as acc = acc + a*b (fp16 K: lo then hi half of
- *             each word; q8_0 K: k_d = f16(scale)*int8 in fp32, so each product rounds once)
+ *             each word); q8_0 K (this build's contract): per 32-block the correctly rounded exact
+ *             sum of q16_d * int8_d, then acc = acc + f16(scale) * inner in block order
  *   v_j = score_j * scale; mx = max_j v_j from -INF; p_j = exp(v_j - mx); sum ascending; p_j /= sum
  *   p16_j = f16_rne(p_j); out_d = sum over j ascending of f16->f32(p16_j) * V_jd
  *   gated_d = out_d * (1 / (1 + exp(-gate_d)))
@@ -239,19 +240,22 @@ static void decode_row(const bkv_cache_desc *d, int layer, uint32_t nfill, const
       }
     } else {
       /* q8_0 K (no reference counterpart: the reference never compresses K). The block scale is
-       * factored out of each 32-element block: inner = sum over the block, ascending, of
-       * q16_d * int8_d (every product exact in fp32), then acc = acc + f16(scale) * inner. */
+       * factored out of each 32-element block, and the block's inner sum q16_d * int8_d is the
+       * fp32 rounding of its EXACT value: every product is a multiple of 2^-24 below 2^23, so the
+       * fp64 sum below is exact in any order (below 2^28 in magnitude) and one cast rounds it.
+       * Then acc = acc + f16(scale) * inner, in block order. */
       const uint32_t *row = arr(d, 0, layer) + (slot * d->nkv + g) * (hd / 4);
       const uint32_t *srow = arr(d, 1, layer) + (slot * d->nkv + g) * (hd / 64);
       for (int b = 0; b < hd / 32; ++b) {
         const uint32_t sw = srow[b >> 1];
         const float sc = bko_f16_to_f32((uint16_t)((b & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
-        float inner = 0.0f;
+        double x = 0.0;
         for (int e = 32 * b; e < 32 * b + 32; ++e) {
           const uint32_t w = row[e >> 2];
           const int by = (int)((w >> ((e & 3) * 8)) & 0xFFu);
-          inner = inner + q16[e] * (float)(by >= 128 ? by - 256 : by);
+          x += (double)q16[e] * (double)(by >= 128 ? by - 256 : by);
         }
+        const float inner = (float)x;
         const float t = sc * inner;
         acc = acc + t;
       }

@@ -26,6 +26,9 @@
  *   bko_attn_decode .. the reference's attn_score_row/attn_softmax_row/attn_pv_row/attn_gate_row
  *                      compiled from runtime_vk/attn_vk.h (bit-exact, fp16 cache), plus closed forms:
  *                      one key -> p = 1, identical keys -> uniform p, GQA-identical scores.
+ *                      q8_0 K (no reference counterpart, this build's contract): each block's inner
+ *                      sum against exact rational arithmetic (Python fractions) rounded once to fp32,
+ *                      and against brute-force edge blocks (fp16 subnormal q, -128 bytes, max fp16).
  *   bko_attn_decode_ideal ... numpy float64 recomputation in tests.
  *   bko_norm_rope_row  in libm-float mode, the reference's attn_rms_norm + attn_rope compiled from
  *                      runtime_vk/attn_vk.h (bit-exact); closed forms: position 0 is the weighted

@@ -2,6 +2,8 @@
 (runtime_vk/attn_vk.h compiled into oracle/_ref) and by closed forms."""
 import ctypes
 
+from fractions import Fraction
+
 import numpy as np
 import pytest
 
@@ -192,21 +194,49 @@ def test_exp_modes_differ_only_where_libm_is_not_correctly_rounded():
     assert oracle.rel_err(a, b) < 1e-4 and oracle.rel_err(ag, bg) < 1e-4
 
 
+def _exact_q8_inner(q16_row, i8_block):
+    """The exact rational sum of q16 * int8 over one block, rounded once to fp32. The sum is a
+    multiple of 2^-24 below 2^28, so float() of the Fraction is exact and only np.float32 rounds."""
+    s = sum((Fraction(float(a)) * int(b) for a, b in zip(q16_row, i8_block)), Fraction(0))
+    return np.float32(float(s))
+
+
 def test_q8_k_dot_is_block_factored():
-    """q8_0 K: score = sum over blocks of f16(scale) * (ascending exact sum of q16*int8)."""
+    """q8_0 K: score = sum in block order of f16(scale) * inner_b, inner_b = the exact sum of
+    q16 * int8 over the block rounded once to fp32 (checked here with exact rational arithmetic)."""
     n = 8
     c, _, _ = make_cache(n, Q8_0, F16, seed=14, outliers=3)
     q, _ = q_gate(14)
+    # edge operands: fp16 subnormal q, a max-magnitude q and a q that rounds to zero
+    q[0, 3] = 3e-7
+    q[1, 40] = 60000.0
+    q[2, 7] = 1e-9
     _, _, sc, _, _ = c.decode(0, n, q, debug=True)
     q16 = oracle.f16_to_f32(oracle.f32_to_f16(q))
-    i8 = c.k_data[0].view(np.int8).reshape(n, 4, 8, 32).astype(np.float32)
+    i8 = c.k_data[0].view(np.int8).reshape(n, 4, 8, 32)
     s = c.k_scales[0].view(np.float16).reshape(n, 4, 8).astype(np.float32)
     for h in range(16):
         for j in range(n):
             acc = np.float32(0)
             for b in range(8):
-                inner = np.float32(0)
-                for e in range(32):
-                    inner = np.float32(inner + np.float32(q16[h, 32 * b + e] * i8[j, h // 4, b, e]))
+                inner = _exact_q8_inner(q16[h, 32 * b:32 * b + 32], i8[j, h // 4, b])
                 acc = np.float32(acc + np.float32(s[j, h // 4, b] * inner))
             assert acc == sc[h, j]
+
+
+def test_q8_k_inner_is_correctly_rounded_not_serial():
+    """A block whose serial fp32 chain rounds differently from the exact sum: the oracle's score
+    follows the exact sum (the property that makes the inner sum order-free)."""
+    n = 1
+    c, _, _ = make_cache(n, Q8_0, F16, seed=3, outliers=0)
+    i8 = c.k_data[0].view(np.int8).reshape(n, 4, 8, 32).copy()
+    i8[0, 0, 0, :] = 0
+    i8[0, 0, 0, 0], i8[0, 0, 0, 1], i8[0, 0, 0, 2] = 127, 1, -127
+    c.k_data[0][:] = i8.view(np.uint8).reshape(c.k_data[0].shape)
+    q = np.zeros((16, 256), np.float32)
+    q[0, 0], q[0, 1], q[0, 2] = 2048.0, 2.0 ** -14, 2048.0   # serial: (2048*127 + tiny) - 2048*127 = 0
+    _, _, sc, _, _ = c.decode(0, n, q, debug=True)
+    sc0 = np.float32(c.k_scales[0].view(np.float16).reshape(n, 4, 8)[0, 0, 0])
+    assert sc[0, 0] == np.float32(sc0 * np.float32(2.0 ** -14))
+    serial = np.float32(np.float32(2048.0 * 127) + np.float32(2.0 ** -14)) - np.float32(2048.0 * 127)
+    assert serial == 0.0 and sc[0, 0] != 0.0
