@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
   __shared__ int s_lt[kGqa * 8];            // q8_0 K digits: the exponent of each (head, block)
-  __shared__ unsigned s_wide, s_limctr;     // the digits do not fit (fp64 path); waves done reading them
+  __shared__ unsigned s_wide;               // the q8_0 K digits do not fit (fp64 score path)
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups
   // of one key range share an XCD (each 64 B scale line holds all groups' scales of a slot)
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2, 0ull);
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
-  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; s_wide = 0u; s_limctr = 0u; }
+  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; s_wide = 0u; }
   if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
@@ -326,7 +326,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   Q8Lim qlim;
   q8lim_load(s_lim, s_lt, qlim);
   const bool wide = s_wide != 0u;
-  lds_arrive(&s_limctr);
   wait_vm<0>();                                // this wave's K tile
   RTSV(0);
 
@@ -439,28 +438,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
   }
   RTSC(7);
-  // V after the scores: a wave requests its V rows once it has scored its K rows, so the K stream
-  // (which the scores wait for) is not shared with the V stream (which only the PV needs)
-  lds_wait(&s_limctr, NW);                     // every wave has read its digits (they sit in vsc)
-  {
-    const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
-    const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
-                 "s"(sb) : "memory", "m0");
-  }
-  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
-  uint32_t xs = 0u;                            // the tail slot's scale word
-  if (vt) {
-    const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
-    xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-  }
-#pragma unroll
-  for (int s = 0; s < kSwSlots; ++s) {
-    const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
-    const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
-    vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-  }
-
   RTS(1);
   RTSV(2);
   // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
@@ -481,6 +458,32 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   block_sum4(lsum, shf4);
   if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
   RTS(9);
+  // V after the statistics: the K stream (which the scores wait for) is not shared with the V
+  // stream (which only the PV needs), and the statistics do not wait behind the V requests, whose
+  // issue stalls a wave while its CU's memory queue is full. (Polling waves that request theirs
+  // only after barrier A hold up the e pass: 288 against 280 us per token.) The digits in vsc were
+  // read before the barriers of the statistics.
+  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
+  uint32_t xs = 0u;                            // the tail slot's scale word
+  auto request_v = [&]() {
+    {
+      const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
+      const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
+                   "s"(sb) : "memory", "m0");
+    }
+    if (vt) {
+      const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
+      xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+    }
+#pragma unroll
+    for (int s = 0; s < kSwSlots; ++s) {
+      const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
+      const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
+      vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+    }
+  };
+  request_v();
 
   // ---------------------------------------------------------------- barrier A: global max
   // wave h polls head h's statistics of every workgroup of the group (the V stream has landed by
