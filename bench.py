@@ -148,16 +148,64 @@ def kernel_name(cache, n):
             0: "qk_kernel + e_kernel + pv_kernel + merge_kernel (four launches per layer)"}[cache.decode_path(n)]
 
 
+# the sources whose code a decode launch runs: a traffic summary measured on other code is stale
+TRAFFIC_SOURCES = ["bkv_stream.hip", "bkv_resident.hip", "bkv_res_shared.h", "bkv_device.h", "bkv_common.h",
+                   "bkv_exp.h", "bkv_q8dot.h", "bkv_internal.h"]
+
+
+def kernel_sources_sha():
+    """sha256 (first 16 hex digits) of the decode kernels' sources, as the traffic summaries
+    record it"""
+    import hashlib
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, "bonsai_vk_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def launched_kernel(cache, n):
+    """rocprof's name of the single-launch kernel a contiguous q8_0 K+V decode_step at n keys runs
+    (None for the split path)"""
+    path = cache.decode_path(n)
+    if path == 3:
+        # the library's plan: 64 workgroups per KV group (256 CUs, nkv 4), at least 96 keys each;
+        # workgroups of at most 128 keys run the short instantiation
+        wgs = min(64, -(-n // 96))
+        short = -(-n // wgs) <= 128
+        return f"void bkv::stream_kernel<false, {'true' if short else 'false'}>(bkv::ResArgs)"
+    if path == 2:
+        return "void bkv::resident_kernel<1, 1, true, false>(bkv::ResArgs)"
+    return None
+
+
 def measured_traffic(cache, n):
     """HBM bytes per launch of the single-launch kernel this workload takes, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_q8_32k_traffic.json), or None when
-    that summary is absent or the call takes the split path."""
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_q8_32k_traffic.json); None when
+    that summary is absent, names another kernel than the one this run launches, or was measured on
+    other kernel sources (its source_sha differs from the tree's)."""
     name = {3: "stream_kernel", 2: "resident_kernel"}.get(cache.decode_path(n))
+    if name is None:
+        return None
     path = os.path.join(ROOT, "profiles", f"{name}_q8_32k_traffic.json")
-    if name is None or not os.path.exists(path):
+    if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        summary = json.load(f)
+    if summary.get("kernel") != launched_kernel(cache, n) or summary.get("source_sha") != kernel_sources_sha():
+        return None
+    return summary.get("hbm_bytes_per_launch")
+
+
+def check_no_timeout(cache, where):
+    """A decode whose bounded wait gave up produced no valid output: stop with an error instead of
+    reporting its time."""
+    from bonsai_vk_amd import BkvError
+    try:
+        cache.check_workspace()
+    except BkvError as e:
+        print(f"bench.py: a decode call timed out ({where}): {e}", file=sys.stderr, flush=True)
+        sys.exit(3)
 
 
 def host_threads():
@@ -360,6 +408,7 @@ def main():
         step(W + i)
     t_end.record()
     torch.cuda.synchronize()
+    check_no_timeout(cache, "timed region")
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / K
     ns = [ctx + 1 + i for i in range(K)]
@@ -373,6 +422,7 @@ def main():
         step(W + K + i)
         evs[i + 1].record()
     torch.cuda.synchronize()
+    check_no_timeout(cache, "roofline pass")
     avg_call_s = sum(evs[i].elapsed_time(evs[i + 1]) for i in range(RP)) / RP / L / 1e3
     rp_bytes = sum(algorithmic_bytes(ctx + 1 + K + i, args.gate) for i in range(RP)) / RP
     achieved = rp_bytes / avg_call_s / 1e9

@@ -24,6 +24,7 @@ EXPORTS = [
     "bkv_last_hip_error", "bkv_version", "bkv_debug_layout", "bkv_workspace_init", "bkv_decode_path",
     "bkv_kv_fill_synthetic", "bkv_attn_decode_qg", "bkv_decode_step_qg", "bkv_attn_prefill_chunk_qg", "bkv_prefill_step", "bkv_qk_norm_rope_append", "bkv_attn_decode_window",
     "bkv_workspace_error", "bkv_error_words", "bkv_decode_step_static", "bkv_static_scratch_bytes",
+    "bkv_static_error", "bkv_static_reset", "bkv_static_debug_address",
 ]
 
 
@@ -88,6 +89,9 @@ def lib():
         "bkv_error_words": (i32, [D, ctypes.POINTER(ctypes.c_uint64)]),
         "bkv_decode_step_static": (i32, [D, i32, u32, P, P, P, P, P, P, P]),
         "bkv_static_scratch_bytes": (sz, []),
+        "bkv_static_error": (i32, [D, P]),
+        "bkv_static_reset": (i32, [P]),
+        "bkv_static_debug_address": (i32, [ctypes.POINTER(ctypes.c_void_p)]),
         "bkv_qk_norm_rope_append": (i32, [D, i32, u32, i32, P, P, P, P, P, i32, ctypes.c_float,
                                           ctypes.c_float, P, P]),
     }

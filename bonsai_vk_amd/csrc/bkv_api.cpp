@@ -36,8 +36,10 @@ constexpr int64_t kResMinKeysPerWg = 96;
 // keys). Probability chunks: kE2Chunk keys. PV: enough workgroups to cover the chip (512 at nkv = 4)
 // with 16..512 keys each. Every array is sized
 // by a bound that grows monotonically with n, so a workspace sized for max_ctx fits every n <= max_ctx.
-// BKV_DECODE selects a decode implementation: "split" (four launches), "fused" (the older single
-// launch) or "resident" (the default). Read on every call, so tests can switch it.
+// BKV_DECODE forces a decode implementation where its plan fits: "split" (four launches),
+// "resident" or "stream" (single launches). Without it, q8_0 K + V plans that fit the stream kernel
+// take it, other single-launch plans the resident kernel, the rest the split path. Read on every
+// call, so tests can switch it.
 enum { kPathSplit = 0, kPathResident = 2, kPathStream = 3 };
 static int forced_path() {
   const char *e = std::getenv("BKV_DECODE");
@@ -620,8 +622,7 @@ int bkv_workspace_error(const bkv_cache_desc *d, void *workspace, size_t ws_byte
   if (result == BKV_ETIMEOUT) {
     // a call that gave up left its counters and tags mid-protocol: start the workspace afresh (this
     // also clears the error word), as bkv_workspace_init does
-    if (ws_bytes / sizeof(unsigned) > 0x7FFFFFFFull) return BKV_EINVAL;
-    if ((e = launch_workspace_init((unsigned *)workspace, (int)(ws_bytes / sizeof(unsigned)), stream)) != hipSuccess ||
+    if ((e = launch_workspace_init((unsigned *)workspace, ws_bytes / sizeof(unsigned), stream)) != hipSuccess ||
         (e = hipStreamSynchronize(stream)) != hipSuccess)
       return hip_fail(e);
   }
@@ -652,8 +653,7 @@ int bkv_workspace_init(const bkv_cache_desc *d, void *workspace, size_t ws_bytes
   if (ws_bytes < kSyncBytes) return BKV_EWORKSPACE;
   // the whole workspace: the sync words, and the tagged partials of the resident path (a tag is
   // the call generation, which starts at 1)
-  if (ws_bytes / sizeof(unsigned) > 0x7FFFFFFFull) return BKV_EINVAL;
-  return hip_fail(launch_workspace_init((unsigned *)workspace, (int)(ws_bytes / sizeof(unsigned)), stream));
+  return hip_fail(launch_workspace_init((unsigned *)workspace, ws_bytes / sizeof(unsigned), stream));
 }
 
 int bkv_kv_fill_synthetic(const bkv_cache_desc *d, hipStream_t stream) {

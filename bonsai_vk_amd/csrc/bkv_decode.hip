@@ -463,12 +463,12 @@ hipError_t launch_decode(const QkArgs &qa, const EArgs &ea, const PvArgs &pa, co
 
 // zero a workspace (bkv_workspace_init) and fill cache arrays (bkv_kv_fill_synthetic): kernels,
 // not memsets, so that the calls can sit inside a captured graph
-__global__ void workspace_init_kernel(unsigned *sync, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) sync[i] = 0u;
+__global__ void workspace_init_kernel(unsigned *sync, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) sync[i] = 0u;
 }
 
-hipError_t launch_workspace_init(unsigned *sync, int nwords, hipStream_t st) {
-  const int blocks = (int)std::min<long long>(1024, ((long long)nwords + 255) / 256);
+hipError_t launch_workspace_init(unsigned *sync, size_t nwords, hipStream_t st) {
+  const int blocks = (int)std::min<size_t>(1024, (nwords + 255) / 256);
   hipLaunchKernelGGL(workspace_init_kernel, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, st, sync, nwords);
   return hipGetLastError();
 }

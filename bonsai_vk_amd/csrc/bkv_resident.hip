@@ -21,6 +21,7 @@
 // Barriers count arrivals on per-group counters (two sets, alternating by call parity; each call
 // clears the set the next one uses). Every wait is bounded and records an error word on timeout.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -957,21 +958,22 @@ static int occupancy_of(K kernel, int dev) {
 // once per device
 template <int KF, int VF>
 static int resident_capacity() {
+  // per device, published once computed (value + 1; 0: not yet): threads that race here compute
+  // the same value
   constexpr int kMaxDev = 64;
-  static int cap[kMaxDev];
-  static bool done[kMaxDev];
+  static std::atomic<int> cached[kMaxDev];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-  if (!done[dev]) {
-    int c = std::min(occupancy_of(resident_kernel<KF, VF, false, false>, dev),
-                     occupancy_of(resident_kernel<KF, VF, false, true>, dev));
-    if constexpr (KF == BKV_Q8_0 && VF == BKV_Q8_0)
-      c = std::min({c, occupancy_of(resident_kernel<KF, VF, true, false>, dev),
-                     occupancy_of(resident_kernel<KF, VF, true, true>, dev)});
-    cap[dev] = c;
-    done[dev] = true;
-  }
-  return cap[dev];
+  const int known = cached[dev].load(std::memory_order_acquire);
+  if (known > 0) return known - 1;
+  int c = std::min(occupancy_of(resident_kernel<KF, VF, false, false>, dev),
+                   occupancy_of(resident_kernel<KF, VF, false, true>, dev));
+  if constexpr (KF == BKV_Q8_0 && VF == BKV_Q8_0)
+    c = std::min({c, occupancy_of(resident_kernel<KF, VF, true, false>, dev),
+                   occupancy_of(resident_kernel<KF, VF, true, true>, dev)});
+  c = std::max(c, 0);
+  cached[dev].store(c + 1, std::memory_order_release);
+  return c;
 }
 
 int resident_max_workgroups(int kf, int vf) {

@@ -36,7 +36,7 @@ static void *device_scratch(hipStream_t stream, hipError_t *err) {
     void *ptr = nullptr;
     *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (*err != hipSuccess) return nullptr;
-    *err = launch_workspace_init(static_cast<unsigned *>(ptr), (int)(kStaticScratchBytes / sizeof(unsigned)), stream);
+    *err = launch_workspace_init(static_cast<unsigned *>(ptr), kStaticScratchBytes / sizeof(unsigned), stream);
     if (*err != hipSuccess) return nullptr;
     g_scratch[dev] = ptr;
   }
@@ -65,6 +65,45 @@ int bkv_decode_step_static(const bkv_cache_desc *d, int layer, uint32_t pos, con
   void *ws = device_scratch(stream, &e);
   if (!ws) return hip_fail(e);
   return bkv_decode_step(d, layer, pos, k, v, q, gate, out, out_gated, ws, kStaticScratchBytes, stream);
+}
+
+int bkv_static_error(const bkv_cache_desc *d, hipStream_t stream) {
+  int rc = bkv_geom_check(d);
+  if (rc) return rc;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= kMaxDevices) return hip_fail(hipErrorInvalidDevice);
+  void *ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ws = g_scratch[dev];
+  }
+  if (!ws) return BKV_OK;                       // no static call has run on this device
+  // bkv_workspace_error on the array: it synchronises the stream, reads the error word and, when
+  // it is set, zeroes the whole array (the workspace of every later static call on this device)
+  return bkv_workspace_error(d, ws, kStaticScratchBytes, stream);
+}
+
+int bkv_static_debug_address(void **out) {
+  if (!out) return BKV_EINVAL;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= kMaxDevices) return hip_fail(hipErrorInvalidDevice);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  *out = g_scratch[dev];
+  return BKV_OK;
+}
+
+int bkv_static_reset(hipStream_t stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= kMaxDevices) return hip_fail(hipErrorInvalidDevice);
+  void *ws = device_scratch(stream, &e);
+  if (!ws) return hip_fail(e);
+  return hip_fail(launch_workspace_init(static_cast<unsigned *>(ws), kStaticScratchBytes / sizeof(unsigned), stream));
 }
 
 }  // extern "C"

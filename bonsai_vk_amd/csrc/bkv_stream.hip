@@ -24,6 +24,7 @@
 //  5. The workgroup's [4][256] partial goes out as tagged words, and workgroup i sums slice i of
 //     the group's partials in workgroup order (+ gate).
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 
 #include "bkv_exp.h"
@@ -1151,34 +1152,30 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 
 template <bool PG>
 static int stream_capacity() {
-  // every instantiation launch_stream may launch (full and short plans)
-  static int cap[64];
-  static bool done[64];
+  // every instantiation launch_stream may launch (full and short plans). Per device, published
+  // once computed (value + 1; 0: not yet): threads that race here compute the same value.
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!done[dev]) {
-    int per = 0;
-    hipDeviceProp_t pr;
-    if (hipGetDeviceProperties(&pr, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG, false>, kResNT, 0) != hipSuccess)
-      cap[dev] = 0;
-    else
-      cap[dev] = per * pr.multiProcessorCount;
-    int per2 = 0;
-    if (cap[dev] > 0 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per2, stream_kernel<PG, true>, kResNT, 0) == hipSuccess)
-      cap[dev] = std::min(cap[dev], per2 * pr.multiProcessorCount);
-    else
-      cap[dev] = 0;
-    done[dev] = true;
-  }
-  return cap[dev];
+  const int known = cached[dev].load(std::memory_order_acquire);
+  if (known > 0) return known - 1;
+  int cap = 0, per = 0, per2 = 0;
+  hipDeviceProp_t pr;
+  if (hipGetDeviceProperties(&pr, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG, false>, kResNT, 0) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per2, stream_kernel<PG, true>, kResNT, 0) == hipSuccess)
+    cap = std::min(per, per2) * pr.multiProcessorCount;
+  cached[dev].store(cap + 1, std::memory_order_release);
+  return cap;
 }
 
 int stream_max_workgroups(bool paged) { return paged ? stream_capacity<true>() : stream_capacity<false>(); }
 
-// A cooperative launch: the runtime refuses a grid whose workgroups cannot all be resident at once,
-// which every wait in the kernel relies on.
+// Every wait in the kernel relies on all workgroups being resident at once. The host sizes the grid
+// from the occupancy query (stream_capacity: one workgroup per CU) and launches it as an ordinary
+// kernel; a grid that is not co-resident (another kernel holding CUs) makes the bounded waits give
+// up and set the workspace's error word (bkv_workspace_error). BKV_COOP=1 launches cooperatively
+// instead, so that the runtime refuses such a grid up front, at about 18 us more per call.
 hipError_t launch_stream(const ResArgs &a, hipStream_t st) {
   const dim3 grid(a.G * a.nkv), block(kResNT);
   static const bool coop = [] { const char *e = std::getenv("BKV_COOP"); return e && e[0] == '1'; }();

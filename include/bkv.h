@@ -227,6 +227,22 @@ int bkv_decode_step_static(const bkv_cache_desc *d, int layer, uint32_t pos,
                            float *out, float *out_gated, hipStream_t stream);
 size_t bkv_static_scratch_bytes(void);
 
+/* bkv_workspace_error for the static array of bkv_decode_step_static (no counterpart in the
+ * reference; for the same callers): synchronises `stream`, returns BKV_ETIMEOUT if a static call
+ * on the current GPU gave up waiting (its output is not valid) and then zeroes the array, so that
+ * later static calls start from a clean workspace; BKV_OK otherwise (also when no static call has
+ * run on this GPU). d: any descriptor of the calls (its nkv places the error word). */
+int bkv_static_error(const bkv_cache_desc *d, hipStream_t stream);
+
+/* Zeroes the current GPU's static array on `stream` (no counterpart in the reference): what
+ * bkv_workspace_init is for a caller's workspace, e.g. after the decode path was switched with
+ * BKV_DECODE. Stream-ordered; no allocation. */
+int bkv_static_reset(hipStream_t stream);
+
+/* Diagnostics (no counterpart in the reference; for tests): the device address of the current
+ * GPU's static array in *out (NULL before the first static call or reset on this GPU). */
+int bkv_static_debug_address(void **out);
+
 /* Human-readable text of an enum bkv_err value (static storage). */
 const char *bkv_strerror(int err);
 

@@ -3,7 +3,8 @@ bonsai_vk_amd/csrc/bkv_prefill.hip) restated in C and checked against the correc
 quotient (float)((double)e / sum) (exact: a double-precision quotient rounded to fp32 is the
 correctly rounded fp32 quotient), which is what the reference's p16 = f16(e / sum) rounds
 (runtime_vk/attn_vk.h:190-200). The steps: q0 = e * rs with rs = fp32(1/sum), then twice
-q = q + fma(-sum, q, e) * rs. Inputs: sum in [1, 2^14) with random significands and 0 <= e <= sum
+q = q + fma(-sum, q, e) * rs. Inputs: sum in [1, 2^18) with random significands (a softmax sum
+reaches the key count: past 2^15 at 32K keys, 2^17 at the longest contexts the workspace takes) and 0 <= e <= sum
 (a softmax sum includes its maximum's e = 1), spread over every binade of e and over e close to sum,
 and sums whose significands are all ones or just above a power of two.
 Below 2^-26 the quotient rounds to an fp16 zero whatever its last bits, so only the fp16 value is
@@ -30,7 +31,7 @@ int main(int argc, char **argv) {
   const long n = atol(argv[1]);
   long bad = 0;
   for (long i = 0; i < n; ++i) {
-    const float s = u2f(0x3F800000u + (uint32_t)(rnd() % (14u << 23)));
+    const float s = u2f(0x3F800000u + (uint32_t)(rnd() % (18u << 23)));
     const uint64_t r = rnd();
     float e;
     switch (r & 3) {
@@ -47,7 +48,7 @@ int main(int argc, char **argv) {
   }
   /* sums whose significands are all ones or just above a power of two (1/sum closest to a rounding
      boundary), against every 9973rd float of e in [2^-31, min(1, sum)] */
-  for (int k = 0; k < 14; ++k)
+  for (int k = 0; k < 18; ++k)
     for (uint32_t m = 0; m < 16; ++m) {
       const float s = u2f(((127u + k) << 23) | (m < 8 ? 0x7FFFFFu - m : m - 8));
       for (uint32_t eb = 0x30000000u; eb <= 0x3F800000u && u2f(eb) <= s; eb += 9973) {

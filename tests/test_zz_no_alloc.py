@@ -70,3 +70,47 @@ def test_static_rejects_oversize():
     assert rc == -9                                    # BKV_ESCRATCH, nothing launched
     torch.cuda.synchronize()
     assert int(c.k_data.count_nonzero()) == 0          # the cache was not written
+
+
+def _hip():
+    h = ctypes.CDLL("libamdhip64.so")
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return h
+
+
+def test_static_error_word_and_reset():
+    """bkv_static_error: clean after ordinary static calls. A timed-out static call is imitated from
+    the host (the array's error word set): the check reports BKV_ETIMEOUT and zeroes the array, the
+    next check is clean, and static calls after it (and after bkv_static_reset) equal the workspace
+    entry point bit for bit."""
+    n = 3000
+    a, b = _filled(n, BKV_Q8_0, BKV_Q8_0, 60), _filled(n, BKV_Q8_0, BKV_Q8_0, 60)
+    gen = torch.Generator(device="cuda").manual_seed(61)
+    k, v, q, g = (torch.randn(s, generator=gen, device="cuda") for s in [(4, 256), (4, 256), (16, 256), (16, 256)])
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    d = ctypes.byref(b.desc)
+    _step(a, n, k, v, q, g, static=False)
+    _step(b, n, k, v, q, g, static=True)
+    assert lib().bkv_static_error(d, st) == 0
+    addr = ctypes.c_void_p()
+    check(lib().bkv_static_debug_address(ctypes.byref(addr)), "address")
+    assert addr.value
+    off = (ctypes.c_uint64 * 1)()
+    check(lib().bkv_error_words(d, off), "error word")
+    hip = _hip()
+    one = ctypes.c_uint32(1)
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(addr.value + off[0], ctypes.byref(one), 4, 1) == 0      # host to device
+    assert lib().bkv_static_error(d, st) == -8                                   # BKV_ETIMEOUT
+    head = np.zeros(1 << 16, np.uint32)
+    assert hip.hipMemcpy(head.ctypes.data, addr.value, head.nbytes, 2) == 0      # device to host
+    assert int(np.count_nonzero(head)) == 0                                      # zeroed
+    assert lib().bkv_static_error(d, st) == 0
+    for reset in (False, True):
+        if reset:
+            check(lib().bkv_static_reset(st), "reset")
+        pos = n + 1 + int(reset)
+        want = _step(a, pos, k, v, q, g, static=False)
+        got = _step(b, pos, k, v, q, g, static=True)
+        for w, x in zip(want, got):
+            assert torch.equal(w.view(torch.int32), x.view(torch.int32))
