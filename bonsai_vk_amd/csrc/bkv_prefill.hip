@@ -576,8 +576,8 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     // queries' 4 q rows in LDS, their A operands in registers. A wave scores its 64 keys of a tile
     // as 4 key groups x 4 queries (one MFMA per block each) and transposes each key group's 4
     // queries so that lane l holds rows 4(l/16) + k: query l/16, heads 0..3. Each key group's K
-    // bytes are requested two key groups ahead (the rows come from HBM the first time any
-    // workgroup of the XCD reads them; the workgroups run nearly in step).
+    // bytes are requested a whole tile ahead (the rows come from HBM the first time any workgroup
+    // of the XCD reads them; the workgroups run nearly in step).
     int8_t *s_lim = reinterpret_cast<int8_t *>(s_big);                    // [query][kLimBytes]
     int *s_lt = reinterpret_cast<int *>(s_big + kPxQ * kLimBytes);        // [query][head][block]
     static_assert(kPxQ * (kLimBytes + kGqa * 8 * 4) <= sizeof(s_big), "digits in the big LDS area");
@@ -594,6 +594,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     __syncthreads();
     const bool wide = s_wide != 0u;
     long qa[kPxQ][8];
+    uint32_t qt[kPxQ][2];                      // the exponents of head l/16, packed as signed bytes
     {
       Q8Lim t;
 #pragma unroll
@@ -601,66 +602,90 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
         q8lim_load(s_lim + jq * kLimBytes, s_lt + jq * kGqa * 8, t);
 #pragma unroll
         for (int b = 0; b < 8; ++b) qa[jq][b] = t.a[b];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          qt[jq][i] = (uint32_t)(t.t[4 * i] & 0xFF) | ((uint32_t)(t.t[4 * i + 1] & 0xFF) << 8) |
+                      ((uint32_t)(t.t[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(t.t[4 * i + 3] & 0xFF) << 24);
       }
     }
     const int ql = lane >> 4, n16 = lane & 15;
     const bool qlive = ql < nqv;
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     constexpr int RB = row_bytes(BKV_Q8_0);
-    struct KG { long b[8]; uint4 s; };        // one key group's B operands and the lane key's scales
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    struct KG { long b[8]; u32x4 s; };        // one key group's B operands and the lane key's scales
+    // The loads are issued as inline asm, so that they stay where they are written (the compiler
+    // would sink them to the end of the tile) and its wait counting leaves them alone: kg_wait<N>
+    // waits until at most N vector memory operations issued after them are in flight, and names
+    // the registers, so no read of them moves above it.
     auto load_kg = [&](uint32_t key0, int kg, KG &r) {
       const uint32_t key = min(key0 + (uint32_t)(16 * kg + n16), kend - 1);
       const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
       const uint8_t *src = a.L.kd + ro * RB + 8 * ql;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) r.b[b] = *reinterpret_cast<const long *>(src + 32 * b);
-      r.s = *reinterpret_cast<const uint4 *>(a.L.ks + ro * kScaleRowBytes);
+      const uint8_t *sp = a.L.ks + ro * kScaleRowBytes;
+#define BKV_LD2(i) asm volatile("global_load_dwordx2 %0, %1, off offset:" #i "*32" : "=v"(r.b[i]) : "v"(src) : "memory")
+      BKV_LD2(0); BKV_LD2(1); BKV_LD2(2); BKV_LD2(3); BKV_LD2(4); BKV_LD2(5); BKV_LD2(6); BKV_LD2(7);
+#undef BKV_LD2
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r.s) : "v"(sp) : "memory");
     };
-    KG kn[2];
+    // the scores of key group kg of the tile at key0 (r[k]: row 4(l/16) + k), scaled and masked,
+    // into the scratch and the row maxima
+    auto emit = [&](uint32_t key0, int kg, const float (&r)[4]) {
+      const uint32_t j = key0 + (uint32_t)(16 * kg + n16);
+      const bool live = qlive && (int)j <= lim0 + ql;
+      float v[4];
 #pragma unroll
-    for (int kg = 0; kg < 2; ++kg) load_kg((uint32_t)((ntile - 1) * kPxTile + 64 * w), kg, kn[kg]);
-    for (int t = ntile - 1; t >= 0; --t) {
-      const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
-      const uint32_t nkey0 = (uint32_t)(max(t - 1, 0) * kPxTile + 64 * w);
-      float acc[4][4];
+      for (int k = 0; k < 4; ++k) {
+        v[k] = live ? r[k] * a.scale : -INFINITY;
+        mx[k] = v[k] > mx[k] ? v[k] : mx[k];
+      }
+      st_sc4(sc + (size_t)j * kPxRows + 4 * ql, make_float4(v[0], v[1], v[2], v[3]));
+    };
+    if (!wide) {
+      // a whole tile ahead. When key group kg is used, what was issued after its loads is the store
+      // that followed them, the 3 later key groups' loads (9 each) and their stores: 31 operations
+      // (27 to 30 in the first tile, whose loads went out back to back), so 27 are left in flight.
+      KG kn[4];
+      auto kg_wait = [](KG &r) {
+        asm volatile("s_waitcnt vmcnt(27)"
+                     : "+v"(r.b[0]), "+v"(r.b[1]), "+v"(r.b[2]), "+v"(r.b[3]), "+v"(r.b[4]), "+v"(r.b[5]),
+                       "+v"(r.b[6]), "+v"(r.b[7]), "+v"(r.s)::"memory");
+      };
 #pragma unroll
-      for (int kg = 0; kg < 4; ++kg) {
-        const KG cur = kn[kg & 1];
-        __builtin_amdgcn_sched_barrier(0);
-        load_kg(kg < 2 ? key0 : nkey0, (kg + 2) & 3, kn[kg & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (!wide) {
+      for (int kg = 0; kg < 4; ++kg) load_kg((uint32_t)((ntile - 1) * kPxTile + 64 * w), kg, kn[kg]);
+      for (int t = ntile - 1; t >= 0; --t) {
+        const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
+#pragma unroll
+        for (int kg = 0; kg < 4; ++kg) {
+          KG &cur = kn[kg];
+          kg_wait(cur);
           float r[4];
+          const uint4 scl = make_uint4(cur.s.x, cur.s.y, cur.s.z, cur.s.w);
 #pragma unroll
-          for (int jq = 0; jq < kPxQ; ++jq) {
-            int tt[8];
-            const int4 t0 = *reinterpret_cast<const int4 *>(s_lt + (jq * kGqa + ql) * 8);
-            const int4 t1 = *reinterpret_cast<const int4 *>(s_lt + (jq * kGqa + ql) * 8 + 4);
-            tt[0] = t0.x; tt[1] = t0.y; tt[2] = t0.z; tt[3] = t0.w;
-            tt[4] = t1.x; tt[5] = t1.y; tt[6] = t1.z; tt[7] = t1.w;
-            r[jq] = q8_score16r(cur.b, cur.s, qa[jq], tt);
-          }
+          for (int jq = 0; jq < kPxQ; ++jq) r[jq] = q8_score16p(cur.b, scl, qa[jq], qt[jq]);
+          load_kg((uint32_t)(max(t - 1, 0) * kPxTile + 64 * w), kg, cur);
           transpose_rows4(r);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) acc[kg][k] = r[k];
-        } else {                               // lane: key 16 kg + l%16 against query l/16's 4 heads
-          const uint32_t key = min(key0 + (uint32_t)(16 * kg + n16), kend - 1);
-          const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
-          q8_score_key_slow(reinterpret_cast<const uint32_t *>(a.L.kd + ro * RB),
-                            reinterpret_cast<const uint32_t *>(a.L.ks + ro * kScaleRowBytes), qrows(ql), a.qs, acc[kg]);
+          emit(key0, kg, r);
         }
       }
+      // every load has landed before its registers are free again
 #pragma unroll
-      for (int kg = 0; kg < 4; ++kg) {
-        const uint32_t j = key0 + (uint32_t)(16 * kg + (lane & 15));
-        const bool live = qlive && (int)j <= lim0 + ql;
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          v[k] = live ? acc[kg][k] * a.scale : -INFINITY;
-          mx[k] = v[k] > mx[k] ? v[k] : mx[k];
+      for (int kg = 0; kg < 4; ++kg)
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(kn[kg].b[0]), "+v"(kn[kg].b[1]), "+v"(kn[kg].b[2]), "+v"(kn[kg].b[3]), "+v"(kn[kg].b[4]),
+                       "+v"(kn[kg].b[5]), "+v"(kn[kg].b[6]), "+v"(kn[kg].b[7]), "+v"(kn[kg].s)::"memory");
+    } else {
+      // the wide path: lane = key 16 kg + l%16 against query l/16's 4 heads, fp64 inner sums
+      for (int t = ntile - 1; t >= 0; --t) {
+        const uint32_t key0 = (uint32_t)(t * kPxTile + 64 * w);
+        for (int kg = 0; kg < 4; ++kg) {
+          const uint32_t key = min(key0 + (uint32_t)(16 * kg + n16), kend - 1);
+          const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+          float r[4];
+          q8_score_key_slow(reinterpret_cast<const uint32_t *>(a.L.kd + ro * RB),
+                            reinterpret_cast<const uint32_t *>(a.L.ks + ro * kScaleRowBytes), qrows(ql), a.qs, r);
+          emit(key0, kg, r);
         }
-        st_sc4(sc + (size_t)j * kPxRows + 4 * ql, make_float4(v[0], v[1], v[2], v[3]));
       }
     }
 #pragma unroll

@@ -117,6 +117,15 @@ __device__ __forceinline__ float q8_score16r(const long (&bv)[8], const uint4 &s
   return acc;
 }
 
+// The same with the exponents packed as signed bytes: t[b] is byte b % 4 of tp[b / 4].
+__device__ __forceinline__ float q8_score16p(const long (&bv)[8], const uint4 &scl, const long (&a)[8],
+                                             const uint32_t (&tp)[2]) {
+  int t[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) t[b] = __builtin_amdgcn_sbfe((int)tp[b >> 2], 8 * (b & 3), 8);
+  return q8_score16r(bv, scl, a, t);
+}
+
 // Scores of 16 keys: row is the LDS row (16 data uint4, then the scale uint4) of key lane % 16;
 // lane l receives the score of key l % 16 against head l / 16.
 __device__ __forceinline__ float q8_score16(const uint4 *row, const Q8Lim &L) {
