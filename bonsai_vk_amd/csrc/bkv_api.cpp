@@ -84,12 +84,15 @@ PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q, size_t base) {
 }
 
 // the exact prefill's workspace for chunks ending at or before max_ctx: per workgroup of one slice,
-// the [keys][rows] score / exp scratch
+// the [keys][rows] score / exp scratch; then (q8_0 V) the slice's sums and the PV kernel's partials
+static size_t prefill_exact_extra(int nh, int nkv) {
+  const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
+  return align256(wgs * kPxRows * sizeof(float)) + align256((size_t)2 * kPxSlice * nh * kHd * sizeof(float));
+}
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base) {
-  (void)nh;
   const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile + kPxTile;   // + the exp sweep's overhang
   const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
-  return base + align256(wgs * (size_t)ld * kPxRows * sizeof(float));
+  return base + align256(wgs * (size_t)ld * kPxRows * sizeof(float)) + prefill_exact_extra(nh, nkv);
 }
 
 // the largest plan_prefill(...).total over every chunk length and start position
@@ -487,6 +490,11 @@ static int prefill_common(const bkv_cache_desc *d, int layer, uint32_t pos0, int
     a.qs = qs;
     a.gs = gs;
     a.sc = (float *)(w + base);
+    {
+      const size_t scb = align256((size_t)d->nkv * (kPxSlice / kPxQ) * (size_t)ld * kPxRows * sizeof(float));
+      a.sums = (float *)(w + base + scb);
+      a.part = (float *)(w + base + scb + align256((size_t)d->nkv * (kPxSlice / kPxQ) * kPxRows * sizeof(float)));
+    }
     a.gate = gate;
     a.out = out;
     a.out_gated = out_gated;

@@ -180,6 +180,8 @@ struct PrefillXArgs {
   int qs, gs;
   float *out, *out_gated;
   float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp (the slice's workgroups)
+  float *sums;                   // q8_0 V: [nkv * nqb][kPxRows] the exact serial sums, for the PV kernel
+  float *part;                   // q8_0 V: [2][kPxSlice][nh][hd] the PV kernel's half-key partials
   unsigned *ts;                  // sweep timestamps (experiment builds), or null
 };
 hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st);

@@ -878,115 +878,10 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   PXTS(2);
   // ---------------------------------------------------------------- sweep 3: p16 and PV
   if constexpr (VF) {
-    // q8_0 V straight from memory into the A operand (no LDS tile): out^T = V^T . P^T on
-    // v_mfma_f32_16x16x32_f16, wave w owning dims 64 w .. + 63. Lane l supplies row i = l%16 of
-    // dimension tile mt as dim 64 w + 4 i + mt, and keys 8(l/16) .. + 7 of each 32-key half, so one
-    // 4-byte load per key brings the lane's bytes of all four dimension tiles; a byte transpose in
-    // registers and the exact fp16 split of d*b (hi = f16(d*b), lo = d*b - hi) form the operands.
-    // P^T (p16 = f16(e / sum), all 16 rows) goes through a double-buffered LDS tile.
-    const int lr = lane & 15, lq = lane >> 4;
-    char *s_p = s_big;                                              // [2][kPxRows][kPfRS]
-    f4 o[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) o[mt] = f4{0.f, 0.f, 0.f, 0.f};
-    const int nt64 = (int)((kend + kPfTile - 1) / kPfTile);
-    const int pk = tid >> 2, pr0 = PR * (tid & 3);   // this thread's probabilities: key pk, rows pr0..+PR
-    float ssum[PR], srcp[PR];
-#pragma unroll
-    for (int i = 0; i < PR; ++i) {
-      ssum[i] = s_sum[pr0 + i];
-      srcp[i] = 1.0f / ssum[i];
-    }
-    const int dcol = 64 * w + 4 * lr;                 // the lane's 4 dims
-    const int sblk = dcol >> 5;                       // their q8_0 block
-    struct PvIn {
-      float4 en;                                      // e of key pk, rows pr0 .. + 3
-      uint32_t vw[16], vs[16];                        // [ks * 8 + c]: key 32 ks + 8 lq + c of the tile
-    };
-    auto load_tile = [&](int t, PvIn &in) {
-      in.en = ld_sc4(sc + ((size_t)t * kPfTile + pk) * kPxRows + pr0);
-#pragma unroll
-      for (int kc = 0; kc < 16; ++kc) {
-        const uint32_t key = min((uint32_t)(t * kPfTile + 32 * (kc >> 3) + 8 * lq + (kc & 7)), kend - 1);
-        const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
-        in.vw[kc] = *reinterpret_cast<const uint32_t *>(a.L.vd + ro * kHd + dcol);
-        in.vs[kc] = *reinterpret_cast<const uint16_t *>(a.L.vs + ro * kScaleRowBytes + 2 * sblk);
-      }
-    };
-    auto tile = [&](int t, const PvIn &in) {
-      char *pb = s_p + (t & 1) * kPxRows * kPfRS;
-      const float ev[PR] = {in.en.x, in.en.y, in.en.z, in.en.w};
-#pragma unroll
-      for (int i = 0; i < PR; ++i) {
-        const _Float16 h = (_Float16)div_by_sum(ev[i], ssum[i], srcp[i]);
-        *reinterpret_cast<_Float16 *>(pb + (pr0 + i) * kPfRS + 2 * pk) = h;
-      }
-      // the A operands (registers only): pair p of key half ks holds keys 2p, 2p+1
-      h8 ah[2][4], al[2][4];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          constexpr uint32_t kSel[4] = {0x0C040C00u, 0x0C050C01u, 0x0C060C02u, 0x0C070C03u};
-          uint32_t hw[4], lw[4];
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t bw = __builtin_amdgcn_perm(in.vw[8 * ks + 2 * pp + 1], in.vw[8 * ks + 2 * pp], kSel[mt]) ^ 0x64806480u;
-            const h2 x = as_h2(bw) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
-            h2 hi, lo;
-            split_prod(x, as_h2(in.vs[8 * ks + 2 * pp] | (in.vs[8 * ks + 2 * pp + 1] << 16)), hi, lo);
-            hw[pp] = as_u(hi);
-            lw[pp] = as_u(lo);
-          }
-          ah[ks][mt] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-          al[ks][mt] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-        }
-      }
-      lds_barrier();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const h8 bp = *reinterpret_cast<const h8 *>(pb + lr * kPfRS + 2 * (32 * ks + 8 * lq));
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          o[mt] = mfma16(ah[ks][mt], bp, o[mt]);
-          o[mt] = mfma16(al[ks][mt], bp, o[mt]);
-        }
-      }
-    };
-    // tiles in descending key order (the PV sum's order is free), the last-written exp values
-    // first; two register sets, each tile's operands requested one tile ahead
-    PvIn ia, ib;
-    load_tile(nt64 - 1, ia);
-    for (int t = nt64 - 1; t >= 0; t -= 2) {
-      if (t >= 1) load_tile(t - 1, ib);
-      __builtin_amdgcn_sched_barrier(0);
-      tile(t, ia);
-      if (t < 1) break;
-      if (t >= 2) load_tile(t - 2, ia);
-      __builtin_amdgcn_sched_barrier(0);
-      tile(t - 1, ib);
-    }
-    PXTS(3);
-    // lane l holds out^T[dim 64 w + 4 m + mt][row l%16] in o[mt][r], m = 4(l/16) + r
-    const int r = lr;
-    if ((r >> 2) < nqv) {
-      const size_t row = (size_t)(q0 + (r >> 2)) * a.nh + g * kGqa + (r & 3);
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int d = 64 * w + 4 * (4 * lq + rr);
-        const float4 v = make_float4(o[0][rr], o[1][rr], o[2][rr], o[3][rr]);
-        *reinterpret_cast<float4 *>(a.out + row * kHd + d) = v;
-        if (a.gate) {
-          const float4 gt = *reinterpret_cast<const float4 *>(a.gate + row * a.gs + d);
-          float4 og;
-          og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
-          og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
-          og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
-          og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
-          *reinterpret_cast<float4 *>(a.out_gated + row * kHd + d) = og;
-        }
-      }
-    }
+    // q8_0 V: the exact sums go out, and prefill_pv64_kernel forms p16 and the PV for 64 rows at a
+    // time (each V byte converted once per 64 rows instead of per 16)
+    if (tid < kPxRows) a.sums[(size_t)wi * kPxRows + tid] = s_sum[tid];
+    return;
   } else {
   const int lr = lane & 15, lq = lane >> 4, kp = lane & 31, vh = lane >> 5;
   char *s_p = s_big;                                              // [2][kPxRows][kPfRS]
@@ -1077,6 +972,180 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- the exact prefill's PV, q8_0 V
+// 16 queries (64 rows: query i, head h at row 4 i + h) of one KV group over one half of their key
+// tiles: p16 = f16(e / sum) from the exact kernel's e scratch and sums (the reference's P16,
+// attn_vk.h:190-200), out^T = V^T . P^T on v_mfma_f32_16x16x32_f16, wave w of 8 owning dims
+// 32 w .. + 31 (one q8_0 block). Lane l supplies A row i = l%16 of dimension tile mt as dim
+// 32 w + 2 i + mt, and keys 8(l/16) .. + 7 of each 32-key half, so one 2-byte load per key brings the
+// lane's bytes of both dimension tiles; a byte transpose in registers and the exact fp16 split of d*b
+// (hi = f16(d*b), lo = d*b - hi) form the operands, shared by the 64 rows. The two halves' partials
+// are added in a fixed order by prefill_pv_merge_kernel.
+template <bool PG>
+__global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
+  constexpr int R = 4 * kPxRows;                   // 64 rows, 4 exact-kernel workgroups' worth
+  constexpr int NTR = R / 16;                      // MFMA row tiles
+  const int n = gridDim.x, b = blockIdx.x;
+  const int nq16 = (a.n_q + 15) / 16;
+  const int wb = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
+  const int qb = wb % nq16, half = (wb / nq16) & 1, g = wb / (2 * nq16);
+  const int q0 = a.q_base + 16 * qb;               // chunk index of the first query
+  const int nqv = min(16, a.q_base + a.n_q - q0);
+  const uint32_t kend = a.pos0 + (uint32_t)(q0 + nqv);
+  const int ntl = (int)((kend + kPfTile - 1) / kPfTile);
+  const int t0 = half ? ntl / 2 : 0, t1 = half ? ntl : ntl / 2;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lq = lane >> 4;
+  __shared__ __attribute__((aligned(16))) char s_p[2][R * kPfRS];   // P tiles [row][64 keys] fp16
+  // this thread's probabilities: key pk of a tile, rows 8 w .. + 7 (of exact-kernel workgroup xq,
+  // whose scratch holds their e up to its own last key kx); the wave's sums in scalar registers
+  const int pk = lane;
+  const int xq = min(4 * qb + (w >> 1), a.nqb - 1);
+  const bool pv = 16 * qb + 4 * (w >> 1) < a.n_q;
+  const uint32_t kx = a.pos0 + (uint32_t)min(a.q_base + 4 * (4 * qb + (w >> 1)) + kPxQ, a.q_base + a.n_q);
+  const size_t xw = (size_t)g * a.nqb + xq;
+  const float *esrc = a.sc + xw * a.ld * kPxRows + 8 * (w & 1);
+  float ssum[8], srcp[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ssum[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                            __builtin_bit_cast(int, a.sums[xw * kPxRows + 8 * (w & 1) + i])));
+    srcp[i] = 1.0f / ssum[i];
+  }
+  f4 o[2][NTR];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTR; ++nt) o[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+  const int dcol = 32 * w + 2 * lr;                 // the lane's 2 dims (q8_0 block w)
+  // (the loaded values are kept raw until the tile uses them: any arithmetic on them here would
+  // make the wave wait for the loads at once)
+  struct PvIn {
+    float4 en[2];                                   // e of key pk, the thread's 8 rows (valid if live)
+    bool live;
+    uint32_t vw[16];                                // [ks * 8 + c]: key 32 ks + 8 lq + c of the tile (2 bytes)
+    uint32_t vs;                                    // the block scale of key 32 (l%16 / 8) + 8 lq + l%8
+  };
+  // tiles past t1 (the loop runs whole groups of three) load tile t1 - 1 again and add nothing
+  auto load_tile = [&](int tt, PvIn &in) {
+    const int t = min(tt, t1 - 1);
+    const uint32_t j = (uint32_t)(t * kPfTile + pk);
+    const float *src = esrc + (size_t)min(j, kx - 1) * kPxRows;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) in.en[i] = ld_sc4(src + 4 * i);
+    in.live = pv && j < kx && tt < t1;
+#pragma unroll
+    for (int kc = 0; kc < 16; ++kc) {
+      const uint32_t key = min((uint32_t)(t * kPfTile + 32 * (kc >> 3) + 8 * lq + (kc & 7)), kend - 1);
+      const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
+      in.vw[kc] = *reinterpret_cast<const uint16_t *>(a.L.vd + ro * kHd + dcol);
+    }
+    // one scale load per lane: lane l%16 of each 16-lane row loads key (l%16 / 8, l%8)'s, and the row
+    // shares them by DPP broadcasts in the tile (fewer loads in flight: the wait counter holds 63)
+    const uint32_t skey = min((uint32_t)(t * kPfTile + 32 * (lr >> 3) + 8 * lq + (lr & 7)), kend - 1);
+    in.vs = *reinterpret_cast<const uint16_t *>(a.L.vs + (slot_t<PG>(a.L, skey) * a.nkv + g) * kScaleRowBytes + 2 * w);
+  };
+  auto tile = [&](int t, const PvIn &in) {
+    char *pb = s_p[t & 1];
+    const float ev[8] = {in.en[0].x, in.en[0].y, in.en[0].z, in.en[0].w, in.en[1].x, in.en[1].y, in.en[1].z, in.en[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const _Float16 h = (_Float16)div_by_sum(in.live ? ev[i] : 0.0f, ssum[i], srcp[i]);
+      *reinterpret_cast<_Float16 *>(pb + (8 * w + i) * kPfRS + 2 * pk) = h;
+    }
+    // the block scales of the lane's 16 keys: key (ks, c) from lane 8 ks + c of its row
+    uint32_t vsk[16];
+#define BKV_BC(i) vsk[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)in.vs, 0x150 + (i), 0xF, 0xF, false)
+    BKV_BC(0); BKV_BC(1); BKV_BC(2); BKV_BC(3); BKV_BC(4); BKV_BC(5); BKV_BC(6); BKV_BC(7);
+    BKV_BC(8); BKV_BC(9); BKV_BC(10); BKV_BC(11); BKV_BC(12); BKV_BC(13); BKV_BC(14); BKV_BC(15);
+#undef BKV_BC
+    // the A operands (registers only): pair p of key half ks holds keys 2p, 2p+1
+    h8 ah[2][2], al[2][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        constexpr uint32_t kSel[2] = {0x0C040C00u, 0x0C050C01u};
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t bw = __builtin_amdgcn_perm(in.vw[8 * ks + 2 * pp + 1], in.vw[8 * ks + 2 * pp], kSel[mt]) ^ 0x64806480u;
+          const h2 x = as_h2(bw) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+          h2 hi, lo;
+          split_prod(x, as_h2(vsk[8 * ks + 2 * pp] | (vsk[8 * ks + 2 * pp + 1] << 16)), hi, lo);
+          hw[pp] = as_u(hi);
+          lw[pp] = as_u(lo);
+        }
+        ah[ks][mt] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+        al[ks][mt] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+      }
+    }
+    lds_barrier();                                  // the P tile (the other buffer's readers are done)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int nt = 0; nt < NTR; ++nt) {
+        const h8 bp = *reinterpret_cast<const h8 *>(pb + (16 * nt + lr) * kPfRS + 2 * (32 * ks + 8 * lq));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          o[mt][nt] = mfma16(ah[ks][mt], bp, o[mt][nt]);
+          o[mt][nt] = mfma16(al[ks][mt], bp, o[mt][nt]);
+        }
+      }
+    }
+  };
+  // three register sets, each tile's operands requested two tiles ahead (branch-free groups of
+  // three, so that the compiler's wait counting keeps the two younger tiles' loads in flight)
+  if (t0 < t1) {
+    PvIn in[3];
+    load_tile(t0, in[0]);
+    load_tile(t0 + 1, in[1]);
+    for (int t = t0; t < t1; t += 3) {
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        load_tile(t + u + 2, in[(u + 2) % 3]);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(t + u, in[u]);
+      }
+    }
+  }
+  // lane l holds out^T[dim 32 w + 2 m + mt][row 16 nt + l%16] in o[mt][nt][r], m = 4(l/16) + r
+  float *part = a.part + (size_t)half * kPxSlice * a.nh * kHd;
+#pragma unroll
+  for (int nt = 0; nt < NTR; ++nt) {
+    const int r = 16 * nt + lr;
+    if ((r >> 2) >= nqv) continue;
+    const size_t row = (size_t)(q0 - a.q_base + (r >> 2)) * a.nh + g * kGqa + (r & 3);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int d = 32 * w + 2 * (4 * lq + rr);
+      *reinterpret_cast<float2 *>(part + row * kHd + d) = make_float2(o[0][nt][rr], o[1][nt][rr]);
+    }
+  }
+}
+
+// out = partial of the first key half + partial of the second (in that order), and the gate
+__global__ __launch_bounds__(256) void prefill_pv_merge_kernel(PrefillXArgs a) {
+  const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 *p0 = reinterpret_cast<const float4 *>(a.part);
+  const float4 *p1 = reinterpret_cast<const float4 *>(a.part + (size_t)kPxSlice * a.nh * kHd);
+  const float4 x = p0[i], y = p1[i];
+  const float4 v = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+  const size_t row = i / (kHd / 4), d = 4 * (i % (kHd / 4));
+  const size_t grow = (size_t)a.q_base * a.nh + row;             // row of the whole chunk
+  *reinterpret_cast<float4 *>(a.out + grow * kHd + d) = v;
+  if (a.gate) {
+    const float4 gt = *reinterpret_cast<const float4 *>(a.gate + grow * a.gs + d);
+    float4 og;
+    og.x = v.x * (1.0f / (1.0f + exp_cr(-gt.x)));
+    og.y = v.y * (1.0f / (1.0f + exp_cr(-gt.y)));
+    og.z = v.z * (1.0f / (1.0f + exp_cr(-gt.z)));
+    og.w = v.w * (1.0f / (1.0f + exp_cr(-gt.w)));
+    *reinterpret_cast<float4 *>(a.out_gated + grow * kHd + d) = og;
+  }
+}
+
 hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st) {
   const int grid = a.nkv * a.nqb;
   const bool pg = a.L.page != 0;
@@ -1084,6 +1153,13 @@ hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream
     if (pg) hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, true>), dim3(grid), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, false>), dim3(grid), dim3(256), 0, st, a);
   });
+  if (vf == BKV_Q8_0) {
+    const int pgrid = a.nkv * 2 * ((a.n_q + 15) / 16);
+    if (pg) hipLaunchKernelGGL(prefill_pv64_kernel<true>, dim3(pgrid), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL(prefill_pv64_kernel<false>, dim3(pgrid), dim3(512), 0, st, a);
+    const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
+    hipLaunchKernelGGL(prefill_pv_merge_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 

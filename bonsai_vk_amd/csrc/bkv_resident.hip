@@ -88,22 +88,6 @@ struct VSlots<0> {
                                              float (&)[kGqa][16]) {}
 };
 
-// fp16 K, half row CH (dims 128*CH .. 128*CH+127): acc = acc + q16_d * k_d in ascending d, exact
-// products (attn_vk.h:156-170)
-template <int CH>
-__device__ __forceinline__ void qk_f16_half(const uint4 *row, const float (&qv)[kGqa][kHd / 16],
-                                            float (&acc)[kGqa]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
-    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) Dot16<16>::run(acc[h], qv[h][CH * 8 + j], x);
-  }
-}
 
 // no lane of the wave needs is skipped.
 template <bool DELTA>
