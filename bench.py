@@ -173,7 +173,7 @@ def launched_kernel(cache, n):
         # workgroups of at most 128 keys run the short instantiation
         wgs = min(64, -(-n // 96))
         short = -(-n // wgs) <= 128
-        return f"void bkv::stream_kernel<false, {'true' if short else 'false'}>(bkv::ResArgs)"
+        return f"void bkv::stream_kernel<1, false, {'true' if short else 'false'}>(bkv::ResArgs)"
     if path == 2:
         return "void bkv::resident_kernel<1, 1, true, false>(bkv::ResArgs)"
     return None

@@ -149,7 +149,9 @@ DecodePlan plan_decode(int nh, int nkv, int kfmt, int vfmt, int64_t n, int page)
       p.rkpw = (int)kpw;
       p.rG = (int)cdiv(n, kpw);
       p.rvres = vfmt == BKV_Q8_0 && kfmt == BKV_Q8_0 && kpw <= kResNT + kResTail;
-      p.rstream = p.rvres && p.rG * nkv <= stream_max_workgroups(page > 0);
+      // the stream kernel: q8_0 V with q8_0 or fp16 K, one pass plus a tail per workgroup
+      p.rstream = vfmt == BKV_Q8_0 && (kfmt == BKV_Q8_0 || kfmt == BKV_F16) && kpw <= kResNT + kResTail &&
+                  p.rG * nkv <= stream_max_workgroups(page > 0);
       p.r_part = kSyncBytes;
       size_t f = kSyncBytes + tagged_part;
       p.r_spec = f;   f += align256((size_t)nh * gmax * kMaxSpecial * sizeof(Special));
@@ -298,7 +300,7 @@ static int decode_common(const bkv_cache_desc *d, int layer, uint32_t nfill, con
     ra.ts = (unsigned *)w + 32768;
     ra.tsw = (unsigned *)(w + p.ts_off);
 #endif
-    if (path == kPathStream) return hip_fail(launch_stream(ra, st));
+    if (path == kPathStream) return hip_fail(launch_stream(ra, d->k_fmt, st));
     return hip_fail(launch_resident(ra, d->k_fmt, d->v_fmt, p.rvres, st));
   }
 

@@ -226,7 +226,7 @@ int qk_keys_per_wg(int kfmt);
 int resident_max_workgroups(int kf, int vf);
 hipError_t launch_resident(const ResArgs &a, int kf, int vf, bool vres, hipStream_t st);
 int stream_max_workgroups(bool paged);
-hipError_t launch_stream(const ResArgs &a, hipStream_t st);
+hipError_t launch_stream(const ResArgs &a, int kf, hipStream_t st);
 hipError_t launch_workspace_init(unsigned *sync, size_t nwords, hipStream_t st);
 // records a HIP error for bkv_last_hip_error and maps it to BKV_EHIP (BKV_OK for hipSuccess)
 int hip_fail(hipError_t e);

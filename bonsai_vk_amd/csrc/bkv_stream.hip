@@ -66,8 +66,21 @@ __device__ __forceinline__ void stage_tail(uint4 *tt, const SlotMap &sm, int nkv
 // s = 0..15 of each 32-lane half own elements 16 s .. 16 s + 15 (lanes 0..31: K, 32..63: V). d gets
 // the lane's 16 data bytes, sw (lanes s % 4 == 0) the scale word of blocks s/2 and s/2 + 1. The rows
 // are stored to the cache slot here (attn_norm_rope2.comp:184-217 for the arithmetic).
+// K16: the K row in fp16 instead (lanes 0..31, 8 elements each; d gets the lane's 16 bytes).
+template <bool K16>
 __device__ __forceinline__ void append_q8_rows(const AppendArgs &ap, int64_t slot, const float *xk, const float *xv,
                                                int g, int lane, uint4 &d, uint32_t &sw) {
+  if (K16 && lane < 32) {
+    const float *x = xk + 8 * lane;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = f32_to_f16_rne(x[2 * i]) | (f32_to_f16_rne(x[2 * i + 1]) << 16);
+    d = make_uint4(w[0], w[1], w[2], w[3]);
+    sw = 0u;
+    uint8_t *dr = const_cast<uint8_t *>(ap.L.kd) + (slot * ap.nkv + g) * row_bytes(BKV_F16);
+    *reinterpret_cast<uint4 *>(dr + 16 * lane) = d;
+    return;
+  }
   const int s = lane & 15;
   const float *x = (lane < 32 ? xk : xv) + 16 * s;
   float v[16];
@@ -170,9 +183,13 @@ __device__ __forceinline__ int wave_sum64_i(int v) { return __builtin_amdgcn_rea
 
 // SHORT: a plan of at most 128 keys per workgroup (every workgroup then has no tail keys); its own
 // instantiation, so that the block-split scores and e pass leave the full-pass code as it is
-template <bool PG, bool SHORT>
+// KF: the K format, q8_0 (scores on the int8 matrix cores) or fp16 (the reference's own cache
+// format, kv_guard.h:118-130: scores as DPP chains in the reference's order, attn_vk.h:156-170,
+// over half rows staged twice); V is q8_0.
+template <int KF, bool PG, bool SHORT>
 __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   constexpr int NT = kResNT, NW = kResNW, NP = kSwNP, KS = kSwKeys;
+  constexpr bool K16 = KF == BKV_F16;
   using WS = WalkScratchT<kResMaxGroupWgs, 192>;
   using VR = KRow<BKV_Q8_0>;
   // LDS. kt: the K tiles (pass key k at row k: kt + k * kUPR); once every tile is scored the same
@@ -304,15 +321,23 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
                    "s"(xbs + 1024u) : "memory", "m0");
     }
   }
-  if (t0) stage_k_wave<BKV_Q8_0, PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 0);
-  if (tr > 0) {                                // 2 rows x 17 uint4: lanes 0..33
-    const uint32_t tb = __builtin_amdgcn_readfirstlane(lds_addr(ttl + 2 * wave * kUPR));
-    const int row = lane / kUPR, col = lane - row * kUPR;
-    const int64_t sl = slot_k<PG>(sm, NP + 2 * wave + min(row, tr - 1));
-    const uint8_t *src = col == 16 ? L.ks + (sl * nkv + g) * kScaleRowBytes : L.kd + (sl * nkv + g) * kHd + col * 16;
-    if (lane < 2 * kUPR)
-      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(tb) : "memory", "m0");
-  }
+  // (fp16 K: half row ch, dims 128 ch .., of each key; column 16 an unused copy)
+  auto stage_tile = [&](int ch) {
+    if (t0) stage_k_wave<KF, PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), ch);
+  };
+  auto stage_tail = [&](int ch) {
+    if (tr > 0) {                              // 2 rows x 17 uint4: lanes 0..33
+      const uint32_t tb = __builtin_amdgcn_readfirstlane(lds_addr(ttl + 2 * wave * kUPR));
+      const int row = lane / kUPR, col = lane - row * kUPR;
+      const int64_t sl = slot_k<PG>(sm, NP + 2 * wave + min(row, tr - 1));
+      const uint8_t *src = K16 ? L.kd + (sl * nkv + g) * row_bytes(KF) + (ch * 16 + (col & 15)) * 16
+                         : col == 16 ? L.ks + (sl * nkv + g) * kScaleRowBytes : L.kd + (sl * nkv + g) * kHd + col * 16;
+      if (lane < 2 * kUPR)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(tb) : "memory", "m0");
+    }
+  };
+  stage_tile(0);
+  stage_tail(0);
   // q (and x) are read by every wave: wave 0 waits for them (the K loads it issued after them may
   // still be in flight), then the workgroup syncs once; each wave then waits for its own K rows only
   // and scores them while the other waves' tiles are still landing
@@ -320,13 +345,27 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __syncthreads();                             // s_q (and s_x) visible to every wave
   // the q8_0 K digits of the group's q rows, in the V scale rows' LDS (their loads come after the
   // scores, once every wave has read its A operands)
+  // (fp16 K: q16 in registers for the DPP chains, qv[h][j] = q16[h][16 j + lane % 16])
   int8_t *s_lim = reinterpret_cast<int8_t *>(vsc);
   static_assert(kLimBytes <= (int)sizeof(vsc), "digits in the V scale rows");
-  q8lim_build(reinterpret_cast<const float *>(s_q), kHd, s_lim, s_lt, &s_wide, tid, NT);
-  __syncthreads();
   Q8Lim qlim;
-  q8lim_load(s_lim, s_lt, qlim);
-  const bool wide = s_wide != 0u;
+  float qv[kGqa][K16 ? kHd / 16 : 1];
+  if constexpr (!K16) {
+    q8lim_build(reinterpret_cast<const float *>(s_q), kHd, s_lim, s_lt, &s_wide, tid, NT);
+    __syncthreads();
+    q8lim_load(s_lim, s_lt, qlim);
+  } else {
+    const float *qf = reinterpret_cast<const float *>(s_q) + (lane & 15);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qf[h * kHd + 16 * j]);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+      for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qv[h][j]));
+  }
+  const bool wide = !K16 && s_wide != 0u;
   wait_vm<0>();                                // this wave's K tile
   RTSV(0);
 
@@ -348,7 +387,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     uint32_t asw = 0u;
     if (wave == aw) {
       const float *xf = reinterpret_cast<const float *>(s_x);
-      append_q8_rows(a.ap, slot_k<PG>(sm, kp), xf, xf + kHd, g, lane, ad, asw);   // (decode_step: base 0)
+      append_q8_rows<K16>(a.ap, slot_k<PG>(sm, kp), xf, xf + kHd, g, lane, ad, asw);   // (decode_step: base 0)
       wave_lds_sync();
       __builtin_amdgcn_wave_barrier();
       if (lane >= 32 && lane < 48) {           // the V patch row: 16 data uint4, then the scale row
@@ -356,8 +395,10 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         if (((lane - 32) & 3) == 0) reinterpret_cast<uint32_t *>(&s_x[16])[(lane - 32) >> 2] = asw;
       }
     }
-    auto patch_k = [&](uint4 *row) {          // the appended K row over its staged copy
-      if (lane < 16) {
+    auto patch_k = [&](uint4 *row, int ch) {  // the appended K row (fp16: half row ch) over its staged copy
+      if constexpr (K16) {
+        if (lane >= 16 * ch && lane < 16 * ch + 16) row[lane - 16 * ch] = ad;
+      } else if (lane < 16) {
         row[lane] = ad;
         if ((lane & 3) == 0) reinterpret_cast<uint32_t *>(&row[16])[lane >> 2] = asw;
       }
@@ -369,13 +410,30 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     if (bsplit) {
       // at most 2 x 64 keys: every wave scores one MFMA key group of 16
       RTS(14);
-      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
+      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 0);
       __syncthreads();                         // both tiles (and the patched row) are in LDS
       // wave w: keys 16 w + lane % 16 against head lane / 16 (the scores go to s_e, over the K
       // tiles, once every wave has scored)
       const int i16 = lane & 15, hg = lane >> 4, key = 16 * wave + i16;
       float v = 0.0f;
-      if (16 * wave < np) {                    // (uniform)
+      if constexpr (K16) {
+        // one chain per lane over both half rows: the second half is staged once every wave has
+        // taken the first
+        float qt[kHd / 16];
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, hg, j);
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
+        asm volatile("s_nop 4");
+        const uint4 *row = kt + min(key, np - 1) * kUPR;
+        if (16 * wave < np) qk_f16_half1<0>(row, qt, v);   // (uniform)
+        __syncthreads();
+        stage_tile(1);
+        wait_vm<0>();
+        if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 1);
+        __syncthreads();
+        if (16 * wave < np) qk_f16_half1<1>(row, qt, v);
+      } else if (16 * wave < np) {             // (uniform)
         const uint4 *row = kt + min(key, np - 1) * kUPR;
         if (!wide) {
           v = q8_score16(row, qlim);
@@ -394,9 +452,20 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       RTSV(1);
     } else if (t0) {
       RTS(14);
-      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR);
+      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 0);
       float acc1[kGqa];
-      if (!wide) {
+      if constexpr (K16) {
+        // the DPP chains over half row 0, the wave's tile restaged with half row 1, the chains on
+        // (attn_vk.h:156-170: one chain per key and head in ascending d)
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) acc1[h] = 0.0f;
+        qk_f16_half<0>(kt + kl * kUPR, qv, acc1);
+        wave_lds_sync();
+        stage_tile(1);
+        wait_vm<0>();
+        if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 1);
+        qk_f16_half<1>(kt + kl * kUPR, qv, acc1);
+      } else if (!wide) {
         // four MFMA key groups of 16 (lane: key 16 c + lane % 16, head lane / 16), then transposed
         // to one key per lane
         q8_score64(kt + 64 * wave * kUPR, kUPR, qlim, acc1);
@@ -411,13 +480,29 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       RTSV(1);
     }
     if (tr > 0) {
-      if (wave == aw && kp >= NP) patch_k(ttl + (kp - NP) * kUPR);
-      // the wave's tail keys 2 w, 2 w + 1 as MFMA columns 0, 1 (lane: key column lane % 16, head
-      // lane / 16)
+      if (wave == aw && kp >= NP) patch_k(ttl + (kp - NP) * kUPR, 0);
+      // the wave's tail keys 2 w, 2 w + 1 (lane: key lane % 16, head lane / 16; q8_0 K: as MFMA
+      // columns 0, 1)
       const int n16 = lane & 15, hg = lane >> 4, t = 2 * wave + n16;
       const uint4 *row = ttl + (2 * wave + min(n16, tr - 1)) * kUPR;
       float v[kGqa];
-      if (!wide) {
+      if constexpr (K16) {
+        float qt[kHd / 16];
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, hg, j);
+#pragma unroll
+        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
+        asm volatile("s_nop 4");
+        float x = 0.0f;
+        qk_f16_half1<0>(row, qt, x);
+        wave_lds_sync();
+        stage_tail(1);
+        wait_vm<0>();
+        if (wave == aw && kp >= NP) patch_k(ttl + (kp - NP) * kUPR, 1);
+        qk_f16_half1<1>(row, qt, x);
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) v[h] = x;
+      } else if (!wide) {
         const float x = q8_score16(row, qlim);
 #pragma unroll
         for (int h = 0; h < kGqa; ++h) v[h] = x;
@@ -1159,12 +1244,14 @@ static int stream_capacity() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   const int known = cached[dev].load(std::memory_order_acquire);
   if (known > 0) return known - 1;
-  int cap = 0, per = 0, per2 = 0;
+  int cap = 0, per[4] = {0, 0, 0, 0};
   hipDeviceProp_t pr;
   if (hipGetDeviceProperties(&pr, dev) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, stream_kernel<PG, false>, kResNT, 0) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per2, stream_kernel<PG, true>, kResNT, 0) == hipSuccess)
-    cap = std::min(per, per2) * pr.multiProcessorCount;
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per[0], stream_kernel<BKV_Q8_0, PG, false>, kResNT, 0) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per[1], stream_kernel<BKV_Q8_0, PG, true>, kResNT, 0) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per[2], stream_kernel<BKV_F16, PG, false>, kResNT, 0) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per[3], stream_kernel<BKV_F16, PG, true>, kResNT, 0) == hipSuccess)
+    cap = std::min({per[0], per[1], per[2], per[3]}) * pr.multiProcessorCount;
   cached[dev].store(cap + 1, std::memory_order_release);
   return cap;
 }
@@ -1176,12 +1263,16 @@ int stream_max_workgroups(bool paged) { return paged ? stream_capacity<true>() :
 // kernel; a grid that is not co-resident (another kernel holding CUs) makes the bounded waits give
 // up and set the workspace's error word (bkv_workspace_error). BKV_COOP=1 launches cooperatively
 // instead, so that the runtime refuses such a grid up front, at about 18 us more per call.
-hipError_t launch_stream(const ResArgs &a, hipStream_t st) {
+hipError_t launch_stream(const ResArgs &a, int kf, hipStream_t st) {
   const dim3 grid(a.G * a.nkv), block(kResNT);
   static const bool coop = [] { const char *e = std::getenv("BKV_COOP"); return e && e[0] == '1'; }();
   const bool shrt = a.kpw <= 2 * 64;
-  const void *fn = a.L.page ? (shrt ? (const void *)stream_kernel<true, true> : (const void *)stream_kernel<true, false>)
-                            : (shrt ? (const void *)stream_kernel<false, true> : (const void *)stream_kernel<false, false>);
+  const void *fn;
+#define BKV_STREAM_FN(KF)                                                                              \
+  (a.L.page ? (shrt ? (const void *)stream_kernel<KF, true, true> : (const void *)stream_kernel<KF, true, false>) \
+            : (shrt ? (const void *)stream_kernel<KF, false, true> : (const void *)stream_kernel<KF, false, false>))
+  fn = kf == BKV_F16 ? BKV_STREAM_FN(BKV_F16) : BKV_STREAM_FN(BKV_Q8_0);
+#undef BKV_STREAM_FN
   ResArgs args = a;
   void *kp[] = {&args};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, block, kp, 0, st);

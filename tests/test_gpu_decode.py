@@ -121,7 +121,8 @@ def test_deterministic_repeat(path):
 
 @pytest.mark.parametrize("kf,vf,n,seed", [(BKV_Q8_0, BKV_Q8_0, 4097, 1), (BKV_F16, BKV_F16, 3000, 7),
                                           (BKV_Q8_0, BKV_Q8_0, 40000, 2), (BKV_Q8_0, BKV_Q8_0, 65537, 3),
-                                          (BKV_F16, BKV_F16, 65537, 5)])
+                                          (BKV_F16, BKV_F16, 65537, 5), (BKV_F16, BKV_Q8_0, 4097, 11),
+                                          (BKV_F16, BKV_Q8_0, 32769, 12), (BKV_F16, BKV_Q8_0, 90, 13)])
 def test_scores_probabilities_and_sum_bit_exact(kf, vf, n, seed, path, monkeypatch):
     """The intermediates the reference's bitwise gate (BONSAI_QCHECK stages A/B) compares: every score,
     every e_j = exp(s_j*scale - max) and the serial fp32 softmax sum match the oracle bit for bit, and
