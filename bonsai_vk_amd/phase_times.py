@@ -2,11 +2,11 @@
 layer's time goes. Needs the instrumented build:
 
     python -m bonsai_vk_amd.build --timestamps
-    BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so python -m bonsai_vk_amd.phase_times [ctx] [--paged]
+    BKV_LIBRARY=bonsai_vk_amd/libbkv_ts.so python -m bonsai_vk_amd.phase_times [ctx] [--paged] [--b2b] [--f16k]
 
 With BKV_EXPERIMENT_TS every workgroup's thread 0 writes the GPU wall clock (100 MHz) at each phase
 boundary into the workspace at byte 131072 ([workgroup][16] u32). The probe runs six decode_steps
-of one q8_0 layer at ctx keys (256-token pages with --paged), and prints min / median / max over
+of one q8_0 layer at ctx keys (256-token pages with --paged; fp16 K with --f16k), and prints min / median / max over
 the workgroups of the last call, in microseconds from the first workgroup's start.
 """
 import os
@@ -31,17 +31,17 @@ PHASES = [(0, "start"), (1, "scores done (wave 0)"), (2, "barrier A passed"), (1
 TS_WORD = 131072 // 4
 
 
-def probe(ctx=32768, paged=False, calls=6, b2b=False):
+def probe(ctx=32768, paged=False, calls=6, b2b=False, k_fmt=BKV_Q8_0):
     """Timestamps [workgroups][16] (raw 100 MHz clocks) of the last of `calls` decode_steps; b2b:
     the calls run back to back as in the bench (one synchronisation at the end), otherwise each
     call starts on an idle GPU."""
     if paged:
         npg = (ctx + calls + 255) // 256
         bt = np.random.default_rng(3).permutation(npg).astype(np.int32)[None]
-        cache = KvCache(n_layers=1, cap=npg * 256, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=ctx + calls,
+        cache = KvCache(n_layers=1, cap=npg * 256, k_fmt=k_fmt, v_fmt=BKV_Q8_0, max_ctx=ctx + calls,
                         page_tokens=256, max_pages=npg, block_table=bt)
     else:
-        cache = KvCache(n_layers=1, cap=ctx + calls, k_fmt=BKV_Q8_0, v_fmt=BKV_Q8_0, max_ctx=ctx + calls)
+        cache = KvCache(n_layers=1, cap=ctx + calls, k_fmt=k_fmt, v_fmt=BKV_Q8_0, max_ctx=ctx + calls)
     g = torch.Generator(device="cuda")
     g.manual_seed(0)
     for s in range(0, ctx, 8192):
@@ -75,7 +75,8 @@ def probe(ctx=32768, paged=False, calls=6, b2b=False):
 
 def main(argv):
     ctx = int(next((a for a in argv if not a.startswith("-")), 32768))
-    ts = probe(ctx, "--paged" in argv, b2b="--b2b" in argv)
+    from bonsai_vk_amd import BKV_F16
+    ts = probe(ctx, "--paged" in argv, b2b="--b2b" in argv, k_fmt=BKV_F16 if "--f16k" in argv else BKV_Q8_0)
     phases = PHASES if os.environ.get("BKV_DECODE") == "resident" else PHASES_STREAM
     t0 = ts[:, 0].min()
     print(f"ctx {ctx}{' paged' if '--paged' in argv else ''}{' back to back' if '--b2b' in argv else ''}: phase clocks in us from the first "
