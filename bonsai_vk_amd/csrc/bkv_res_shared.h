@@ -3,6 +3,8 @@
 // scans and the exact-sum walk over the group's chunk records.
 #pragma once
 
+#include <type_traits>
+
 #include "bkv_common.h"
 #include "bkv_device.h"
 #include "bkv_internal.h"
@@ -459,9 +461,16 @@ __device__ __forceinline__ float pick4h(const float (&qv)[kGqa][kHd / 16], int h
   return __uint_as_float(b);
 }
 
+// v[i] by masks over the values (a select of the elements lets the compiler select their addresses
+// instead, which keeps the array in scratch memory)
 template <typename T>
 __device__ __forceinline__ T pick4(const T (&v)[kGqa], int i) {
-  return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit elements");
+  using U = std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>;
+  U b = 0;
+#pragma unroll
+  for (int j = 0; j < kGqa; ++j) b |= __builtin_bit_cast(U, v[j]) & (U(0) - (U)(i == j));
+  return __builtin_bit_cast(T, b);
 }
 
 // PV over a wave's register-resident q8_0 V rows (slots s: key 32 s + 4 wave + vkk), probabilities

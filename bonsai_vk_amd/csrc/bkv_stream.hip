@@ -26,20 +26,23 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
+#include <utility>
 
 #include "bkv_exp.h"
-#include "bkv_q8dot.h"
+#include "bkv_pv8.h"
 #include "bkv_res_shared.h"
 
 namespace bkv {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kSwKW = 4;                 // waves 0..3 poll, walk and correct
 constexpr int kSwNP = kResNT;            // pass keys per workgroup (one per thread)
-constexpr int kSwSlots = 17;             // V slots per lane: 16 x 32 pass rows, 1 x 16 tail rows (waves 0..3)
 constexpr int kSwKeys = kSwNP + kResTail;
 constexpr int kSwTailLoads = (kResTail * kUPR + 63) / 64;   // direct-to-LDS loads of the tail rows
 constexpr int kSwBlocks = kSwNP / 64 + 1;                  // e-pass blocks: 8 of 64 keys, the tail
-constexpr int kSwRisk = 128;             // at-risk V rows the LDS keeps (more: re-read from the cache)
+constexpr int kSwRisk = 32;              // at-risk V rows the LDS keeps (more: re-read from the cache)
 // relative distance from S_a inside which the exact sum is expected: the serial fp32 sum departs
 // from the exact one by up to ~7e-6 relative at 32K keys (2e-6 median), and S_a adds its own ~1e-6;
 // a key is at risk when p16' would round differently anywhere within twice this distance of it
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   // bytes hold the e values, probabilities, binade map, specials, walk scratch, the at-risk V rows
   // and the PV reduction.
   __shared__ uint4 kt[NP * kUPR];
-  __shared__ uint4 vsc[NW * 64];            // V scale rows: wave w, slot s < 16, row vkk at [w][4 s + vkk]
+  __shared__ uint4 vsc[NW * 64];            // V scale rows: pass key k of wave w at [w][k - NKW w]
   __shared__ uint4 ttl[kResTail * kUPR];    // the tail's K rows
   __shared__ float4 s_q[kGqa * kHd / 4];    // the group's q rows (fp32)
   __shared__ uint4 s_x[2 * kHd / 4];        // decode_step: the new token's K and V (fp32), then its V row
@@ -214,6 +217,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ int s_nrisk;
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
+  __shared__ unsigned s_pvctr;              // waves done reading their PV staging rows
   __shared__ int s_lt[kGqa * 8];            // q8_0 K digits: the exponent of each (head, block)
   __shared__ unsigned s_wide;               // the q8_0 K digits do not fit (fp64 score path)
 
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2, 0ull);
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
-  if (tid == 0) { s_kctr = 0u; s_nrisk = 0; s_wide = 0u; }
+  if (tid == 0) { s_kctr = 0u; s_pvctr = 0u; s_nrisk = 0; s_wide = 0u; }
   if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
@@ -266,8 +270,9 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 
   const bool appender = a.ap.k && (int64_t)a.ap.pos >= kb && (int64_t)a.ap.pos < ke;
   const int kp = appender ? (int)((int64_t)a.ap.pos - kb) : -1;     // the new token's key in this workgroup
-  // pass key k sits in wave k / 64 (its K tile) and V slot (k / 32, wave (k % 32) / 4, row group
-  // k % 4); tail key NP + t: its K row on wave t / 2, its V row on wave t / 4 (slot 16)
+  // pass key k sits in wave k / 64 (its K tile) and, for the PV, in wave k / NKW (V slot
+  // (k % NKW) / 4, row group k % 4); tail key NP + t: its K row on wave t / 2, its V row on wave
+  // t / 4 (the tail slot)
   const int aw = kp < 0 ? -1 : (kp < NP ? kp >> 6 : (kp - NP) >> 1);   // the wave that appends it
   SlotMap sm{&L, kb, s_pg, 0u};
   if constexpr (PG) {
@@ -287,15 +292,24 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   int16_t *s_ridx = reinterpret_cast<int16_t *>(s_bin + kGqa * KS);   // [KS] at-risk row index, -1: none
   Special *s_spec = reinterpret_cast<Special *>(xb + 24576);          // [kGqa][kMaxSpecial]
   WS *s_walk = reinterpret_cast<WS *>(xb + 24576 + kGqa * kMaxSpecial * sizeof(Special));
-  uint4 *s_rrow = reinterpret_cast<uint4 *>(xb + 53248);              // [kSwRisk + 8][16] at-risk V rows
-  float *s_red = reinterpret_cast<float *>(xb + 53248 + (kSwRisk + 8) * 256);  // [wave][head][EPL][LPR]
-  int16_t *s_rl = reinterpret_cast<int16_t *>(xb + 53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4);  // [K wave][KS]
+  constexpr int kStg = 53248 + kSwRisk * 256;                         // the PV staging rows, 8 waves
+  constexpr int kStgW = kPv8Rows * kPv8Stride;
+  uint4 *s_rrow = reinterpret_cast<uint4 *>(xb + 53248);              // [kSwRisk][16] at-risk V rows
+  // [wave][head][dim]: each wave's PV partial; over the staging rows of waves 0..3, written once
+  // every wave has finished reading its staging rows (s_pvctr)
+  float *s_red = reinterpret_cast<float *>(xb + kStg);
+  int16_t *s_rl = reinterpret_cast<int16_t *>(xb + kStg + NW * kStgW);   // [K wave][KS]
   static_assert(kGqa * KS * 4 + 2 * KS * 8 + kGqa * KS + 2 * KS <= 24576, "e, p16', p16, binade map, risk index");
   static_assert(24576 + kGqa * kMaxSpecial * sizeof(Special) + kGqa * sizeof(WS) <= 53248, "specials, walk scratch");
-  static_assert(53248 + (kSwRisk + 8) * 256 + NW * kGqa * kHd * 4 + kSwKW * KS * 2 <= sizeof(kt),
-                "at-risk rows, PV reduction, at-risk key lists");
+  static_assert(NW * kGqa * kHd * 4 <= NW * kStgW, "the PV partials over the staging rows");
+  static_assert(kStg + NW * kStgW + kSwKW * KS * 2 <= sizeof(kt), "at-risk rows, PV staging, at-risk key lists");
   const int th = lane >> 4, tt = lane & 15;   // tail e pass: lane 16 h + t takes tail key t, head h
   const int vsub = lane & 15, vkk = lane >> 4;
+  // the PV's pass keys per wave (kw0 = NKW w ..) and V slots per lane (slot s: key kw0 + 4 s + vkk,
+  // its 16-byte chunk vsub), staged for the matrix cores in rounds of 32 keys
+  constexpr int NKW = SHORT ? 16 : 64, NS = NKW / 4, NR = (NKW + kPv8Rows - 1) / kPv8Rows;
+  const int kw0 = NKW * wave;
+  auto vsc_row = [&](int k) { return SHORT ? (k / NKW) * 64 + k % NKW : k; };   // pass key k's V scale row
 
   // ---------------------------------------------------------------- loads
   // Wave 0 first brings q (and decode_step's new K and V) into LDS; every wave then stages its K
@@ -305,7 +319,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   // were issued after the ones it needs (the V loads are the compiler's and come last).
   const bool t0 = 64 * wave < np;              // the wave's K tile holds keys
   const int tr = min(2, max(0, tn - 2 * wave));   // the wave's tail K rows
-  const bool vt = wave < 4;                    // the wave holds a tail V slot
+  const bool vt = !SHORT && wave < 4;          // the wave holds a tail V slot
   if (wave == 0) {
     const uint32_t qb = __builtin_amdgcn_readfirstlane(lds_addr(s_q));
     const float *qsrc = a.q + (size_t)g * kGqa * a.qs;
@@ -549,24 +563,27 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   // issue stalls a wave while its CU's memory queue is full. (Polling waves that request theirs
   // only after barrier A hold up the e pass: 288 against 280 us per token.) The digits in vsc were
   // read before the barriers of the statistics.
-  uint4 vd[kSwSlots];                          // slot s: row 32 s + 4 w + vkk; slot 16: row NP + 4 w + vkk
+  // (vector types: copies of HIP's uint4 struct into LDS are memcpys, which keep the array in
+  // scratch memory)
+  u32x4 vd[NS];                                // slot s: row kw0 + 4 s + vkk
+  u32x4 vtl = u32x4{0u, 0u, 0u, 0u};           // the tail slot (waves 0..3): row NP + 4 w + vkk
   uint32_t xs = 0u;                            // the tail slot's scale word
   auto request_v = [&]() {
     {
       const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
-      const int64_t sl = slot_k<PG>(sm, min(32 * (lane >> 2) + 4 * wave + (lane & 3), nk - 1));
+      const int64_t sl = slot_k<PG>(sm, min(kw0 + (lane & (NKW - 1)), nk - 1));
       asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(L.vs + (sl * nkv + g) * kScaleRowBytes),
                    "s"(sb) : "memory", "m0");
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int64_t sl = slot_k<PG>(sm, min(kw0 + 4 * s + vkk, nk - 1));
+      vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
     if (vt) {
       const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
       xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-    }
-#pragma unroll
-    for (int s = 0; s < kSwSlots; ++s) {
-      const int k = s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk;
-      const int64_t sl = slot_k<PG>(sm, min(k, nk - 1));
-      vd[s] = *reinterpret_cast<const uint4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+      vtl = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
   };
   request_v();
@@ -849,7 +866,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
     }
   }
-  wait_vm_n(kSwSlots + (vt ? 1 : 0));          // this wave's V scale rows are in LDS (for every wave)
+  wait_vm_n(NS + (vt ? 2 : 0));                // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
   RTS(3);
 
@@ -877,97 +894,120 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   }
 
   // ---------------------------------------------------------------- the speculative PV (every wave)
-  // out += p16' * V over the wave's slots; each at-risk row is kept in LDS for the corrections
+  // out += p16' * V over the wave's pass keys on the int8 matrix cores (bkv_pv8.h), in rounds of 32
+  // keys staged from the V registers into LDS; the rows of at-risk keys are kept in LDS for the
+  // corrections. Waves 0..3 add the tail slot on the VALU (acc, which later takes the corrections).
   float acc[kGqa][VR::EPL];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
     for (int i = 0; i < VR::EPL; ++i) acc[h][i] = 0.0f;
-  const uint16_t *vsc16 = reinterpret_cast<const uint16_t *>(vsc + wave * 64);
-  auto slot_key = [&](int s) { return s < kSwSlots - 1 ? 32 * s + 4 * wave + vkk : NP + 4 * wave + vkk; };
-  auto slot_scale = [&](int s) -> float {
-    if (s < kSwSlots - 1) return f16_to_f32(vsc16[(4 * s + vkk) * 8 + (vsub >> 1)]);
-    return f16_to_f32(((vsub >> 1) & 1) ? (xs >> 16) : (xs & 0xFFFFu));
-  };
   auto p4 = [](uint2 pw, float (&p)[kGqa]) {
     p[0] = f16_to_f32(pw.x & 0xFFFFu);
     p[1] = f16_to_f32(pw.x >> 16);
     p[2] = f16_to_f32(pw.y & 0xFFFFu);
     p[3] = f16_to_f32(pw.y >> 16);
   };
-  const int sp_slot = kp < 0 ? -1 : (kp < NP ? kp / 32 : kSwSlots - 1);
-  const int sp_w = kp < 0 ? -1 : (kp < NP ? (kp % 32) / 4 : (kp - NP) / 4), sp_kk = kp % 4;
-  auto patched = [&](int s) { return s == sp_slot && wave == sp_w && vkk == sp_kk; };
   // the appended row (decode_step) replaces the loaded copy, which may predate it
-  const uint4 pd = s_x[vsub];
+  const u32x4 pd = reinterpret_cast<const u32x4 *>(s_x)[vsub];
   const uint32_t pws = reinterpret_cast<const uint32_t *>(&s_x[16])[vsub >> 2];
   const float pscale = f16_to_f32(((vsub >> 1) & 1) ? (pws >> 16) : (pws & 0xFFFFu));
+  float pvp[16];                               // the wave's partial: head lane / 16, dim 16 t + lane % 16
   {
-    // each slot's LDS operands are read one slot ahead, and no further (held back by the compiler
-    // barrier at the end of a slot, they would all be read up front into registers)
-    uint2 pn = s_ps[min(slot_key(0), KS - 1)];
-    int rn = s_ridx[min(slot_key(0), KS - 1)];
-    float vn = slot_scale(0);
-    auto pv_slot = [&](int s, const uint4 &vrow, uint2 pw, int ri, float vs) {
-      const int k = slot_key(s);
-      const bool live = (s < kSwSlots - 1 ? k < np : (vt && k < nk));
-      pw.x = live ? pw.x : 0u;
-      pw.y = live ? pw.y : 0u;
-      float p[kGqa];
-      p4(pw, p);
-      v_accum<BKV_Q8_0>(vrow, live && !patched(s) ? vs : 0.0f, p, acc);
-      // (stored unconditionally, rows not at risk into spare rows: no branch per slot)
-      s_rrow[(live && ri >= 0 ? ri : kSwRisk + wave) * 16 + vsub] = vrow;
-    };
-    // the pass slots that hold keys of this wave (slot s: keys 32 s + 4 w ..), then the tail slot
-    const int nsl = min(kSwSlots - 1, max(0, (np - 4 * wave + 31) / 32));
-    auto scale_bits = [&](int s) -> uint32_t { return vsc16[(4 * s + vkk) * 8 + (vsub >> 1)]; };
-    if (nsl == kSwSlots - 1) {
-      // every pass slot holds keys: straight-line code, each slot's LDS operands requested at the
-      // start of the slot before and waited for at the start of the next
-      uint32_t vr = scale_bits(0);
+    // 2^sig(h): every p16' * scale of the wave's keys times it stays below 2^29 (p16' <= the
+    // workgroup's largest e, exp(mloc - M), times 1 / S_a, plus a margin for the roundings; the
+    // scale <= the largest of the wave's V scale rows)
+    const bool apw = kp >= 0 && kp < NP && wave == kp / NKW;   // the appended key is one of this wave's
+    if (apw && lane == 0) vsc[vsc_row(kp)] = s_x[16];        // its scale row over the loaded one
+    wave_lds_sync();
+    int sig[kGqa];
+    {
+      const uint32_t dm = f16_row_max(vsc[wave * 64 + (lane & (NKW - 1))]);
+      const int ed = f16_exp_bound(__builtin_bit_cast(uint16_t, (_Float16)wave_max64(f16_to_f32(dm))));
 #pragma unroll
-      for (int s = 0; s < kSwSlots - 1; ++s) {
-        const uint2 pw = pn;
-        const int ri = rn;
-        const uint32_t vsr = vr;
-        if (s + 1 < kSwSlots - 1) {
-          pn = s_ps[min(slot_key(s + 1), KS - 1)];
-          rn = s_ridx[min(slot_key(s + 1), KS - 1)];
-          vr = scale_bits(s + 1);
-        }
-        asm volatile("" ::: "memory");
-        pv_slot(s, vd[s], pw, ri, f16_to_f32(vsr));
-        asm volatile("" ::: "memory");
+      for (int h = 0; h < kGqa; ++h) {
+        const float pb = __expf(mloc[h] - Mh[h]) * rSa[h] * 1.002f;
+        const int ep = max(-30, (int)((__float_as_uint(pb) >> 23) & 0xFFu) - 127);
+        sig[h] = min(100, 27 - ep - ed);
       }
-    } else
-#pragma unroll
-    for (int s = 0; s < kSwSlots - 1; ++s) {
-      if (s < nsl) {                           // (uniform)
-        const uint2 pw = pn;
-        const int ri = rn;
-        const float vs = vn;
-        if (s + 1 < kSwSlots - 1) {
-          pn = s_ps[min(slot_key(s + 1), KS - 1)];
-          rn = s_ridx[min(slot_key(s + 1), KS - 1)];
-          vn = slot_scale(s + 1);
+    }
+    const Pv8Sel z = pv8_sel();
+    v4i_t pacc[16];
+    const uint32_t stg = __builtin_amdgcn_readfirstlane(lds_addr(xb + kStg + wave * kStgW));
+    const int ia = lane & 3, ha = (lane & 15) >> 2, kq = lane >> 4;
+    const float sga = __builtin_ldexpf(1.0f, pick4(sig, ha));
+    const int lim = min(np, kw0 + NKW);
+    auto round = [&](auto rc) __attribute__((always_inline)) {
+      constexpr int r = decltype(rc)::value;
+      auto stage = [&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value, sl = 8 * r + j;
+        if constexpr (sl < NS)
+          *reinterpret_cast<u32x4 *>(xb + kStg + wave * kStgW + (4 * j + vkk) * kPv8Stride + 16 * vsub) = vd[sl];
+      };
+      [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+        (stage(std::integral_constant<int, J>{}), ...);
+      }(std::make_integer_sequence<int, 8>{});
+      const int k0 = kw0 + kPv8Rows * r;
+      if (apw && kp >= k0 && kp < k0 + kPv8Rows && vkk == ((kp - k0) & 3))   // the appended row over its loaded copy
+        *reinterpret_cast<u32x4 *>(xb + kStg + wave * kStgW + (kp - k0) * kPv8Stride + 16 * vsub) = pd;
+      // (rare) at-risk keys: their rows kept for the corrections
+      const unsigned rb32 = (unsigned)(s_rb[k0 >> 6] >> (k0 & 63)) & (NKW < 32 ? 0xFFFFu : 0xFFFFFFFFu);
+      if (rb32 != 0u) {
+#pragma unroll 1
+        for (int j = 0; j < NKW / 4 && j < 8; ++j) {
+          const int key = k0 + 4 * j + vkk;
+          if ((rb32 >> (4 * j + vkk)) & 1u) {
+            const int ri = s_ridx[key];
+            if (ri >= 0)
+              reinterpret_cast<u32x4 *>(s_rrow)[ri * 16 + vsub] = *reinterpret_cast<const u32x4 *>(xb + kStg + wave * kStgW + (4 * j + vkk) * kPv8Stride + 16 * vsub);
+          }
         }
-        asm volatile("" ::: "memory");
-        pv_slot(s, vd[s], pw, ri, vs);
       }
       asm volatile("" ::: "memory");
+      const int ka = k0 + 8 * kq + 2 * ia;
+      auto pf = [&](int k) {
+        if (k >= lim) return 0.0f;
+        const uint2 pw = s_ps[k];
+        const uint32_t w = ha < 2 ? pw.x : pw.y;
+        return f16_half(w, ha & 1) * sga;      // exact: a power of two
+      };
+      const float pa = pf(ka), pb = pf(ka + 1);
+      const uint4 sa = vsc[wave * 64 + min(ka - kw0, NKW - 1)], sb = vsc[wave * 64 + min(ka + 1 - kw0, NKW - 1)];
+      long A[8];
+      pv8_prep(pa, pb, sa, sb, z, A);
+      pv8_round<r == 0>(stg, A, pacc);
+      asm volatile("" ::: "memory");
+    };
+    if (kw0 < np) {                            // (uniform) the wave holds keys
+      round(std::integral_constant<int, 0>{});
+      if constexpr (NR > 1)
+        if (kw0 + kPv8Rows < np) round(std::integral_constant<int, 1>{});
+      const int nsig = -pick4(sig, lane >> 4);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) pvp[t] = pv8_value(pacc[t], nsig);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) pvp[t] = 0.0f;
     }
-    if (vt && tn > 0)
-      pv_slot(kSwSlots - 1, vd[kSwSlots - 1], s_ps[min(slot_key(kSwSlots - 1), KS - 1)], s_ridx[min(slot_key(kSwSlots - 1), KS - 1)],
-              slot_scale(kSwSlots - 1));
-    if (vt && (vsub & 3) == 0) s_tsw[(4 * wave + vkk) * 4 + (vsub >> 2)] = xs;
-    if (wave == sp_w) {                        // the appended row, by the lanes of its slot
-      uint2 pw = s_ps[kp];
-      if (vkk != sp_kk) pw = make_uint2(0u, 0u);
-      float p[kGqa];
-      p4(pw, p);
-      v_accum<BKV_Q8_0>(pd, vkk == sp_kk ? pscale : 0.0f, p, acc);
-    }
+    lds_arrive(&s_pvctr);                      // (waits for this wave's staging reads)
+  }
+  if (vt && tn > 0) {                          // the tail slot: key NP + 4 w + vkk
+    const int key = NP + 4 * wave + vkk;
+    const bool live = key < nk;
+    float p[kGqa];
+    p4(live ? s_ps[key] : make_uint2(0u, 0u), p);
+    const u32x4 rv = key == kp ? pd : vtl;
+    const uint4 row = make_uint4(rv.x, rv.y, rv.z, rv.w);
+    const float vs = key == kp ? pscale : f16_to_f32(((vsub >> 1) & 1) ? (xs >> 16) : (xs & 0xFFFFu));
+    v_accum<BKV_Q8_0>(row, live ? vs : 0.0f, p, acc);
+    const int ri = s_ridx[min(key, KS - 1)];
+    if (live && ri >= 0) s_rrow[ri * 16 + vsub] = row;
+  }
+  if (vt && (vsub & 3) == 0) s_tsw[(4 * wave + vkk) * 4 + (vsub >> 2)] = xs;
+  if (!kwave) {                                // the partial goes out once every wave has read its staging
+    lds_wait(&s_pvctr, NW);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) s_red[(wave * kGqa + (lane >> 4)) * kHd + 16 * t + (lane & 15)] = pvp[t];
   }
   RTS(13);
   RTSV(4);
@@ -1046,11 +1086,11 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 #pragma unroll
         for (int hh = 0; hh < kGqa; ++hh) p[hh] -= q[hh];
         if (kc4 == kp) {
-          d = pd;
+          d = make_uint4(pd.x, pd.y, pd.z, pd.w);
           vs = pscale;
         } else {
           const int ri = s_ridx[kc4];
-          const uint32_t sw = kc4 < NP ? reinterpret_cast<const uint32_t *>(vsc + ((kc4 % 32) / 4) * 64 + 4 * (kc4 / 32) + kc4 % 4)[vsub >> 2]
+          const uint32_t sw = kc4 < NP ? reinterpret_cast<const uint32_t *>(vsc + vsc_row(kc4))[vsub >> 2]
                                        : s_tsw[(kc4 - NP) * 4 + (vsub >> 2)];
           vs = f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
           if (ri >= 0) {
@@ -1146,8 +1186,12 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
     RTS(15);
   }
-  // the 4 row groups' sums by a reduce-scatter: row group r ends with head r's totals
-  {
+  if (kwave) {
+    // the partial, then the VALU part (tail, corrections): the 4 row groups' sums by a
+    // reduce-scatter (row group r ends with head r's totals) added to it
+    lds_wait(&s_pvctr, NW);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) s_red[(wave * kGqa + (lane >> 4)) * kHd + 16 * t + (lane & 15)] = pvp[t];
     float red[VR::EPL];
 #pragma unroll
     for (int i = 0; i < VR::EPL; ++i) {
@@ -1158,8 +1202,16 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(za), __float_as_uint(zb), false, false);
       red[i] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
     }
+    float4 *dst = reinterpret_cast<float4 *>(s_red + (wave * kGqa + vkk) * kHd + 16 * vsub);
 #pragma unroll
-    for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + vkk) * VR::EPL + i) * VR::LPR + vsub] = red[i];
+    for (int i = 0; i < 4; ++i) {
+      float4 x = dst[i];
+      x.x += red[4 * i];
+      x.y += red[4 * i + 1];
+      x.z += red[4 * i + 2];
+      x.w += red[4 * i + 3];
+      dst[i] = x;
+    }
   }
   __syncthreads();
   RTS(10);
@@ -1167,12 +1219,11 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   {
     static_assert(kGqa * kHd == 2 * NT, "two partial elements per thread");
     float2 v = make_float2(0.0f, 0.0f);
-    const int hh = (2 * tid) / kHd, dd = (2 * tid) % kHd;
-    const int ro = (hh * VR::EPL + dd % VR::EPL) * VR::LPR + dd / VR::EPL;
 #pragma unroll
     for (int wv = 0; wv < NW; ++wv) {
-      v.x += s_red[wv * kGqa * kHd + ro];
-      v.y += s_red[wv * kGqa * kHd + ro + VR::LPR];
+      const float2 x = reinterpret_cast<const float2 *>(s_red + wv * kGqa * kHd)[tid];
+      v.x += x.x;
+      v.y += x.y;
     }
     unsigned long long *dst = part_g + (size_t)wi * kGqa * kHd + 2 * tid;
     st_agent(dst, (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)gen << 32));
