@@ -315,19 +315,20 @@ def prefill_leg(cpu=True, reps=5):
         res[mode] = e0.elapsed_time(e1) / reps * 1e3   # us per 8-layer chunk
         os.environ.pop("BKV_PREFILL", None)
     fl = L * prefill_flops(pos0, n_q)
-    # the exact path's score sweep: 16 rows x 34 tiles x 256 keys per workgroup, 256 serial fp32 fma
-    # per (row, key) on v_mfma_f32_16x16x1_4b_f32 (fp32 matrix peak 157.3 TFLOP/s), over 512
-    # workgroups per layer; timed against the whole chunk, so a lower bound of the sweep's own rate
-    score_flops = L * 512 * 16 * (34 * 256) * 256 * 2
+    # the exact path's score sweep on the int8 matrix cores: each (query, head) row is 4 base-256
+    # digit rows of its fp16 value, so 4 x 2 x 256 int8 ops per (row, key), over the causal key range
+    # pos0 + i + 1 of query i, 16 heads per query
+    score_ops = L * 16 * sum(pos0 + i + 1 for i in range(n_q)) * 4 * 2 * 256
     out = {"workload": "bkv_attn_prefill_chunk x 8 layers: 512 q8_0 queries onto 8192 cached keys "
                        "(BASELINE config 5)",
            "unit": "us/chunk", "value": round(res["exact"], 1),
            "us_per_layer": round(res["exact"] / L, 1),
            "algorithmic_tflops": round(fl / (res["exact"] * 1e-6) / 1e12, 2),
-           "bound": "fp32 matrix cores (serial-order score chains, one fma per MFMA step) and the "
-                    "vector ALUs (correctly rounded exp, serial sums, the p16 quotients)",
-           "score_chain_fp32_mfma_tflops_over_chunk": round(score_flops / (res["exact"] * 1e-6) / 1e12, 1),
-           "fp32_mfma_peak_tflops": 157.3,
+           "bound": "vector ALUs (correctly rounded exp in fp64, serial sums, the p16 quotients, the "
+                    "serial outer chain of each q8_0 score), with the scores' inner sums on the int8 "
+                    "matrix cores",
+           "score_int8_mfma_tops_over_chunk": round(score_ops / (res["exact"] * 1e-6) / 1e12, 1),
+           "int8_mfma_peak_tops": 5000.0,
            "mfma_variant": {"value": round(res["mfma"], 1), "unit": "us/chunk",
                             "algorithmic_tflops": round(fl / (res["mfma"] * 1e-6) / 1e12, 1),
                             "peak_tflops": 2500.0,

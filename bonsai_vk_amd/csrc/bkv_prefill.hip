@@ -493,17 +493,18 @@ hipError_t launch_prefill(const PrefillArgs &a, int kf, int vf, hipStream_t st) 
 // ================================================================== exact prefill
 // The default prefill: every (query, head) row reproduces the serial reference bit for bit up to
 // the PV contraction. A workgroup owns 4 queries x 4 heads = 16 rows of one KV group and all of
-// their keys, in three sweeps:
-//   1  scores in the reference's order (q8_0 K: inner = sum of q16*int8 over a block ascending,
-//      as exact fp32 fma chains on the matrix cores, then acc = acc + f16(scale)*inner on the
-//      VALU; fp16 K: acc = acc + q16*k ascending on the VALU; every product is exact, so each step
-//      is one fma), times the softmax scale, masked causally; the row max. Scores go to a scratch
-//      region [key][row].
+// their keys, in up to three sweeps:
+//   1  scores (q8_0 K: the correctly rounded inner sum of each block from the int8 matrix cores,
+//      bkv_q8dot.h, then acc = acc + f16(scale)*inner in block order; fp16 K: the reference's serial
+//      chain acc = acc + q16*k in ascending d, one exact fma per step on the fp32 matrix cores),
+//      times the softmax scale, masked causally; the row max. Scores go to a scratch region
+//      [key][row].
 //   2  e = exp(v - max) correctly rounded, written back over the scores; one lane per row adds
 //      them in key order (the reference's serial fp32 sum, attn_vk.h:175-189).
-//   3  p16 = f16(e / sum) (the correctly rounded fp32 quotient, from e * (1/sum) by two remainder
-//      corrections, then round to nearest even), and out = sum p16 * v on the matrix cores with V
-//      as its exact fp16 hi/lo pair.
+//   3  (fp16 V) p16 = f16(e / sum) (the correctly rounded fp32 quotient, from e * (1/sum) by two
+//      remainder corrections, then round to nearest even), and out = sum p16 * v on the matrix
+//      cores. q8_0 V: the sums go out instead, and prefill_pv64_kernel forms p16 and the PV for 64
+//      rows at a time.
 // Only the PV sum runs in another order than the reference (fp32 accumulation of exact products).
 
 #ifdef BKV_EXPERIMENT_TS

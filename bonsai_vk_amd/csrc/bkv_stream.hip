@@ -913,6 +913,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   const uint32_t pws = reinterpret_cast<const uint32_t *>(&s_x[16])[vsub >> 2];
   const float pscale = f16_to_f32(((vsub >> 1) & 1) ? (pws >> 16) : (pws & 0xFFFFu));
   float pvp[16];                               // the wave's partial: head lane / 16, dim 16 t + lane % 16
+  RTSV(13);
   {
     // 2^sig(h): every p16' * scale of the wave's keys times it stays below 2^29 (p16' <= the
     // workgroup's largest e, exp(mloc - M), times 1 / S_a, plus a margin for the roundings; the
@@ -977,6 +978,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       pv8_prep(pa, pb, sa, sb, z, A);
       pv8_round<r == 0>(stg, A, pacc);
       asm volatile("" ::: "memory");
+      if constexpr (r == 0) RTSV(14);
     };
     if (kw0 < np) {                            // (uniform) the wave holds keys
       round(std::integral_constant<int, 0>{});
@@ -985,6 +987,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       const int nsig = -pick4(sig, lane >> 4);
 #pragma unroll
       for (int t = 0; t < 16; ++t) pvp[t] = pv8_value(pacc[t], nsig);
+      RTSV(15);
     } else {
 #pragma unroll
       for (int t = 0; t < 16; ++t) pvp[t] = 0.0f;

@@ -99,6 +99,10 @@ def main(argv):
             ok = dw > 0
             ghz = f"   score clock {np.median(dc[ok] / dw[ok]) / 10.0:5.2f} GHz over {np.median(dw[ok]) / 100.0:5.2f} us" if ok.any() else ""
             print(f"    wave {wv}: " + " ".join(cells) + ghz)
+        print("  the PV (median): start, first round of 32 keys done, partial formed")
+        for wv in range(8):
+            cells = [f"{(np.median(pw[:, wv, j]) - t0) / 100.0:7.2f}" if pw[:, wv, j].any() else "      -" for j in (13, 14, 15)]
+            print(f"    wave {wv}: " + " ".join(cells))
         print("  the walk (waves 0-3, median): records scanned, specials loaded, segments checked, "
               "chain done; specials walked")
         for wv in range(4):
