@@ -150,7 +150,7 @@ def kernel_name(cache, n):
 
 # the sources whose code a decode launch runs: a traffic summary measured on other code is stale
 TRAFFIC_SOURCES = ["bkv_stream.hip", "bkv_resident.hip", "bkv_res_shared.h", "bkv_device.h", "bkv_common.h",
-                   "bkv_exp.h", "bkv_q8dot.h", "bkv_internal.h"]
+                   "bkv_exp.h", "bkv_q8dot.h", "bkv_pv8.h", "bkv_internal.h"]
 
 
 def kernel_sources_sha():

@@ -23,6 +23,9 @@
 namespace bkv {
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
+// (vector types for rows that go into LDS: a copy of HIP's uint4 struct is a memcpy, which keeps
+// an array of them in scratch memory)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPv8Stride = 272;          // LDS bytes per staged V row (256 + 16: 2-way bank spread)
 constexpr int kPv8Rows = 32;             // keys per staging round (one MFMA k-extent)
@@ -59,11 +62,13 @@ __device__ __forceinline__ Pv8Sel pv8_sel() {
 // i = l % 4), keys 8 (l / 16) .. + 7 of the round. The lane computes the digits of its quad's keys
 // 2 i, 2 i + 1 (pa, pb: their p of head h times 2^sig(h); sa, sb: their scale rows, fp16 x 8) and
 // the quad exchanges bytes so that every lane ends with digit i of all 8 keys.
+// (B0, NB: blocks B0 .. B0 + NB - 1 only, into A[0 .. NB - 1])
+template <int B0 = 0, int NB = 8>
 __device__ __forceinline__ void pv8_prep(float pa, float pb, const uint4 &sa, const uint4 &sb, const Pv8Sel &z,
-                                         long (&A)[8]) {
+                                         long (&A)[NB]) {
   const uint32_t wa[4] = {sa.x, sa.y, sa.z, sa.w}, wb[4] = {sb.x, sb.y, sb.z, sb.w};
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
+  for (int b = B0; b < B0 + NB; ++b) {
     // x = p * 2^sig * s (v_fma_mix_f32 with + 0: the product is exact), below 2^30; Q = x rounded
     // to an integer (half up: v_cvt_rpi_i32_f32)
     const int sh = 16 * (b & 1);
@@ -82,7 +87,7 @@ __device__ __forceinline__ void pv8_prep(float pa, float pb, const uint4 &sa, co
     const uint32_t Zv = (uint32_t)__builtin_amdgcn_mov_dpp((int)Y, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
     const uint32_t lo = __builtin_amdgcn_perm(X, Zv, z.lo) ^ 0x80808080u;
     const uint32_t hi = __builtin_amdgcn_perm(X, Zv, z.hi) ^ 0x80808080u;
-    A[b] = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+    A[b - B0] = (long)((unsigned long)lo | ((unsigned long)hi << 32));
   }
 }
 
@@ -98,6 +103,57 @@ __device__ __forceinline__ void pv8_round(uint32_t rows, const long (&A)[8], v4i
         (__attribute__((address_space(3))) v2i_t *)(uintptr_t)(base + 16u * t));
     const long b = (long)((unsigned long)(uint32_t)bv.x | ((unsigned long)(uint32_t)bv.y << 32));
     acc[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[t >> 1], b, FIRST ? v4i_t{0, 0, 0, 0} : acc[t], 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------- the blocked region layout
+// A wave's 64 keys of V in one 17 KiB LDS region (a K tile's bytes, at a multiple of 1 KiB): block i
+// (keys 4 i .. 4 i + 3) at 1024 i, its 16-byte chunk c of row r at 64 (c ^ (i & 3)) + 16 r (the XOR
+// spreads the 32 rows one ds_read_b64_tr_b8 reads over the banks), then the 64 keys' scale rows
+// (16 B each) at 16384. Direct-to-LDS loads fill it (one 1 KiB block per load), or the V registers.
+constexpr int kPv8Region = 17408;
+constexpr int kPv8Scales = 16384;
+
+// direct-to-LDS loads of the region: rows(k) / scl(k): global addresses of key k's 256 data bytes
+// and 16 scale bytes (k = 0 .. 63, the caller clamps keys past its range); 17 loads (inline asm: the
+// caller waits for them with an explicit vmcnt)
+template <typename RowF, typename SclF>
+__device__ __forceinline__ void pv8_dma_region(uint32_t region, RowF rows, SclF scl) {
+  const int lane = threadIdx.x & 63, r = lane & 3, sl = lane >> 2;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint8_t *src = rows(4 * i + r) + 16 * (sl ^ (i & 3));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(region + 1024u * i)
+                 : "memory", "m0");
+  }
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(scl(lane)), "s"(region + (uint32_t)kPv8Scales)
+               : "memory", "m0");
+}
+
+// the region from registers: vd[i] = chunk lane % 16 of key 4 i + lane / 16, vs[i] = that key's
+// scale word (lane % 16) / 4
+__device__ __forceinline__ void pv8_store_region(char *region, const u32x4 (&vd)[16], const uint32_t (&vs)[16]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, r = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    *reinterpret_cast<u32x4 *>(region + 1024 * i + 64 * (c ^ (i & 3)) + 16 * r) = vd[i];
+    if ((c & 3) == 0) *reinterpret_cast<uint32_t *>(region + kPv8Scales + 16 * (4 * i + r) + 4 * (c >> 2)) = vs[i];
+  }
+}
+
+// One round over the region's keys 32 rd .. 32 rd + 31 (see pv8_round), dim tiles T0 .. T0 + NT - 1
+// into acc[0 .. NT - 1] with A[i] the operand of block T0 / 2 + i
+template <bool FIRST, int T0 = 0, int NT = 16>
+__device__ __forceinline__ void pv8_round_region(uint32_t region, int rd, const long (&A)[NT / 2], v4i_t (&acc)[NT]) {
+  const int lane = threadIdx.x & 63, j = (lane & 15) >> 1;
+  const int b = 8 * rd + 2 * (lane >> 4) + (j >> 2);            // the block of the lane's key 8 (l/16) + j
+  const uint32_t a0 = region + (uint32_t)(1024 * b + 16 * (j & 3) + 8 * (lane & 1) + 64 * (b & 3));
+#pragma unroll
+  for (int t = T0; t < T0 + NT; ++t) {
+    const v2i_t bv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (__attribute__((address_space(3))) v2i_t *)(uintptr_t)(a0 ^ (uint32_t)(64 * t)));
+    const long bb = (long)((unsigned long)(uint32_t)bv.x | ((unsigned long)(uint32_t)bv.y << 32));
+    acc[t - T0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[(t - T0) >> 1], bb, FIRST ? v4i_t{0, 0, 0, 0} : acc[t - T0], 0, 0, 0);
   }
 }
 

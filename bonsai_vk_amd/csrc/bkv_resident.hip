@@ -24,11 +24,12 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "bkv_common.h"
 #include "bkv_device.h"
 #include "bkv_exp.h"
-#include "bkv_q8dot.h"
+#include "bkv_pv8.h"
 #include "bkv_internal.h"
 #include "bkv_res_shared.h"
 
@@ -141,7 +142,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // (68 rows x 256 B, the same bytes) and at the end the PV reduction and the merge.
   // X: the binade map, then the walk scratch, then the fp16 probabilities.
   using WS = WalkScratchT<kResMaxGroupWgs, 192>;
-  __shared__ uint4 lds[NW * 64 * kUPR];
+  __shared__ __attribute__((aligned(1024))) uint4 lds[NW * 64 * kUPR];
+  static_assert(64 * kUPR * 16 == kPv8Region, "a wave's K tile holds its PV region");
   __shared__ uint4 ldx[kResXBytes / 16];
   static_assert(64 * kUPR * 16 == kResVTiles * 1024 + 64 * 16, "a wave's V rows and scales fill its K tile");
   static_assert(kResTail <= 16 && NT == 32 * kResVTiles, "the tail rows are the streamed slot");
@@ -350,24 +352,26 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h)
         if (th == h) mloc[h] = fmaxf(mloc[h], sct * a.scale);
   }
-  // q8_0 V without the register V form (fp16 K, or more than one pass): this wave's V rows
-  // 32 i + 4 wave + vkk of the first pass (i < 16) and their block-pair scale words, requested once
-  // the scores are done, so that they stream in during barrier A, the e pass and the walk instead
-  // of after them (requested after barrier A instead, they hold up the e pass: 377 against 364 us
-  // per token for fp16 K at 32K)
+  // q8_0 V without the register V form (more than one pass, or fp16 K): the PV runs on the int8
+  // matrix cores after the walk (bkv_pv8.h). Once the statistics are out, the first pass's rows of
+  // the wave's keys 64 wave .. + 63 go into its K tile by direct-to-LDS loads (the region layout),
+  // and the second pass's rows into registers (keys NT + 64 wave + 4 i + lane / 16), so that both
+  // stream in during barrier A, the e pass and the walk
   constexpr bool VPF = !VRES && VF == BKV_Q8_0;
-  constexpr int kPfRows = NT / 32;
-  uint4 pv_w[VPF ? kPfRows : 1];
-  uint32_t pv_s[VPF ? kPfRows : 1];
-  if constexpr (VPF) {
+  u32x4 pv_w[VPF ? 16 : 1];
+  uint32_t pv_s[VPF ? 16 : 1];
+  static_assert(kResTail == 16, "the tail fills blocks 0..3 of wave 0's region");
+  u32x4 tl_w[VPF ? kResTail / 4 : 1];       // VPF: the tail rows (wave 0)
+  uint32_t tl_s[VPF ? kResTail / 4 : 1];
+  auto pv_regs = [&](int r) {                // pass r's rows of this wave into pv_w / pv_s
 #pragma unroll
-    for (int i = 0; i < kPfRows; ++i) {
-      const int kl = 32 * i + wave * VR::KPW + vkk;
+    for (int i = 0; i < 16; ++i) {
+      const int kl = r * NT + 64 * wave + 4 * i + vkk;
       const int64_t slot = slot_k<PG>(sm, min(kl, nk - 1));
-      pv_w[i] = *reinterpret_cast<const uint4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+      pv_w[i] = *reinterpret_cast<const u32x4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
       pv_s[i] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
     }
-  }
+  };
   RTS(1);
 
   // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
@@ -385,6 +389,32 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   }
   block_sum4(lsum, shf4);
   if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
+  // VPF: the V requests once the statistics are out (every wave is done with its K tile: the
+  // reductions above synchronise the workgroup), so that the K stream of the later passes and the
+  // statistics do not wait behind them
+  if constexpr (VPF) {
+    if (64 * wave < tpk) {
+      const uint32_t region = __builtin_amdgcn_readfirstlane(lds_addr(kt));
+      pv8_dma_region(
+          region,
+          [&](int k) {
+            const int64_t slot = slot_k<PG>(sm, min(64 * wave + k, nk - 1));
+            return L.vd + (slot * nkv + g) * kHd;
+          },
+          [&](int k) {
+            const int64_t slot = slot_k<PG>(sm, min(64 * wave + k, nk - 1));
+            return L.vs + (slot * nkv + g) * kScaleRowBytes;
+          });
+    }
+    if (NT < tpk) pv_regs(1);
+    if (tn > 0 && wave == 0)                 // the tail keys tb + 4 i + lane / 16 (wave 0)
+#pragma unroll
+      for (int i = 0; i < kResTail / 4; ++i) {
+        const int64_t slot = slot_k<PG>(sm, min(tb + 4 * i + vkk, nk - 1));
+        tl_w[i] = *reinterpret_cast<const u32x4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+        tl_s[i] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+      }
+  }
 
   // ---------------------------------------------------------------- barrier A: global max
   // wave h polls head h's statistics of every workgroup of the group: the global max and this
@@ -591,7 +621,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // VRES: p16' = f16(e / S_a), the probabilities with the sum barrier A already gives, into the
   // (now free) K tile area, for the speculative PV of waves kGqa.. during the walk
   uint2 *s_ps = reinterpret_cast<uint2 *>(lds);
-  if constexpr (VRES || VPF) {
+  if constexpr (VRES) {
     static_assert(2048 * 4 >= NT * sizeof(uint2), "s_ps (one pass) must end before s_acc");
     if (tid < nk) {
       _Float16 pk[kGqa];
@@ -626,7 +656,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // rows with p16', and park the partial in the K tile area; after the walk they add
   // (p16 - p16') only for the keys whose rounding the exact sum changes
   float *s_acc = reinterpret_cast<float *>(lds) + 2048;   // [kGqa*EPL][NW-kGqa][64], past s_ps
-  if constexpr (VRES || VPF) {
+  if constexpr (VRES) {
     static_assert((2048 + kGqa * VR::EPL * (NW - kGqa) * 64) * 4 <= sizeof(lds), "s_acc must fit");
     if (wave >= kGqa) {
       float sacc[kGqa][VR::EPL];
@@ -634,8 +664,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       for (int h = 0; h < kGqa; ++h)
 #pragma unroll
         for (int i = 0; i < VR::EPL; ++i) sacc[h][i] = 0.0f;
-      if constexpr (VRES) pv_res_slots<false>(vd, vsw, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
-      else pv_res_slots<false>(pv_w, pv_s, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
+      pv_res_slots<false>(vd, vsw, s_ps, nullptr, nk, wave, vkk, vsub, sacc);
 #pragma unroll
       for (int h = 0; h < kGqa; ++h)
 #pragma unroll
@@ -724,6 +753,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   }
   __syncthreads();
   float acc[kGqa][VR::EPL];
+  float pvp[16];                           // VPF: the matrix cores' part, head lane / 16, dim 16 t + lane % 16
+#pragma unroll
+  for (int t = 0; t < 16; ++t) pvp[t] = 0.0f;
   RTS(12);
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
@@ -765,20 +797,87 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     constexpr int RB = row_bytes(VF);
     int base0 = 0;
     if constexpr (VPF) {
-      // the first pass's rows are in registers (requested after the scores): waves 0..3 add them
-      // with the exact p16; waves 4..7 added them with p16' during the walk and now add
-      // (p16 - p16') for the keys whose rounding the exact sum changed
-      static_assert(RS * U * (kPfRows / U) == NT && kPfRows == kResVTiles, "prefetched rows cover one pass");
-      if (wave < kGqa) {
-        pv_res_slots<false>(pv_w, pv_s, s_p16, nullptr, nk, wave, vkk, vsub, acc);
-      } else {
+      // out += p16 * V over the passes on the int8 matrix cores: each wave over its keys
+      // 64 wave .. + 63 of each pass, in its region (pass 0 loaded there directly, pass 1 from
+      // registers, later passes loaded now), two rounds of 32 keys per pass; 2^sig(h) keeps every
+      // p16 * scale of the pass below 2^29 (p16 <= the workgroup's largest e over the exact sum,
+      // plus a margin; the scale <= the wave's largest of the pass)
+      const Pv8Sel z = pv8_sel();
+      const int ia = lane & 3, ha = (lane & 15) >> 2, kq = lane >> 4;
+      char *region = reinterpret_cast<char *>(kt);
+      const uint32_t rg = __builtin_amdgcn_readfirstlane(lds_addr(kt));
+      int ep[kGqa];
 #pragma unroll
-        for (int h = 0; h < kGqa; ++h)
-#pragma unroll
-          for (int i = 0; i < VR::EPL; ++i) acc[h][i] = s_acc[((h * VR::EPL + i) * (NW - kGqa) + wave - kGqa) * 64 + lane];
-        pv_res_slots<true>(pv_w, pv_s, s_p16, s_ps, nk, wave, vkk, vsub, acc);
+      for (int h = 0; h < kGqa; ++h) {
+        const float pb = __expf(mloc[h] - s_M[h]) / s_S[h] * 1.002f;
+        ep[h] = max(-30, (int)((__float_as_uint(pb) >> 23) & 0xFFu) - 127);
       }
-      base0 = NT;
+      wait_vm<0>();                            // pass 0's direct-to-LDS rows, pass 1's registers
+      // one part (a pass's 64 keys of this wave, or the tail on wave 0) already in the region:
+      // keys kw0 + k (k < 64) with probabilities below kend
+      auto part = [&](int kw0, int kend) __attribute__((always_inline)) {
+        const uint4 sr = *reinterpret_cast<const uint4 *>(region + kPv8Scales + 16 * lane);
+        const uint32_t dm = kw0 + lane < kend ? f16_row_max(sr) : 0u;
+        const int ed = f16_exp_bound(__builtin_bit_cast(uint16_t, (_Float16)rd_lane(wave_max_l63(f16_to_f32(dm)), 63)));
+        int sig[kGqa];
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) sig[h] = min(100, 27 - ep[h] - ed);
+        const float sga = __builtin_ldexpf(1.0f, pick4(sig, ha));
+        // two halves of 8 dim tiles (blocks 0..3, 4..7): half the accumulators live at a time
+        auto half = [&](auto hc) __attribute__((always_inline)) {
+          constexpr int hf = decltype(hc)::value;
+          v4i_t pacc[8];
+          auto round = [&](auto rc) __attribute__((always_inline)) {
+            constexpr int rd = decltype(rc)::value;
+            const int ka = 32 * rd + 8 * kq + 2 * ia;
+            auto pf = [&](int k) {
+              if (kw0 + k >= kend) return 0.0f;
+              const uint2 pw = s_p16[kw0 + k];
+              const uint32_t w2 = ha < 2 ? pw.x : pw.y;
+              return f16_half(w2, ha & 1) * sga;   // exact: a power of two
+            };
+            const float pa = pf(ka), pb = pf(ka + 1);
+            const uint4 sa = *reinterpret_cast<const uint4 *>(region + kPv8Scales + 16 * ka);
+            const uint4 sb = *reinterpret_cast<const uint4 *>(region + kPv8Scales + 16 * (ka + 1));
+            long A[4];
+            pv8_prep<4 * hf, 4>(pa, pb, sa, sb, z, A);
+            pv8_round_region<rd == 0, 8 * hf, 8>(rg, rd, A, pacc);
+          };
+          round(std::integral_constant<int, 0>{});
+          if (kw0 + 32 < kend) round(std::integral_constant<int, 1>{});
+          const int nsig = -pick4(sig, lane >> 4);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) pvp[8 * hf + t] += pv8_value(pacc[t], nsig);
+        };
+        half(std::integral_constant<int, 0>{});
+        half(std::integral_constant<int, 1>{});
+      };
+#pragma unroll 1
+      for (int r = 0; r < MP; ++r) {
+        if (r * NT >= tpk) break;
+        const int kw0 = r * NT + 64 * wave;
+        if (r >= 1) {
+          if (r >= 2) {
+            pv_regs(r);
+            wait_vm<0>();
+          }
+          wave_lds_sync();                     // the previous part's reads of the region are done
+          pv8_store_region(region, pv_w, pv_s);
+          wave_lds_sync();
+        }
+        if (kw0 < tpk) part(kw0, tpk);         // (uniform)
+      }
+      if (tn > 0 && wave == 0) {               // the tail keys tb .. nk - 1 as blocks 0..3 of the region
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < kResTail / 4; ++i) {
+          *reinterpret_cast<u32x4 *>(region + 1024 * i + 64 * (vsub ^ (i & 3)) + 16 * vkk) = tl_w[i];
+          if ((vsub & 3) == 0) *reinterpret_cast<uint32_t *>(region + kPv8Scales + 16 * (4 * i + vkk) + 4 * (vsub >> 2)) = tl_s[i];
+        }
+        wave_lds_sync();
+        part(tb, nk);
+      }
+      base0 = nk;
     }
     for (int base = base0; base < nk; base += RS * U) {
       uint4 wv[U];
@@ -842,8 +941,13 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   float *s_red = reinterpret_cast<float *>(lds);
   static_assert(VR::LPR * VR::EPL == kHd && (VR::LPR != 16 || 64 / VR::LPR == kGqa), "partial layout");
   if constexpr (VR::LPR == 16) {
+    if constexpr (VPF) {                   // element (head lane / 16, dim 16 t + lane % 16)
 #pragma unroll
-    for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + vkk) * VR::EPL + i) * VR::LPR + vsub] = red[i];
+      for (int t = 0; t < 16; ++t) s_red[((wave * kGqa + (lane >> 4)) * VR::EPL + (lane & 15)) * VR::LPR + t] = pvp[t];
+    } else {
+#pragma unroll
+      for (int i = 0; i < VR::EPL; ++i) s_red[((wave * kGqa + vkk) * VR::EPL + i) * VR::LPR + vsub] = red[i];
+    }
   } else if (vkk == 0) {
 #pragma unroll
     for (int h = 0; h < kGqa; ++h)

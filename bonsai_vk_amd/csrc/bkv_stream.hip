@@ -35,8 +35,6 @@
 
 namespace bkv {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kSwKW = 4;                 // waves 0..3 poll, walk and correct
 constexpr int kSwNP = kResNT;            // pass keys per workgroup (one per thread)
 constexpr int kSwKeys = kSwNP + kResTail;
