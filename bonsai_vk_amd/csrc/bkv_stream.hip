@@ -566,6 +566,10 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   u32x4 vd[NS];                                // slot s: row kw0 + 4 s + vkk
   u32x4 vtl = u32x4{0u, 0u, 0u, 0u};           // the tail slot (waves 0..3): row NP + 4 w + vkk
   uint32_t xs = 0u;                            // the tail slot's scale word
+  // V1 (slots of the first round, and the scale rows) before barrier A; the rest once the records
+  // are out (the barrier-A polls wait behind every load their CU has queued, and only the PV reads
+  // the later slots)
+  constexpr int NS1 = NS < 8 ? NS : 8;
   auto request_v = [&]() {
     {
       const uint32_t sb = __builtin_amdgcn_readfirstlane(lds_addr(vsc + wave * 64));
@@ -574,7 +578,14 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
                    "s"(sb) : "memory", "m0");
     }
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
+    for (int s = 0; s < NS1; ++s) {
+      const int64_t sl = slot_k<PG>(sm, min(kw0 + 4 * s + vkk, nk - 1));
+      vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+    }
+  };
+  auto request_v2 = [&]() {
+#pragma unroll
+    for (int s = NS1; s < NS; ++s) {
       const int64_t sl = slot_k<PG>(sm, min(kw0 + 4 * s + vkk, nk - 1));
       vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
@@ -864,7 +875,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
     }
   }
-  wait_vm_n(NS + (vt ? 2 : 0));                // this wave's V scale rows are in LDS (for every wave)
+  wait_vm_n(NS1);                              // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
   RTS(3);
 
@@ -890,6 +901,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + wi) * 2 + 1, w1);
     }
   }
+  request_v2();
 
   // ---------------------------------------------------------------- the speculative PV (every wave)
   // out += p16' * V over the wave's pass keys on the int8 matrix cores (bkv_pv8.h), in rounds of 32
