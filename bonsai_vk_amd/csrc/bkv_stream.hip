@@ -582,17 +582,19 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       const int64_t sl = slot_k<PG>(sm, min(kw0 + 4 * s + vkk, nk - 1));
       vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
+    if (vt) {
+      const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
+      xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+      vtl = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
+    }
   };
+  // (the tail slot goes with V1: loads only some waves issue, between the two groups, would make
+  // the compiler's wait for the first round's rows also wait for part of V2 on those waves)
   auto request_v2 = [&]() {
 #pragma unroll
     for (int s = NS1; s < NS; ++s) {
       const int64_t sl = slot_k<PG>(sm, min(kw0 + 4 * s + vkk, nk - 1));
       vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
-    }
-    if (vt) {
-      const int64_t sl = slot_k<PG>(sm, min(NP + 4 * wave + vkk, nk - 1));
-      xs = *reinterpret_cast<const uint32_t *>(L.vs + (sl * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-      vtl = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
   };
   request_v();
@@ -875,7 +877,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
     }
   }
-  wait_vm_n(NS1);                              // this wave's V scale rows are in LDS (for every wave)
+  wait_vm_n(NS1 + (vt ? 2 : 0));               // this wave's V scale rows are in LDS (for every wave)
   __syncthreads();                             // specials, p16', the risk index, the V scale rows
   RTS(3);
 
