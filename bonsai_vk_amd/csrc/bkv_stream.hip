@@ -926,6 +926,30 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   const float pscale = f16_to_f32(((vsub >> 1) & 1) ? (pws >> 16) : (pws & 0xFFFFu));
   float pvp[16];                               // the wave's partial: head lane / 16, dim 16 t + lane % 16
   RTSV(13);
+  if constexpr (SHORT) {
+    // short plans: 16 keys per wave on the VALU (with so few keys the matrix-core form's fixed
+    // costs and LDS round trips take longer)
+    const unsigned rbw = (unsigned)(s_rb[kw0 >> 6] >> (kw0 & 63)) & 0xFFFFu;
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+      const int key = kw0 + 4 * sl + vkk;
+      const bool live = key < np;
+      float p[kGqa];
+      p4(live ? s_ps[key] : make_uint2(0u, 0u), p);
+      const uint32_t sw = reinterpret_cast<const uint32_t *>(vsc + wave * 64 + 4 * sl + vkk)[vsub >> 2];
+      const u32x4 rv = key == kp ? pd : vd[sl];
+      const uint4 row = make_uint4(rv.x, rv.y, rv.z, rv.w);
+      const float vs = key == kp ? pscale : f16_to_f32(((vsub >> 1) & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+      v_accum<BKV_Q8_0>(row, live ? vs : 0.0f, p, acc);
+      if ((rbw >> (4 * sl + vkk)) & 1u) {      // (rare) an at-risk key: its row for the corrections
+        const int ri = s_ridx[key];
+        if (ri >= 0) s_rrow[ri * 16 + vsub] = row;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) pvp[t] = 0.0f;
+    lds_arrive(&s_pvctr);
+  } else {
   {
     // 2^sig(h): every p16' * scale of the wave's keys times it stays below 2^29 (p16' <= the
     // workgroup's largest e, exp(mloc - M), times 1 / S_a, plus a margin for the roundings; the
@@ -1006,6 +1030,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
     lds_arrive(&s_pvctr);                      // (waits for this wave's staging reads)
   }
+  }
   if (vt && tn > 0) {                          // the tail slot: key NP + 4 w + vkk
     const int key = NP + 4 * wave + vkk;
     const bool live = key < nk;
@@ -1019,7 +1044,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     if (live && ri >= 0) s_rrow[ri * 16 + vsub] = row;
   }
   if (vt && (vsub & 3) == 0) s_tsw[(4 * wave + vkk) * 4 + (vsub >> 2)] = xs;
-  if (!kwave) {                                // the partial goes out once every wave has read its staging
+  if (!kwave && !SHORT) {                      // the partial goes out once every wave has read its staging
     lds_wait(&s_pvctr, NW);
 #pragma unroll
     for (int t = 0; t < 16; ++t) s_red[(wave * kGqa + (lane >> 4)) * kHd + 16 * t + (lane & 15)] = pvp[t];
@@ -1201,9 +1226,9 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     }
     RTS(15);
   }
-  if (kwave) {
-    // the partial, then the VALU part (tail, corrections): the 4 row groups' sums by a
-    // reduce-scatter (row group r ends with head r's totals) added to it
+  if (kwave || SHORT) {
+    // the partial, then the VALU part (tail, corrections; short plans: all of it): the 4 row
+    // groups' sums by a reduce-scatter (row group r ends with head r's totals) added to it
     lds_wait(&s_pvctr, NW);
 #pragma unroll
     for (int t = 0; t < 16; ++t) s_red[(wave * kGqa + (lane >> 4)) * kHd + 16 * t + (lane & 15)] = pvp[t];
