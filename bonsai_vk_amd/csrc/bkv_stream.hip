@@ -249,6 +249,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   constexpr int GM = kResMaxGroupWgs;
   unsigned long long *tstats = a.tstats + (size_t)g * kGqa * GM;
   unsigned long long *trec = a.trec + (size_t)g * kGqa * GM * 2;
+  // the group's specials [head][workgroup][kMaxSpecial], stored where the e pass finds them
+  Special *spec_g = a.spec + (size_t)(g * kGqa) * G * kMaxSpecial;
   if (wi == 0)                                 // entries of workgroups this call does not run
     for (int i = tid; i < kGqa * (GM - G); i += NT) {
       const int h = i / (GM - G), c = G + i % (GM - G);
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   uint2 *s_p16 = s_ps + KS;                                           // [KS] p16
   int8_t *s_bin = reinterpret_cast<int8_t *>(s_p16 + KS);             // [kGqa][KS]
   int16_t *s_ridx = reinterpret_cast<int16_t *>(s_bin + kGqa * KS);   // [KS] at-risk row index, -1: none
-  Special *s_spec = reinterpret_cast<Special *>(xb + 24576);          // [kGqa][kMaxSpecial]
+  // (24576 .. : room for [kGqa][kMaxSpecial] specials, which now go straight to global memory)
   WS *s_walk = reinterpret_cast<WS *>(xb + 24576 + kGqa * kMaxSpecial * sizeof(Special));
   constexpr int kStg = 53248 + kSwRisk * 256;                         // the PV staging rows, 8 waves
   constexpr int kStgW = kPv8Rows * kPv8Stride;
@@ -761,7 +763,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         x.ipre = (long long)(ib + (din[h] - dinc[h]));
         x.e = ev[h];
         x.meta = kl | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
-        s_spec[h * kMaxSpecial + id] = x;
+        st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + id], x);
       }
     }
   }
@@ -777,7 +779,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       x.ipre = (long long)(ib + (dint - dinct));
       x.e = evt;
       x.meta = (NP + tt) | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
-      s_spec[th * kMaxSpecial + id] = x;
+      st_spec(&spec_g[((size_t)th * G + wi) * kMaxSpecial + id], x);
     }
   }
   {
@@ -864,7 +866,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         x.ipre = (long long)(ib + (dins - dincs));
         x.e = evs;
         x.meta = kk | ((bprev == kNoBinade ? 0 : (bprev + 128)) << 16);
-        s_spec[hh * kMaxSpecial + id] = x;
+        st_spec(&spec_g[((size_t)hh * G + wi) * kMaxSpecial + id], x);
       }
     }
     const float p = evs * pick4(rSa, hh);
@@ -877,8 +879,10 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       atomicOr(&s_rb[kk >> 6], 1ull << (kk & 63));
     }
   }
-  wait_vm_n(NS1 + (vt ? 2 : 0));               // this wave's V scale rows are in LDS (for every wave)
-  __syncthreads();                             // specials, p16', the risk index, the V scale rows
+  // every wave's specials are stored (before the records that announce them) and its V scale rows
+  // are in LDS: the first V group and the specials were issued long enough ago for this wait to be short
+  wait_vm<0>();
+  __syncthreads();                             // p16', the risk index, the V scale rows
   RTS(3);
 
   // ---------------------------------------------------------------- records (K waves)
@@ -887,10 +891,6 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     int nsp = 0;
     double t = 0.0;
     for (int b = 0; b < kSwBlocks; ++b) { nsp += s_bc[b * kGqa + h]; t += s_bu[b * kGqa + h]; }
-    Special *spec_g = a.spec + (size_t)(g * kGqa) * G * kMaxSpecial;
-    const int ns = min(nsp, kMaxSpecial);
-    if (lane < ns) st_spec(&spec_g[((size_t)h * G + wi) * kMaxSpecial + lane], s_spec[h * kMaxSpecial + lane]);
-    if (ns > 0) __builtin_amdgcn_s_waitcnt(0);   // the specials are visible before the record is
     if (lane == 0) {
       ChunkRec rc;
       rc.tot = (long long)t;
