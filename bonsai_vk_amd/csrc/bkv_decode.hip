@@ -54,8 +54,8 @@ __global__ __launch_bounds__(QkTile<KF>::NT) void qk_kernel(QkArgs a) {
   float acc[kGqa];
   if constexpr (KF == BKV_Q8_0) {
     // the int8 matrix cores on the q rows' digits (bkv_q8dot.h)
-    __shared__ int8_t s_lim[kLimBytes];
-    __shared__ int s_lt[kGqa * 8];
+    __shared__ __attribute__((aligned(16))) int8_t s_lim[kLimBytes];
+    __shared__ int s_lt[kGqa];
     __shared__ unsigned s_wide;
     if (tid == 0) s_wide = 0u;
     __syncthreads();

@@ -580,8 +580,8 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     // bytes are requested a whole tile ahead (the rows come from HBM the first time any workgroup
     // of the XCD reads them; the workgroups run nearly in step).
     int8_t *s_lim = reinterpret_cast<int8_t *>(s_big);                    // [query][kLimBytes]
-    int *s_lt = reinterpret_cast<int *>(s_big + kPxQ * kLimBytes);        // [query][head][block]
-    static_assert(kPxQ * (kLimBytes + kGqa * 8 * 4) <= sizeof(s_big), "digits in the big LDS area");
+    int *s_lt = reinterpret_cast<int *>(s_big + kPxQ * kLimBytes);        // [query][head]
+    static_assert(kPxQ * (kLimBytes + kGqa * 4) <= sizeof(s_big), "digits in the big LDS area");
     __shared__ unsigned s_wide;
     if (tid == 0) s_wide = 0u;
     __syncthreads();
@@ -591,22 +591,19 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
     };
 #pragma unroll 1
     for (int jq = 0; jq < kPxQ; ++jq)
-      q8lim_build(qrows(jq), a.qs, s_lim + jq * kLimBytes, s_lt + jq * kGqa * 8, &s_wide, tid, 256);
+      q8lim_build(qrows(jq), a.qs, s_lim + jq * kLimBytes, s_lt + jq * kGqa, &s_wide, tid, 256);
     __syncthreads();
     const bool wide = s_wide != 0u;
     long qa[kPxQ][8];
-    uint32_t qt[kPxQ][2];                      // the exponents of head l/16, packed as signed bytes
+    int qt[kPxQ];                              // the exponent of head l/16 of each query
     {
       Q8Lim t;
 #pragma unroll
       for (int jq = 0; jq < kPxQ; ++jq) {
-        q8lim_load(s_lim + jq * kLimBytes, s_lt + jq * kGqa * 8, t);
+        q8lim_load(s_lim + jq * kLimBytes, s_lt + jq * kGqa, t);
 #pragma unroll
         for (int b = 0; b < 8; ++b) qa[jq][b] = t.a[b];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          qt[jq][i] = (uint32_t)(t.t[4 * i] & 0xFF) | ((uint32_t)(t.t[4 * i + 1] & 0xFF) << 8) |
-                      ((uint32_t)(t.t[4 * i + 2] & 0xFF) << 16) | ((uint32_t)(t.t[4 * i + 3] & 0xFF) << 24);
+        qt[jq] = t.t;
       }
     }
     const int ql = lane >> 4, n16 = lane & 15;
@@ -663,7 +660,7 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
           float r[4];
           const uint4 scl = make_uint4(cur.s.x, cur.s.y, cur.s.z, cur.s.w);
 #pragma unroll
-          for (int jq = 0; jq < kPxQ; ++jq) r[jq] = q8_score16p(cur.b, scl, qa[jq], qt[jq]);
+          for (int jq = 0; jq < kPxQ; ++jq) r[jq] = q8_score16r(cur.b, scl, qa[jq], qt[jq]);
           load_kg((uint32_t)(max(t - 1, 0) * kPxTile + 64 * w), kg, cur);
           transpose_rows4(r);
           emit(key0, kg, r);

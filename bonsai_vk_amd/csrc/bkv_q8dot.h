@@ -11,16 +11,21 @@
 // magnitude, so a block's exact sum is a multiple of 2^-24 below 2^28, which fp64 holds exactly
 // (the CPU restatement sums it in fp64 in any order and rounds once).
 //
-// On the device the exact sum is an integer dot product. For head h and block b let t be the
-// smallest exponent of an fp16 ulp among the block's nonzero q16 values; then Q_d = q16_d / 2^t is
-// an integer, and when it fits four balanced base-256 digits, Q_d = sum_i c_i 256^i with c_i in
+// On the device the exact sum is an integer dot product. For head h let t be the smallest exponent
+// of an fp16 ulp among the row's nonzero q16 values (all 256 dims); then Q_d = q16_d / 2^t is an
+// integer, and when it fits four balanced base-256 digits, Q_d = sum_i c_i 256^i with c_i in
 // [-128, 127] (the bytes of Q_d + 0x80808080, each minus 128). One v_mfma_i32_16x16x32_i8 per block
 // and 16 keys then gives, for A row 4h + i (head h, digit i) and key column n, the exact integer
-// o_i = sum_d c_i(d) * int8_d(n); o_0 + 256 o_1 + 65536 o_2 + 2^24 o_3 = sum_d Q_d int8_d exactly
+// o_i = sum_d c_i(d) * int8_d(n); x_b = o_0 + 256 o_1 + 65536 o_2 + 2^24 o_3 = sum_d Q_d int8_d exactly
 // (combined in i32 pairs and one fp64 fma, every intermediate an integer below 2^53), and
-// inner = fp32(that) * 2^t, one rounding. q16 rows whose digits do not fit (an exponent spread of
-// more than 20 binades inside one block) or that hold Inf / NaN take an fp64 VALU path per key
-// with the same result.
+// inner_b = fp32(x_b) * 2^t, one rounding. Because t is shared by the row's 8 blocks, the outer chain
+// runs on the unscaled fp32(x_b) and the score is the chain's value times 2^t: every term of the
+// scaled chain is 2^t times the unscaled one with the same rounding, as no value of either chain is
+// subnormal (a nonzero term is at least 2^-24 * 2^-24, the smallest fp16 ulp times the smallest
+// scale; every sum is a multiple of its terms' ulps) or overflows (|x_b| < 2^43, scales < 2^16,
+// t <= 5). q16 rows whose digits do not fit (Q beyond 31 bits: an exponent spread of more than about
+// 20 binades over the row, which needs |q| >= 2^-24 * 2^31 = 128 beside values near 2^-24) or that
+// hold Inf / NaN take an fp64 VALU path per key with the same result.
 #pragma once
 
 #include "bkv_common.h"
@@ -32,27 +37,27 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int kLimBytes = 8 * 16 * 32;   // digits in LDS: [block][row 4 h + i][32 dims] int8
 
 // The A operands of one wave: lane l holds row l % 16 (head (l%16)/4, digit l % 4), dims
-// 8 (l/16) .. + 7 of each block; t[b]: the exponent of block b for head l / 16 (the head whose
-// scores lane l receives).
+// 8 (l/16) .. + 7 of each block; t: the exponent of head l / 16 (the head whose scores lane l
+// receives).
 struct Q8Lim {
   long a[8];
-  int t[8];
+  int t;
 };
 
 // Cooperative: the digits of the group's 4 q rows (fp32, row h at q + h * qs, in LDS or global
-// memory; rounded to fp16 here as the reference's Q16 operand) into lim (kLimBytes) and the
-// exponents into lt[h * 8 + b].
-// *wide (zeroed by the caller before a barrier) is set when a block's digits do not fit or a q16
-// is not finite. nt: threads taking part (a multiple of 64); tid: this thread's index among them.
+// memory; rounded to fp16 here as the reference's Q16 operand) into lim (kLimBytes, 4-byte aligned)
+// and the rows' exponents into lt[h]. One wave per row: lane l takes dims 4 l .. 4 l + 3 (block l / 8).
+// *wide (zeroed by the caller before a barrier) is set when a row's digits do not fit or a q16 is
+// not finite. nt: threads taking part (a multiple of 64); tid: this thread's index among them.
 __device__ __forceinline__ void q8lim_build(const float *q, int qs, int8_t *lim, int *lt, unsigned *wide, int tid,
                                             int nt) {
-  for (int i = tid; i < kGqa * kHd / 2; i += nt) {    // (uniform trip count: nt divides 512)
-    const int h = i >> 7, d0 = 2 * (i & 127), b = d0 >> 5;
-    int mant[2], ue[2], neg[2];
+  const int lane = tid & 63, d0 = 4 * lane, b = lane >> 3;
+  for (int h = tid >> 6; h < kGqa; h += nt >> 6) {    // (wave-uniform trip count)
+    int mant[4], ue[4], neg[4];
     bool bad = false;
     int key = 127;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const uint32_t bits = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q[(size_t)h * qs + d0 + j]);
       const uint32_t ab = bits & 0x7FFFu;
       const int E = (int)(ab >> 10);
@@ -62,27 +67,26 @@ __device__ __forceinline__ void q8lim_build(const float *q, int qs, int8_t *lim,
       neg[j] = (int)(bits >> 15);
       if (mant[j] != 0) key = min(key, ue[j]);
     }
-    // the block's 32 dims sit in this 16-lane row
-    key = min(key, __shfl_xor(key, 1));
-    key = min(key, __shfl_xor(key, 2));
-    key = min(key, __shfl_xor(key, 4));
-    key = min(key, __shfl_xor(key, 8));
-    const int t = key == 127 ? 0 : key;
-    uint32_t V[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const long long m = mant[j] != 0 ? ((long long)mant[j] << (ue[j] - t)) : 0ll;
+    for (int o = 1; o < 64; o <<= 1) key = min(key, __shfl_xor(key, o));
+    const int t = key == 127 ? 0 : key;
+    uint32_t V[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long long m = mant[j] != 0 ? ((long long)mant[j] << (ue[j] - t)) : 0ll;   // shift <= 29
       const long long vv = (neg[j] ? -m : m) + 0x80808080ll;
       bad = bad || vv < 0 || vv > 0xFFFFFFFFll;
       V[j] = (uint32_t)vv ^ 0x80808080u;            // byte i: digit i as a two's complement int8
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t pair = ((V[0] >> (8 * d)) & 0xFFu) | (((V[1] >> (8 * d)) & 0xFFu) << 8);
-      *reinterpret_cast<uint16_t *>(lim + (b * 16 + 4 * h + d) * 32 + (d0 & 31)) = (uint16_t)pair;
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w |= ((V[j] >> (8 * d)) & 0xFFu) << (8 * j);
+      *reinterpret_cast<uint32_t *>(lim + (b * 16 + 4 * h + d) * 32 + (d0 & 31)) = w;
     }
-    if ((i & 15) == 0) lt[h * 8 + b] = t;
-    if (__ballot(bad) != 0ull && (threadIdx.x & 63) == 0) atomicOr(wide, 1u);
+    if (lane == 0) lt[h] = t;
+    if (__ballot(bad) != 0ull && lane == 0) atomicOr(wide, 1u);
   }
 }
 
@@ -90,40 +94,28 @@ __device__ __forceinline__ void q8lim_load(const int8_t *lim, const int *lt, Q8L
   const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
 #pragma unroll
   for (int b = 0; b < 8; ++b) L.a[b] = *reinterpret_cast<const long *>(lim + (b * 16 + m) * 32 + 8 * kq);
-#pragma unroll
-  for (int b = 0; b < 8; ++b) L.t[b] = lt[kq * 8 + b];
+  L.t = lt[kq];
 }
 
 __device__ __forceinline__ float f16_half(uint32_t w, int hi) { return f16_to_f32(hi ? (w >> 16) : (w & 0xFFFFu)); }
 
 // Scores of 16 keys from registers: bv[b] = the lane's 8 bytes of block b (dims 8 (l/16) .. + 7)
-// of key l % 16, scl = that key's scale row; a, t: the A operands and the exponents (Q8Lim).
+// of key l % 16, scl = that key's scale row; a, t: the A operands and the exponent (Q8Lim).
 // Lane l receives the score of key l % 16 against head l / 16.
-__device__ __forceinline__ float q8_score16r(const long (&bv)[8], const uint4 &scl, const long (&a)[8],
-                                             const int (&t)[8]) {
+__device__ __forceinline__ float q8_score16r(const long (&bv)[8], const uint4 &scl, const long (&a)[8], int t) {
   v4i_t d[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) d[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[b], bv[b], v4i_t{0, 0, 0, 0}, 0, 0, 0);
   const uint32_t sw[4] = {scl.x, scl.y, scl.z, scl.w};
-  float acc = 0.0f;
+  float acc = 0.0f;                            // the chain in units of 2^t
 #pragma unroll
   for (int b = 0; b < 8; ++b) {
     const int lo = d[b][0] + (int)((uint32_t)d[b][1] << 8);
     const int hi = d[b][2] + (int)((uint32_t)d[b][3] << 8);
     const double x = __builtin_fma((double)hi, 65536.0, (double)lo);   // exact: an integer below 2^53
-    const float inner = __builtin_ldexpf((float)x, t[b]);
-    acc = __fadd_rn(acc, __fmul_rn(f16_half(sw[b >> 1], b & 1), inner));
+    acc = __fadd_rn(acc, __fmul_rn(f16_half(sw[b >> 1], b & 1), (float)x));
   }
-  return acc;
-}
-
-// The same with the exponents packed as signed bytes: t[b] is byte b % 4 of tp[b / 4].
-__device__ __forceinline__ float q8_score16p(const long (&bv)[8], const uint4 &scl, const long (&a)[8],
-                                             const uint32_t (&tp)[2]) {
-  int t[8];
-#pragma unroll
-  for (int b = 0; b < 8; ++b) t[b] = __builtin_amdgcn_sbfe((int)tp[b >> 2], 8 * (b & 3), 8);
-  return q8_score16r(bv, scl, a, t);
+  return __builtin_ldexpf(acc, t);
 }
 
 // Scores of 16 keys: row is the LDS row (16 data uint4, then the scale uint4) of key lane % 16;

@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   if constexpr (KF == BKV_Q8_0) {
     int8_t *s_lim = reinterpret_cast<int8_t *>(ldx) + kResTail * kUPR * 16;
     int *s_lt = reinterpret_cast<int *>(s_lim + kLimBytes);
-    static_assert(kResTail * kUPR * 16 + kLimBytes + kGqa * 8 * 4 <= sizeof(ldx), "digits beside the tail rows");
+    static_assert(kResTail * kUPR * 16 + kLimBytes + kGqa * 4 <= sizeof(ldx), "digits beside the tail rows");
     __syncthreads();                             // s_wide cleared
     q8lim_build(qg, a.qs, s_lim, s_lt, &s_wide, tid, NT);
     __syncthreads();

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
   __shared__ unsigned s_pvctr;              // waves done reading their PV staging rows
-  __shared__ int s_lt[kGqa * 8];            // q8_0 K digits: the exponent of each (head, block)
+  __shared__ int s_lt[kGqa];                // q8_0 K digits: the exponent of each head
   __shared__ unsigned s_wide;               // the q8_0 K digits do not fit (fp64 score path)
 
   // workgroups are dealt to the 8 XCDs round-robin by index; when the grid allows, the nkv groups

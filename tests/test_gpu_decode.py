@@ -476,3 +476,40 @@ def test_q8v_scale_spread_and_peaked_scores(nfill, path):
     torch.cuda.synchronize()
     assert report("out", out.cpu().numpy(), want) <= TOL
     assert report("gated", og.cpu().numpy(), wg) <= TOL
+
+
+def spread_q(q, lead=()):
+    """q rows (heads on the second-to-last axis) whose fp16 values span many binades: head 1 holds
+    300 beside 1e-6 (digits past 31 bits: the fp64 path), head 4 a block of values near 1e-4 beside
+    a block near 40 (a wide spread that still fits), head 9 fp16 subnormals."""
+    q = q.copy()
+    q[lead + (1, 0)] = 300.0
+    q[lead + (1, 37)] = 1e-6
+    q[lead + (4, slice(0, 32))] *= 1e-4
+    q[lead + (4, slice(224, 256))] *= 40.0
+    q[lead + (9, slice(100, 110))] = 3e-7 * np.arange(1, 11, dtype=np.float32)
+    return q
+
+
+@pytest.mark.parametrize("n", [4097, 40000])
+def test_q8k_query_exponent_spread(n, path, monkeypatch):
+    """q8_0 K scores of q rows whose exponents spread over many binades (spread_q): the group past
+    the int8 digits' range takes the fp64 path, the others the matrix cores; every e, the sum and
+    the fp16 probabilities bit-exact, the output within the bar."""
+    monkeypatch.setenv("BKV_KEEP_INTERMEDIATES", "1")
+    say(f"q exponent spread n={n} path={path}")
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n, seed=21)
+    q = spread_q(qg(21, 0)[0])
+    want, _, sc, pr, p16 = host.decode(0, n, q, debug=True, nthreads=8)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    score, e, ssum, status = dev.debug_intermediates(n)
+    if score is not None:
+        assert oracle.bit_diff(score.numpy(), sc) == 0
+    e_want = np.exp((sc * np.float32(0.0625) - (sc * np.float32(0.0625)).max(axis=1, keepdims=True)).astype(np.float64)).astype(np.float32)
+    assert oracle.bit_diff(e.numpy(), e_want) == 0
+    p_gpu = (e.numpy() / ssum.numpy()[:, None]).astype(np.float32)
+    assert oracle.bit_diff(p_gpu, pr) == 0
+    assert np.array_equal(oracle.f32_to_f16(p_gpu), p16)
+    assert report("out", out.cpu().numpy(), want) <= TOL

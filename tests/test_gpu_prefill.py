@@ -256,3 +256,23 @@ def test_prefill_step_is_append_then_chunk():
         assert oracle.rel_err(og.cpu().numpy(), wg) <= TOL
         pos += c
     assert not any(same_bytes(dev, host))
+
+
+@pytest.mark.parametrize("pos0,n_q", [(1000, 40), (3000, 300)])
+def test_prefill_q8k_query_exponent_spread(pos0, n_q):
+    """q8_0 K prefill of queries whose q rows spread over many binades (every 7th query as
+    test_gpu_decode.spread_q builds it: one workgroup's group past the int8 digits' range takes the
+    fp64 path), against the oracle."""
+    from tests.test_gpu_decode import spread_q
+    say(f"prefill q exponent spread pos0={pos0} n_q={n_q}")
+    n = pos0 + n_q
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    fill(dev, host, 0, n, seed=n_q + 5)
+    q, g = qg(pos0 + 11, 0, n=n_q)
+    for i in range(0, n_q, 7):
+        q[i] = spread_q(q[i])
+    want, wg = host.prefill(0, pos0, q, g, nthreads=8)
+    out, og = dev.prefill_chunk(0, pos0, torch.from_numpy(q).cuda(), torch.from_numpy(g).cuda())
+    torch.cuda.synchronize()
+    r = max(report("prefill", out.cpu().numpy(), want), report("gated", og.cpu().numpy(), wg))
+    assert r <= TOL
