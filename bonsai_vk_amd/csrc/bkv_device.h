@@ -9,6 +9,11 @@
 
 namespace bkv {
 
+// LDS address (32-bit, LDS aperture) of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
 // ------------------------------------------------------------------ append
 // One 32-lane half wave writes one head row. q8_0: lanes 0..15 each own 16 consecutive elements
 // (half a block); the block absmax pairs lanes 2k and 2k+1. fp16: all 32 lanes own 8 elements.

@@ -26,7 +26,7 @@
 #include "bkv_device.h"
 #include "bkv_exp.h"
 #include "bkv_internal.h"
-#include "bkv_q8dot.h"
+#include "bkv_pv8.h"
 
 namespace bkv {
 
@@ -974,11 +974,12 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 // 16 queries (64 rows: query i, head h at row 4 i + h) of one KV group over one half of their key
 // tiles: p16 = f16(e / sum) from the exact kernel's e scratch and sums (the reference's P16,
 // attn_vk.h:190-200), out^T = V^T . P^T on v_mfma_f32_16x16x32_f16, wave w of 8 owning dims
-// 32 w .. + 31 (one q8_0 block). Lane l supplies A row i = l%16 of dimension tile mt as dim
-// 32 w + 2 i + mt, and keys 8(l/16) .. + 7 of each 32-key half, so one 2-byte load per key brings the
-// lane's bytes of both dimension tiles; a byte transpose in registers and the exact fp16 split of d*b
-// (hi = f16(d*b), lo = d*b - hi) form the operands, shared by the 64 rows. The two halves' partials
-// are added in a fixed order by prefill_pv_merge_kernel.
+// 32 w .. + 31 (one q8_0 block). Each 64-key tile of V goes into LDS by direct-to-LDS loads (one
+// 1 KiB block of 4 keys per load, two per wave) in the blocked layout of bkv_pv8.h; lane l then reads
+// A row i = l%16 of dimension tile mt (dim 32 w + 16 mt + i) over keys 8(l/16) .. + 7 of each 32-key
+// half with one ds_read_b64_tr_b8, and the exact fp16 split of d*b (hi = f16(d*b), lo = d*b - hi)
+// forms the operands, shared by the 64 rows. The two halves' partials are added in a fixed order by
+// prefill_pv_merge_kernel.
 template <bool PG>
 __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
   constexpr int R = 4 * kPxRows;                   // 64 rows, 4 exact-kernel workgroups' worth
@@ -1014,13 +1015,23 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NTR; ++nt) o[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
-  const int dcol = 32 * w + 2 * lr;                 // the lane's 2 dims (q8_0 block w)
+  // V tiles: three LDS buffers (tile t in buffer t % 3), each 16 blocks of 4 keys (block i at 1024 i,
+  // 16-byte chunk c of its row r at 64 (c ^ (i & 3)) + 16 r: the rows one transposed read takes
+  // spread over the banks)
+  __shared__ __attribute__((aligned(1024))) char s_v[3][16384];
+  const uint32_t vbase = __builtin_amdgcn_readfirstlane(lds_addr(s_v));
+  // the lane's read address in a tile buffer for key half ks (dim tile: XOR 64 (2 w + mt))
+  uint32_t vrd[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int j = lr >> 1, bl = 8 * ks + 2 * lq + (j >> 2);
+    vrd[ks] = (uint32_t)(1024 * bl + 16 * (j & 3) + 8 * (lane & 1) + 64 * (bl & 3));
+  }
   // (the loaded values are kept raw until the tile uses them: any arithmetic on them here would
   // make the wave wait for the loads at once)
   struct PvIn {
     float4 en[2];                                   // e of key pk, the thread's 8 rows (valid if live)
     bool live;
-    uint32_t vw[16];                                // [ks * 8 + c]: key 32 ks + 8 lq + c of the tile (2 bytes)
     uint32_t vs;                                    // the block scale of key 32 (l%16 / 8) + 8 lq + l%8
   };
   // tiles past t1 (the loop runs whole groups of three) load tile t1 - 1 again and add nothing
@@ -1031,16 +1042,23 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) in.en[i] = ld_sc4(src + 4 * i);
     in.live = pv && j < kx && tt < t1;
-#pragma unroll
-    for (int kc = 0; kc < 16; ++kc) {
-      const uint32_t key = min((uint32_t)(t * kPfTile + 32 * (kc >> 3) + 8 * lq + (kc & 7)), kend - 1);
-      const int64_t ro = slot_t<PG>(a.L, key) * a.nkv + g;
-      in.vw[kc] = *reinterpret_cast<const uint16_t *>(a.L.vd + ro * kHd + dcol);
-    }
     // one scale load per lane: lane l%16 of each 16-lane row loads key (l%16 / 8, l%8)'s, and the row
-    // shares them by DPP broadcasts in the tile (fewer loads in flight: the wait counter holds 63)
+    // shares them by DPP broadcasts in the tile
     const uint32_t skey = min((uint32_t)(t * kPfTile + 32 * (lr >> 3) + 8 * lq + (lr & 7)), kend - 1);
     in.vs = *reinterpret_cast<const uint16_t *>(a.L.vs + (slot_t<PG>(a.L, skey) * a.nkv + g) * kScaleRowBytes + 2 * w);
+  };
+  // the V rows of tile tt (clamped as above) into buffer tt % 3: wave w loads blocks 2 w, 2 w + 1
+  // (keys 4 i + lane % 4, chunk (lane / 4) ^ (i % 4) at 16 lane)
+  auto dma_tile = [&](int tt) {
+    const int t = min(tt, t1 - 1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = 2 * w + u;
+      const uint32_t key = min((uint32_t)(t * kPfTile + 4 * i + (lane & 3)), kend - 1);
+      const uint8_t *src = a.L.vd + (slot_t<PG>(a.L, key) * a.nkv + g) * kHd + 16 * ((lane >> 2) ^ (i & 3));
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                   "s"(__builtin_amdgcn_readfirstlane(vbase + 16384u * (uint32_t)(tt % 3) + 1024u * i)) : "memory", "m0");
+    }
   };
   auto tile = [&](int t, const PvIn &in) {
     char *pb = s_p[t & 1];
@@ -1056,17 +1074,25 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
     BKV_BC(0); BKV_BC(1); BKV_BC(2); BKV_BC(3); BKV_BC(4); BKV_BC(5); BKV_BC(6); BKV_BC(7);
     BKV_BC(8); BKV_BC(9); BKV_BC(10); BKV_BC(11); BKV_BC(12); BKV_BC(13); BKV_BC(14); BKV_BC(15);
 #undef BKV_BC
+    // this wave's V rows of tile t have landed when at most the loads issued after them are in
+    // flight: tile t + 1's register loads (3) and rows (2), tile t + 2's register loads (3)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    lds_barrier();                                  // the P tile and every wave's V rows of tile t
+    dma_tile(t + 2);                                // (its buffer's last readers, tile t - 1, are done)
+    const uint32_t vb = vbase + 16384u * (uint32_t)(t % 3);
     // the A operands (registers only): pair p of key half ks holds keys 2p, 2p+1
     h8 ah[2][2], al[2][2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        constexpr uint32_t kSel[2] = {0x0C040C00u, 0x0C050C01u};
+        const v2i_t bv = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) v2i_t *)(uintptr_t)((vb + vrd[ks]) ^ (uint32_t)(64 * (2 * w + mt))));
+        constexpr uint32_t kSel[4] = {0x0C010C00u, 0x0C030C02u, 0x0C050C04u, 0x0C070C06u};
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t bw = __builtin_amdgcn_perm(in.vw[8 * ks + 2 * pp + 1], in.vw[8 * ks + 2 * pp], kSel[mt]) ^ 0x64806480u;
+          const uint32_t bw = __builtin_amdgcn_perm((uint32_t)bv.y, (uint32_t)bv.x, kSel[pp]) ^ 0x64806480u;
           const h2 x = as_h2(bw) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
           h2 hi, lo;
           split_prod(x, as_h2(vsk[8 * ks + 2 * pp] | (vsk[8 * ks + 2 * pp + 1] << 16)), hi, lo);
@@ -1077,7 +1103,6 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
         al[ks][mt] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
       }
     }
-    lds_barrier();                                  // the P tile (the other buffer's readers are done)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -1091,12 +1116,15 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
       }
     }
   };
-  // three register sets, each tile's operands requested two tiles ahead (branch-free groups of
-  // three, so that the compiler's wait counting keeps the two younger tiles' loads in flight)
+  // three register sets and V buffers, each tile's operands requested two tiles ahead (branch-free
+  // groups of three, so that the compiler's wait counting keeps the two younger tiles' loads in
+  // flight); the V rows of tile t + 2 go out once every wave has passed tile t's barrier
   if (t0 < t1) {
     PvIn in[3];
     load_tile(t0, in[0]);
+    dma_tile(t0);
     load_tile(t0 + 1, in[1]);
+    dma_tile(t0 + 1);
     for (int t = t0; t < t1; t += 3) {
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
@@ -1105,8 +1133,9 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
         tile(t + u, in[u]);
       }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last rows landed before the LDS is released
   }
-  // lane l holds out^T[dim 32 w + 2 m + mt][row 16 nt + l%16] in o[mt][nt][r], m = 4(l/16) + r
+  // lane l holds out^T[dim 32 w + 16 mt + 4(l/16) + r][row 16 nt + l%16] in o[mt][nt][r]
   float *part = a.part + (size_t)half * kPxSlice * a.nh * kHd;
 #pragma unroll
   for (int nt = 0; nt < NTR; ++nt) {
@@ -1114,10 +1143,9 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
     if ((r >> 2) >= nqv) continue;
     const size_t row = (size_t)(q0 - a.q_base + (r >> 2)) * a.nh + g * kGqa + (r & 3);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int d = 32 * w + 2 * (4 * lq + rr);
-      *reinterpret_cast<float2 *>(part + row * kHd + d) = make_float2(o[0][nt][rr], o[1][nt][rr]);
-    }
+    for (int mt = 0; mt < 2; ++mt)
+      *reinterpret_cast<float4 *>(part + row * kHd + 32 * w + 16 * mt + 4 * lq) =
+          make_float4(o[mt][nt][0], o[mt][nt][1], o[mt][nt][2], o[mt][nt][3]);
   }
 }
 

@@ -59,10 +59,6 @@ __device__ __forceinline__ void group_barrier(unsigned *cnt, unsigned n, unsigne
 // Chunk ch of the K rows of this wave's keys j0 .. j0+63 (rows >= n repeat row n-1) into
 // kt[row * kUPR + col]: 16 uint4 per row (q8_0: the whole 256 B row; fp16: half a row), and for
 // q8_0 the row's 16 B of block scales at column 16. Load i reads rows 4i..4i+3, 16 lanes per row.
-// LDS address (32-bit, LDS aperture) of a __shared__ object
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
 
 // Cache slots of a workgroup's keys kb + k (0 <= k < nk). Paged: through an LDS copy of the block-
 // table entries its keys span (lut[p - pf] for page p), so that no lookup is a global load (whose
