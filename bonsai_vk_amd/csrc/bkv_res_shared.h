@@ -336,6 +336,51 @@ __device__ __forceinline__ void qk_f16_half(const uint4 *row, const float (&qv)[
   }
 }
 
+// The 4 heads' scores of one fp16 K key per lane on the fp32 matrix cores, over dims D0 .. D0 +
+// 16 NJ - 1 of its row (row: those dims' staged bytes, 16 B per 8 dims): v_mfma_f32_4x4x1f32 takes,
+// for lane l and accumulator i, A from lane 4 (l / 4) + i and B from lane l, one exact fma per step
+// (K = 1; the product of two fp16 values is exact in fp32), so with A = q16[l % 4][d] and B = the
+// lane's key at d, accumulator i runs head i's chain acc = acc + q16 * k in ascending d: the
+// reference's score, bit for bit (attn_vk.h:156-170). q16: the group's rounded q rows in LDS,
+// [head][256] fp32.
+typedef float fv4_t __attribute__((ext_vector_type(4)));
+template <int D0, int NJ>
+__device__ __forceinline__ void qk_f16_mfma(const uint4 *row, const float *q16, fv4_t &acc) {
+  const float *qh = q16 + (threadIdx.x & 3) * kHd + D0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint4 w0 = row[2 * j], w1 = row[2 * j + 1];
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float4 *q4 = reinterpret_cast<const float4 *>(qh + 16 * j);
+    float qa[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 t = q4[c];
+      qa[4 * c] = t.x; qa[4 * c + 1] = t.y; qa[4 * c + 2] = t.z; qa[4 * c + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[i], f16_to_f32((u[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu), acc, 0, 0, 0);
+  }
+}
+
+// fp16 K in quarter rows: a wave's 64 keys, quarter Q (dims 64 Q .. + 63, 128 B per key) into LDS
+// slot S of its tile region (kt: the region; slot S at 8 KiB S, key r at 128 r): 8 direct-to-LDS
+// loads, load i taking keys 8 i .. 8 i + 7 (lane: key 8 i + lane / 8, 16-byte chunk lane % 8). As
+// stage_k_wave: inline asm, the caller waits with wait_vm<N>().
+template <bool PG>
+__device__ __forceinline__ void stage_k16_quarter(uint4 *kt, const SlotMap &sm, int nkv, int g, int k0, int n, int Q,
+                                                  int S) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(kt) + 8192u * (uint32_t)S);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t sl = slot_k<PG>(sm, k0 + min(8 * i + (lane >> 3), n - 1));
+    const uint8_t *src = sm.L->kd + (sl * nkv + g) * row_bytes(BKV_F16) + 128 * Q + 16 * (lane & 7);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "s"(base + 1024u * i) : "memory", "m0");
+  }
+}
+
 // one query head's score of one fp16 K key (the tail), half row CH: as qk_row_dot, with qt[j] =
 // q16[h][16j + lane%16] for the head h of the lane's DPP row
 template <int CH>

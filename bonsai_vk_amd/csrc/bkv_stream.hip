@@ -335,9 +335,18 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
                    "s"(xbs + 1024u) : "memory", "m0");
     }
   }
-  // (fp16 K: half row ch, dims 128 ch .., of each key; column 16 an unused copy)
+  // (fp16 K: half row ch, dims 128 ch .., of each key; column 16 an unused copy. Full plans: quarter
+  // rows instead, quarters 0 and 1 here, quarters 2 and 3 once the chains have passed 0 and 1)
+  constexpr bool KQ = K16 && !SHORT;
   auto stage_tile = [&](int ch) {
-    if (t0) stage_k_wave<KF, PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), ch);
+    if (t0) {
+      if constexpr (KQ) {
+        stage_k16_quarter<PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 2 * ch, 0);
+        stage_k16_quarter<PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 2 * ch + 1, 1);
+      } else {
+        stage_k_wave<KF, PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), ch);
+      }
+    }
   };
   auto stage_tail = [&](int ch) {
     if (tr > 0) {                              // 2 rows x 17 uint4: lanes 0..33
@@ -355,30 +364,31 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   // q (and x) are read by every wave: wave 0 waits for them (the K loads it issued after them may
   // still be in flight), then the workgroup syncs once; each wave then waits for its own K rows only
   // and scores them while the other waves' tiles are still landing
-  if (wave == 0) wait_vm_n((t0 ? kUPR : 0) + (tr > 0 ? 1 : 0));
+  if (wave == 0) wait_vm_n((t0 ? (KQ ? 16 : kUPR) : 0) + (tr > 0 ? 1 : 0));
   __syncthreads();                             // s_q (and s_x) visible to every wave
   // the q8_0 K digits of the group's q rows, in the V scale rows' LDS (their loads come after the
   // scores, once every wave has read its A operands)
-  // (fp16 K: q16 in registers for the DPP chains, qv[h][j] = q16[h][16 j + lane % 16])
+  // (fp16 K: the q rows rounded to q16 in place, read from LDS by the score chains)
   int8_t *s_lim = reinterpret_cast<int8_t *>(vsc);
   static_assert(kLimBytes <= (int)sizeof(vsc), "digits in the V scale rows");
   Q8Lim qlim;
-  float qv[kGqa][K16 ? kHd / 16 : 1];
+  float *const q16 = reinterpret_cast<float *>(s_q);
   if constexpr (!K16) {
-    q8lim_build(reinterpret_cast<const float *>(s_q), kHd, s_lim, s_lt, &s_wide, tid, NT);
+    q8lim_build(q16, kHd, s_lim, s_lt, &s_wide, tid, NT);
     __syncthreads();
     q8lim_load(s_lim, s_lt, qlim);
   } else {
-    const float *qf = reinterpret_cast<const float *>(s_q) + (lane & 15);
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h)
-#pragma unroll
-      for (int j = 0; j < kHd / 16; ++j) qv[h][j] = round_f16(qf[h * kHd + 16 * j]);
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h)
-#pragma unroll
-      for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qv[h][j]));
+    for (int i = tid; i < kGqa * kHd; i += NT) q16[i] = round_f16(q16[i]);
+    __syncthreads();
   }
+  // the DPP chains' q operand (short plans and tail keys): qt[j] = q16[h][16 j + lane % 16]
+  auto load_qt = [&](int h, float (&qt)[kHd / 16]) {
+#pragma unroll
+    for (int j = 0; j < kHd / 16; ++j) qt[j] = q16[h * kHd + 16 * j + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
+    asm volatile("s_nop 4");                   // (the DPP reads of qt come from inline asm)
+  };
   const bool wide = !K16 && s_wide != 0u;
   wait_vm<0>();                                // this wave's K tile
   RTSV(0);
@@ -434,11 +444,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         // one chain per lane over both half rows: the second half is staged once every wave has
         // taken the first
         float qt[kHd / 16];
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, hg, j);
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
-        asm volatile("s_nop 4");
+        load_qt(hg, qt);
         const uint4 *row = kt + min(key, np - 1) * kUPR;
         if (16 * wave < np) qk_f16_half1<0>(row, qt, v);   // (uniform)
         __syncthreads();
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
           v = q8_score16(row, qlim);
         } else {
           float a4[kGqa];
-          q8_score_key_slow(row, reinterpret_cast<const float *>(s_q), kHd, a4);
+          q8_score_key_slow(row, q16, kHd, a4);
           v = pick4(a4, hg);
         }
       }
@@ -466,25 +472,45 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       RTSV(1);
     } else if (t0) {
       RTS(14);
-      if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 0);
+      if constexpr (!KQ)
+        if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 0);
       float acc1[kGqa];
       if constexpr (K16) {
-        // the DPP chains over half row 0, the wave's tile restaged with half row 1, the chains on
+        // the chains on the fp32 matrix cores over quarter rows 0 and 1 (slots 0, 1 of the wave's
+        // tile region); each slot is restaged with quarter 2 / 3 as soon as the chains have read it
         // (attn_vk.h:156-170: one chain per key and head in ascending d)
-#pragma unroll
-        for (int h = 0; h < kGqa; ++h) acc1[h] = 0.0f;
-        qk_f16_half<0>(kt + kl * kUPR, qv, acc1);
+        char *reg = reinterpret_cast<char *>(kt + 64 * wave * kUPR);
+        const uint4 *myrow = reinterpret_cast<const uint4 *>(reg + 128 * (lane & 63));
+        auto patch_q = [&](int Q, int S) {       // the appended K row's quarter Q over its staged copy
+          if (wave == aw && kp < NP) {
+            if (lane >= 8 * Q && lane < 8 * Q + 8)
+              reinterpret_cast<uint4 *>(reg + 8192 * S + 128 * (kp - 64 * wave))[lane - 8 * Q] = ad;
+            wave_lds_sync();
+          }
+        };
+        patch_q(0, 0);
+        patch_q(1, 1);
+        fv4_t acc = fv4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        qk_f16_mfma<0, 4>(myrow, q16, acc);
         wave_lds_sync();
-        stage_tile(1);
+        stage_k16_quarter<PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 2, 0);
+        qk_f16_mfma<64, 4>(myrow + 512, q16, acc);
+        wave_lds_sync();
+        stage_k16_quarter<PG>(kt + 64 * wave * kUPR, sm, nkv, g, 64 * wave, min(64, np - 64 * wave), 3, 1);
+        wait_vm<8>();
+        patch_q(2, 0);
+        qk_f16_mfma<128, 4>(myrow, q16, acc);
         wait_vm<0>();
-        if (wave == aw && kp < NP) patch_k(kt + kp * kUPR, 1);
-        qk_f16_half<1>(kt + kl * kUPR, qv, acc1);
+        patch_q(3, 1);
+        qk_f16_mfma<192, 4>(myrow + 512, q16, acc);
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) acc1[h] = acc[h];
       } else if (!wide) {
         // four MFMA key groups of 16 (lane: key 16 c + lane % 16, head lane / 16), then transposed
         // to one key per lane
         q8_score64(kt + 64 * wave * kUPR, kUPR, qlim, acc1);
       } else {
-        q8_score_key_slow(kt + kl * kUPR, reinterpret_cast<const float *>(s_q), kHd, acc1);
+        q8_score_key_slow(kt + kl * kUPR, q16, kHd, acc1);
       }
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
@@ -502,11 +528,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       float v[kGqa];
       if constexpr (K16) {
         float qt[kHd / 16];
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, hg, j);
-#pragma unroll
-        for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
-        asm volatile("s_nop 4");
+        load_qt(hg, qt);
         float x = 0.0f;
         qk_f16_half1<0>(row, qt, x);
         wave_lds_sync();
@@ -521,7 +543,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
 #pragma unroll
         for (int h = 0; h < kGqa; ++h) v[h] = x;
       } else {
-        q8_score_key_slow(row, reinterpret_cast<const float *>(s_q), kHd, v);
+        q8_score_key_slow(row, q16, kHd, v);
       }
       const bool tv = n16 < tr;
       if (!wide) {
