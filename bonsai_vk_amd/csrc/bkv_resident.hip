@@ -241,9 +241,12 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   uint4 *tail_t = ldx;
   if (TAIL && tn > 0 && wave == 0) stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 0);
   // q8_0 K: the digits of the group's q rows (int8 matrix cores, bkv_q8dot.h) in the exchange area
-  // past the tail rows, free until the e phase; fp16 K: q16 in registers for the DPP chains
+  // past the tail rows, free until the e phase; fp16 K: the q rows rounded to q16 for the score
+  // chains ([head][256] fp32), past the whole 64-row tile the tail's staging writes (its loads may
+  // still land while q16 is written: no barrier drains them first)
   const float *qg = a.q + (size_t)g * kGqa * a.qs;
-  float qv[kGqa][kHd / (KF == BKV_Q8_0 ? 256 : 16)];
+  float *q16 = reinterpret_cast<float *>(reinterpret_cast<char *>(ldx) + 64 * kUPR * 16);
+  static_assert(64 * kUPR * 16 + kGqa * kHd * 4 <= sizeof(ldx), "q16 beside the tail tile");
   Q8Lim qlim;
   bool wide = false;
   if constexpr (KF == BKV_Q8_0) {
@@ -256,8 +259,8 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     q8lim_load(s_lim, s_lt, qlim);
     wide = s_wide != 0u;
   } else {
-    load_q16_rows(qg, qv, a.qs);
-    asm volatile("s_nop 4");
+    for (int i = tid; i < kGqa * kHd; i += NT) q16[i] = round_f16(qg[(size_t)(i / kHd) * a.qs + i % kHd]);
+    __syncthreads();
   }
 
   // VRES: this wave's V rows 32 s + 4 wave + vkk (s < kResVTiles) and their block-pair scale words,
@@ -298,11 +301,16 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
         else
           q8_score_key_slow(kt + lane * kUPR, qg, a.qs, acc);
       } else {
-        qk_f16_half<0>(kt + lane * kUPR, qv, acc);
+        // the chains on the fp32 matrix cores (bkv_res_shared.h), half row 0, the tile restaged with
+        // half row 1
+        fv4_t a4 = fv4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        qk_f16_mfma<0, 8>(kt + lane * kUPR, q16, a4);
         wave_lds_sync();
         stage_k_wave<KF, PG>(kt, sm, nkv, g, k0, n, 1);
         wait_vm<0>();
-        qk_f16_half<1>(kt + lane * kUPR, qv, acc);
+        qk_f16_mfma<128, 8>(kt + lane * kUPR, q16, a4);
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) acc[h] = a4[h];
       }
       wave_lds_sync();
 #pragma unroll
@@ -315,9 +323,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     }
   }
   // the tail (keys NT .. nk-1, at most kResTail): wave 0, lane = 16 h + t scores key NT + t against
-  // head h, with its own head's q16 broadcast along the lane's DPP row (qv[h][j] holds q16[h][16 j +
-  // lane % 16]: the lane's row of head th); its rows were staged with the first tile, so only the V
-  // loads (issued after them) may still be in flight
+  // head h, with its own head's q16 broadcast along the lane's DPP row (fp16 K: qt[j] = q16[h][16 j +
+  // lane % 16]); its rows were staged with the first tile, so only the V loads (issued after them)
+  // may still be in flight
   const int th = lane >> 4, tt = lane & 15;
   float sct = 0.0f;
   if (TAIL && tn > 0 && wave == 0) {
@@ -336,10 +344,10 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     } else {                               // fp16 rows: the second half row follows the first
       float qt[kHd / 16];
 #pragma unroll
-      for (int j = 0; j < kHd / 16; ++j) qt[j] = pick4h(qv, th, j);
+      for (int j = 0; j < kHd / 16; ++j) qt[j] = q16[th * kHd + 16 * j + tt];
 #pragma unroll
       for (int j = 0; j < kHd / 16; ++j) asm volatile("" : "+v"(qt[j]));
-      asm volatile("s_nop 4");
+      asm volatile("s_nop 4");                 // (the DPP reads of qt come from inline asm)
       qk_f16_half1<0>(tail_t + tt * kUPR, qt, acc1);
       wave_lds_sync();
       stage_k_wave<KF, PG>(tail_t, sm, nkv, g, tb, tn, 1);
