@@ -29,8 +29,9 @@ static inline int64_t next_pow2(int64_t x) {
 }
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // the fewest keys a resident or stream workgroup takes (short contexts use fewer workgroups; at 4K
-// keys 96 ran ~1 % faster than 64 and 128, and 4 % and more faster than 80, 176, 256 and 512)
-constexpr int64_t kResMinKeysPerWg = 96;
+// keys, config 2: 128 (33 workgroups per group) 149.7-150.8 us per token, 96 150.9-152.4, 112
+// 150.9-153.6, 64 154.0-156.0, 80 159.1-164.0; more than 128 leaves the short plan)
+constexpr int64_t kResMinKeysPerWg = 128;
 
 // Partition sizes of the split path. QK: the LDS K tile of one workgroup (256 q8_0 / 128 fp16
 // keys). Probability chunks: kE2Chunk keys. PV: enough workgroups to cover the chip (512 at nkv = 4)
@@ -87,7 +88,7 @@ PrefillPlan plan_prefill(int nh, int nkv, uint32_t pos0, int n_q, size_t base) {
 // the [keys][rows] score / exp scratch; then (q8_0 V) the slice's sums and the PV kernel's partials
 static size_t prefill_exact_extra(int nh, int nkv) {
   const size_t wgs = (size_t)nkv * (kPxSlice / kPxQ);
-  return align256(wgs * kPxRows * sizeof(float)) + align256((size_t)2 * kPxSlice * nh * kHd * sizeof(float));
+  return align256(wgs * kPxRows * sizeof(float)) + align256((size_t)kPvSplit * kPxSlice * nh * kHd * sizeof(float));
 }
 size_t prefill_exact_workspace(int nh, int nkv, int64_t max_ctx, size_t base) {
   const int64_t ld = cdiv(max_ctx, kPxTile) * kPxTile + kPxTile;   // + the exp sweep's overhang

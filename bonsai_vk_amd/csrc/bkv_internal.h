@@ -163,6 +163,8 @@ constexpr int kPxQ = 4;          // queries per workgroup (x 4 heads = 16 rows)
 constexpr int kPxRows = kPxQ * kGqa;
 constexpr int kPxTile = 256;     // keys per score / exp tile (one per lane of the workgroup)
 constexpr int kPxSlice = 512;    // queries per launch (bounds the score scratch)
+constexpr int kPvQ = 32;         // exact prefill, q8_0 V: queries per PV workgroup (4 kPvQ rows)
+constexpr int kPvSplit = 4;      // ... and key ranges per query block (partials added in order)
 constexpr int kPxMinQ = 16;      // shorter chunks run as decode rows
 
 struct PrefillXArgs {
@@ -181,7 +183,7 @@ struct PrefillXArgs {
   float *out, *out_gated;
   float *sc;                     // [nkv * nqb][ld][kPxRows] scores, then exp (the slice's workgroups)
   float *sums;                   // q8_0 V: [nkv * nqb][kPxRows] the exact serial sums, for the PV kernel
-  float *part;                   // q8_0 V: [2][kPxSlice][nh][hd] the PV kernel's half-key partials
+  float *part;                   // q8_0 V: [kPvSplit][kPxSlice][nh][hd] the PV kernel's key-range partials
   unsigned *ts;                  // sweep timestamps (experiment builds), or null
 };
 hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream_t st);

@@ -982,32 +982,36 @@ __global__ __launch_bounds__(256, 2) void prefill_exact_kernel(PrefillXArgs a) {
 // prefill_pv_merge_kernel.
 template <bool PG>
 __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
-  constexpr int R = 4 * kPxRows;                   // 64 rows, 4 exact-kernel workgroups' worth
+  constexpr int R = kGqa * kPvQ;                   // rows, kPvQ / kPxQ exact-kernel workgroups' worth
   constexpr int NTR = R / 16;                      // MFMA row tiles
+  constexpr int RPW = R / 8;                       // rows per wave of the P tile
+  static_assert(RPW % 4 == 0 && kPxRows % RPW == 0 || RPW % kPxRows == 0, "a wave's rows in whole float4s");
   const int n = gridDim.x, b = blockIdx.x;
-  const int nq16 = (a.n_q + 15) / 16;
+  const int nqp = (a.n_q + kPvQ - 1) / kPvQ;
   const int wb = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
-  const int qb = wb % nq16, half = (wb / nq16) & 1, g = wb / (2 * nq16);
-  const int q0 = a.q_base + 16 * qb;               // chunk index of the first query
-  const int nqv = min(16, a.q_base + a.n_q - q0);
+  const int qb = wb % nqp, sp = (wb / nqp) % kPvSplit, g = wb / (kPvSplit * nqp);
+  const int q0 = a.q_base + kPvQ * qb;             // chunk index of the first query
+  const int nqv = min(kPvQ, a.q_base + a.n_q - q0);
   const uint32_t kend = a.pos0 + (uint32_t)(q0 + nqv);
   const int ntl = (int)((kend + kPfTile - 1) / kPfTile);
-  const int t0 = half ? ntl / 2 : 0, t1 = half ? ntl : ntl / 2;
+  const int t0 = sp * ntl / kPvSplit, t1 = (sp + 1) * ntl / kPvSplit;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lq = lane >> 4;
   __shared__ __attribute__((aligned(16))) char s_p[2][R * kPfRS];   // P tiles [row][64 keys] fp16
-  // this thread's probabilities: key pk of a tile, rows 8 w .. + 7 (of exact-kernel workgroup xq,
-  // whose scratch holds their e up to its own last key kx); the wave's sums in scalar registers
+  // this thread's probabilities: key pk of a tile, rows RPW w .. + RPW - 1 (of exact-kernel
+  // workgroup xq, whose scratch holds their e up to its own last key kx); the wave's sums in scalar
+  // registers
   const int pk = lane;
-  const int xq = min(4 * qb + (w >> 1), a.nqb - 1);
-  const bool pv = 16 * qb + 4 * (w >> 1) < a.n_q;
-  const uint32_t kx = a.pos0 + (uint32_t)min(a.q_base + 4 * (4 * qb + (w >> 1)) + kPxQ, a.q_base + a.n_q);
+  const int xr = (R / kPxRows) * qb + RPW * w / kPxRows, roff = RPW * w % kPxRows;
+  const int xq = min(xr, a.nqb - 1);
+  const bool pv = kPxQ * xr < a.n_q;
+  const uint32_t kx = a.pos0 + (uint32_t)min(a.q_base + kPxQ * xr + kPxQ, a.q_base + a.n_q);
   const size_t xw = (size_t)g * a.nqb + xq;
-  const float *esrc = a.sc + xw * a.ld * kPxRows + 8 * (w & 1);
-  float ssum[8], srcp[8];
+  const float *esrc = a.sc + xw * a.ld * kPxRows + roff;
+  float ssum[RPW], srcp[RPW];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < RPW; ++i) {
     ssum[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
-                                            __builtin_bit_cast(int, a.sums[xw * kPxRows + 8 * (w & 1) + i])));
+                                            __builtin_bit_cast(int, a.sums[xw * kPxRows + roff + i])));
     srcp[i] = 1.0f / ssum[i];
   }
   f4 o[2][NTR];
@@ -1030,7 +1034,7 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
   // (the loaded values are kept raw until the tile uses them: any arithmetic on them here would
   // make the wave wait for the loads at once)
   struct PvIn {
-    float4 en[2];                                   // e of key pk, the thread's 8 rows (valid if live)
+    float4 en[RPW / 4];                             // e of key pk, the thread's rows (valid if live)
     bool live;
     uint32_t vs;                                    // the block scale of key 32 (l%16 / 8) + 8 lq + l%8
   };
@@ -1040,7 +1044,7 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
     const uint32_t j = (uint32_t)(t * kPfTile + pk);
     const float *src = esrc + (size_t)min(j, kx - 1) * kPxRows;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) in.en[i] = ld_sc4(src + 4 * i);
+    for (int i = 0; i < RPW / 4; ++i) in.en[i] = ld_sc4(src + 4 * i);
     in.live = pv && j < kx && tt < t1;
     // one scale load per lane: lane l%16 of each 16-lane row loads key (l%16 / 8, l%8)'s, and the row
     // shares them by DPP broadcasts in the tile
@@ -1062,11 +1066,15 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
   };
   auto tile = [&](int t, const PvIn &in) {
     char *pb = s_p[t & 1];
-    const float ev[8] = {in.en[0].x, in.en[0].y, in.en[0].z, in.en[0].w, in.en[1].x, in.en[1].y, in.en[1].z, in.en[1].w};
+    float ev[RPW];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < RPW / 4; ++i) {
+      ev[4 * i] = in.en[i].x; ev[4 * i + 1] = in.en[i].y; ev[4 * i + 2] = in.en[i].z; ev[4 * i + 3] = in.en[i].w;
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
       const _Float16 h = (_Float16)div_by_sum(in.live ? ev[i] : 0.0f, ssum[i], srcp[i]);
-      *reinterpret_cast<_Float16 *>(pb + (8 * w + i) * kPfRS + 2 * pk) = h;
+      *reinterpret_cast<_Float16 *>(pb + (RPW * w + i) * kPfRS + 2 * pk) = h;
     }
     // the block scales of the lane's 16 keys: key (ks, c) from lane 8 ks + c of its row
     uint32_t vsk[16];
@@ -1075,8 +1083,11 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
     BKV_BC(8); BKV_BC(9); BKV_BC(10); BKV_BC(11); BKV_BC(12); BKV_BC(13); BKV_BC(14); BKV_BC(15);
 #undef BKV_BC
     // this wave's V rows of tile t have landed when at most the loads issued after them are in
-    // flight: tile t + 1's register loads (3) and rows (2), tile t + 2's register loads (3)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    // flight: tile t + 1's register loads (NL) and rows (2), tile t + 2's register loads (NL)
+    constexpr int NL = RPW / 4 + 1;
+    static_assert(2 * NL + 2 == 8 || 2 * NL + 2 == 12, "the wait count below");
+    if constexpr (2 * NL + 2 == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     lds_barrier();                                  // the P tile and every wave's V rows of tile t
     dma_tile(t + 2);                                // (its buffer's last readers, tile t - 1, are done)
     const uint32_t vb = vbase + 16384u * (uint32_t)(t % 3);
@@ -1136,7 +1147,7 @@ __global__ __launch_bounds__(512, 1) void prefill_pv64_kernel(PrefillXArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last rows landed before the LDS is released
   }
   // lane l holds out^T[dim 32 w + 16 mt + 4(l/16) + r][row 16 nt + l%16] in o[mt][nt][r]
-  float *part = a.part + (size_t)half * kPxSlice * a.nh * kHd;
+  float *part = a.part + (size_t)sp * kPxSlice * a.nh * kHd;
 #pragma unroll
   for (int nt = 0; nt < NTR; ++nt) {
     const int r = 16 * nt + lr;
@@ -1154,10 +1165,12 @@ __global__ __launch_bounds__(256) void prefill_pv_merge_kernel(PrefillXArgs a) {
   const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
-  const float4 *p0 = reinterpret_cast<const float4 *>(a.part);
-  const float4 *p1 = reinterpret_cast<const float4 *>(a.part + (size_t)kPxSlice * a.nh * kHd);
-  const float4 x = p0[i], y = p1[i];
-  const float4 v = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+  float4 v = reinterpret_cast<const float4 *>(a.part)[i];
+#pragma unroll
+  for (int s = 1; s < kPvSplit; ++s) {           // the key ranges in order
+    const float4 y = reinterpret_cast<const float4 *>(a.part + (size_t)s * kPxSlice * a.nh * kHd)[i];
+    v = make_float4(v.x + y.x, v.y + y.y, v.z + y.z, v.w + y.w);
+  }
   const size_t row = i / (kHd / 4), d = 4 * (i % (kHd / 4));
   const size_t grow = (size_t)a.q_base * a.nh + row;             // row of the whole chunk
   *reinterpret_cast<float4 *>(a.out + grow * kHd + d) = v;
@@ -1180,7 +1193,7 @@ hipError_t launch_prefill_exact(const PrefillXArgs &a, int kf, int vf, hipStream
     else hipLaunchKernelGGL((prefill_exact_kernel<KF_, VF_, false>), dim3(grid), dim3(256), 0, st, a);
   });
   if (vf == BKV_Q8_0) {
-    const int pgrid = a.nkv * 2 * ((a.n_q + 15) / 16);
+    const int pgrid = a.nkv * kPvSplit * ((a.n_q + kPvQ - 1) / kPvQ);
     if (pg) hipLaunchKernelGGL(prefill_pv64_kernel<true>, dim3(pgrid), dim3(512), 0, st, a);
     else hipLaunchKernelGGL(prefill_pv64_kernel<false>, dim3(pgrid), dim3(512), 0, st, a);
     const size_t n4 = (size_t)a.n_q * a.nh * (kHd / 4);
