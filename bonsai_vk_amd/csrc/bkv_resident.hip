@@ -397,9 +397,10 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   }
   block_sum4(lsum, shf4);
   if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
-  // VPF: the V requests once the statistics are out (every wave is done with its K tile: the
-  // reductions above synchronise the workgroup), so that the K stream of the later passes and the
-  // statistics do not wait behind them
+  // VPF: the first pass's V rows once the statistics are out (every wave is done with its K tile:
+  // the reductions above synchronise the workgroup), so that the K stream of the later passes and
+  // the statistics do not wait behind them. (Issued by waves kGqa.. once barrier A has passed, with
+  // the e pass's barriers LDS-only, config 4 q8_0 took 487 against 467 us per token.)
   if constexpr (VPF) {
     if (64 * wave < tpk) {
       const uint32_t region = __builtin_amdgcn_readfirstlane(lds_addr(kt));
@@ -414,15 +415,22 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
             return L.vs + (slot * nkv + g) * kScaleRowBytes;
           });
     }
-    if (NT < tpk) pv_regs(1);
-    if (tn > 0 && wave == 0)                 // the tail keys tb + 4 i + lane / 16 (wave 0)
-#pragma unroll
-      for (int i = 0; i < kResTail / 4; ++i) {
-        const int64_t slot = slot_k<PG>(sm, min(tb + 4 * i + vkk, nk - 1));
-        tl_w[i] = *reinterpret_cast<const u32x4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
-        tl_s[i] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
-      }
   }
+  // the second pass's rows and the tail's go out once the records are (after barrier A: its polls
+  // would wait behind them; after the record stores: the wait that orders the specials before the
+  // record would too)
+  auto request_later_v = [&]() {
+    if constexpr (VPF) {
+      if (NT < tpk) pv_regs(1);
+      if (tn > 0 && wave == 0)                 // the tail keys tb + 4 i + lane / 16 (wave 0)
+#pragma unroll
+        for (int i = 0; i < kResTail / 4; ++i) {
+          const int64_t slot = slot_k<PG>(sm, min(tb + 4 * i + vkk, nk - 1));
+          tl_w[i] = *reinterpret_cast<const u32x4 *>(L.vd + (slot * nkv + g) * kHd + vsub * 16);
+          tl_s[i] = *reinterpret_cast<const uint32_t *>(L.vs + (slot * nkv + g) * kScaleRowBytes + (vsub >> 2) * 4);
+        }
+    }
+  };
 
   // ---------------------------------------------------------------- barrier A: global max
   // wave h polls head h's statistics of every workgroup of the group: the global max and this
@@ -659,6 +667,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
       st_agent(trec + (h * GM + wi) * 2 + 1, w1);
     }
   }
+  request_later_v();
   RTS(3);
   // VRES: waves kGqa.. (idle through barrier B and the walk) accumulate PV over their register
   // rows with p16', and park the partial in the K tile area; after the walk they add
