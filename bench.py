@@ -169,9 +169,9 @@ def launched_kernel(cache, n):
     (None for the split path)"""
     path = cache.decode_path(n)
     if path == 3:
-        # the library's plan: 64 workgroups per KV group (256 CUs, nkv 4), at least 96 keys each;
+        # the library's plan: 64 workgroups per KV group (256 CUs, nkv 4), at least 128 keys each;
         # workgroups of at most 128 keys run the short instantiation
-        wgs = min(64, -(-n // 96))
+        wgs = min(64, -(-n // 128))
         short = -(-n // wgs) <= 128
         return f"void bkv::stream_kernel<1, false, {'true' if short else 'false'}>(bkv::ResArgs)"
     if path == 2:
