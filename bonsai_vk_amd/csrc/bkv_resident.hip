@@ -177,7 +177,9 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     wi = w / nkv;
   }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < 32) s_t2[tid] = kExp2Tab[tid];     // (read after the barriers before the e pass)
+  // the exp table: loaded here, stored to LDS once the scores are done (a wait for it here would
+  // hold the K stream back by a round trip)
+  const double t2v = tid < 32 ? kExp2Tab[tid] : 0.0;
   if (tid == 0) s_wide = 0u;                   // (read after the barrier that follows the digits)
   const int64_t kb = (int64_t)wi * a.kpw;
   const int64_t ke = min((int64_t)a.nfill, kb + (int64_t)a.kpw);
@@ -187,10 +189,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   // sync lines of group g: generation, then counters A, B, C, F of parity 0 and of parity 1
   unsigned *gs = a.sync + (size_t)g * kResGroupLines * kCounterStride;
   unsigned *err = a.sync + (size_t)nkv * kResGroupLines * kCounterStride;
-  const unsigned gen = ld_agent(gs) + 1u;
-  unsigned *cnt = gs + (1 + (gen & 1u) * 4) * kCounterStride;
-  if (wi == 0 && tid < 4) st_agent(gs + (1 + ((gen + 1u) & 1u) * 4 + tid) * kCounterStride, 0u);
-  const unsigned tag = 1u + (gen & 1u);
+  const unsigned gen0 = ld_agent(gs);          // (first used after the scores, for the same reason)
   constexpr int GM = kResMaxGroupWgs;
   unsigned long long *tstats = a.tstats + (size_t)g * kGqa * GM;        // [kGqa][GM]
   unsigned long long *trec = a.trec + (size_t)g * kGqa * GM * 2;        // [kGqa][GM][2]
@@ -383,6 +382,11 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   RTS(1);
 
   // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
+  if (tid < 32) s_t2[tid] = t2v;           // (published by the reductions' barriers)
+  const unsigned gen = gen0 + 1u;
+  unsigned *cnt = gs + (1 + (gen & 1u) * 4) * kCounterStride;
+  if (wi == 0 && tid < 4) st_agent(gs + (1 + ((gen + 1u) & 1u) * 4 + tid) * kCounterStride, 0u);
+  const unsigned tag = 1u + (gen & 1u);
   block_max4(mloc, shf4);                  // also: every wave is done with its K tile
 
   float lsum[kGqa];
