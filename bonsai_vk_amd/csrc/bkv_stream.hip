@@ -216,6 +216,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ unsigned long long s_rb[kSwBlocks];   // at-risk keys: bit k % 64 of word k / 64 (tail: word 8)
   __shared__ unsigned s_kctr;               // the K waves' spin barrier
   __shared__ unsigned s_pvctr;              // waves done reading their PV staging rows
+  __shared__ unsigned s_stg1;               // K waves done staging their round-1 PV rows
   __shared__ int s_lt[kGqa];                // q8_0 K digits: the exponent of each head
   __shared__ unsigned s_wide;               // the q8_0 K digits do not fit (fp64 score path)
 
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       st_agent(trec + (h * GM + c) * 2, 0ull);
       st_agent(trec + (h * GM + c) * 2 + 1, 0ull);
     }
-  if (tid == 0) { s_kctr = 0u; s_pvctr = 0u; s_nrisk = 0; s_wide = 0u; }
+  if (tid == 0) { s_kctr = 0u; s_pvctr = 0u; s_stg1 = 0u; s_nrisk = 0; s_wide = 0u; }
   if (tid < kSwBlocks) s_rb[tid] = 0ull;
   if (tid < kGqa) {                            // the tail block's totals when there is no tail
     s_bu[(kSwBlocks - 1) * kGqa + tid] = 0.0;
@@ -979,15 +980,15 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     const bool apw = kp >= 0 && kp < NP && wave == kp / NKW;   // the appended key is one of this wave's
     if (apw && lane == 0) vsc[vsc_row(kp)] = s_x[16];        // its scale row over the loaded one
     wave_lds_sync();
-    int sig[kGqa];
+    int sig[kGqa], ep[kGqa];
     {
       const uint32_t dm = f16_row_max(vsc[wave * 64 + (lane & (NKW - 1))]);
       const int ed = f16_exp_bound(__builtin_bit_cast(uint16_t, (_Float16)wave_max64(f16_to_f32(dm))));
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) {
         const float pb = __expf(mloc[h] - Mh[h]) * rSa[h] * 1.002f;
-        const int ep = max(-30, (int)((__float_as_uint(pb) >> 23) & 0xFFu) - 127);
-        sig[h] = min(100, 27 - ep - ed);
+        ep[h] = max(-30, (int)((__float_as_uint(pb) >> 23) & 0xFFu) - 127);
+        sig[h] = min(100, 27 - ep[h] - ed);
       }
     }
     const Pv8Sel z = pv8_sel();
@@ -996,7 +997,9 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     const int ia = lane & 3, ha = (lane & 15) >> 2, kq = lane >> 4;
     const float sga = __builtin_ldexpf(1.0f, pick4(sig, ha));
     const int lim = min(np, kw0 + NKW);
-    auto round = [&](auto rc) __attribute__((always_inline)) {
+    // round r's rows of this wave into its staging rows (the appended row over its loaded copy, the
+    // at-risk keys' rows kept for the corrections)
+    auto stage_rows = [&](auto rc) __attribute__((always_inline)) {
       constexpr int r = decltype(rc)::value;
       auto stage = [&](auto jc) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value, sl = 8 * r + j;
@@ -1023,25 +1026,43 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
         }
       }
       asm volatile("" ::: "memory");
+    };
+    // the matrix-core part of a round: keys k0 .. k0 + 31 of wave bw's keys (its scale rows, its
+    // staging rows at stgb; keys from lmb on weigh 0), scaled by sgab
+    auto comp = [&](auto fc, int bw, int k0, int lmb, float sgab, uint32_t stgb) __attribute__((always_inline)) {
       const int ka = k0 + 8 * kq + 2 * ia;
       auto pf = [&](int k) {
-        if (k >= lim) return 0.0f;
+        if (k >= lmb) return 0.0f;
         const uint2 pw = s_ps[k];
         const uint32_t w = ha < 2 ? pw.x : pw.y;
-        return f16_half(w, ha & 1) * sga;      // exact: a power of two
+        return f16_half(w, ha & 1) * sgab;     // exact: a power of two
       };
       const float pa = pf(ka), pb = pf(ka + 1);
-      const uint4 sa = vsc[wave * 64 + min(ka - kw0, NKW - 1)], sb = vsc[wave * 64 + min(ka + 1 - kw0, NKW - 1)];
+      const int kwb = NKW * bw;
+      const uint4 sa = vsc[bw * 64 + min(ka - kwb, NKW - 1)], sb = vsc[bw * 64 + min(ka + 1 - kwb, NKW - 1)];
       long A[8];
       pv8_prep(pa, pb, sa, sb, z, A);
-      pv8_round<r == 0>(stg, A, pacc);
+      pv8_round<decltype(fc)::value>(stgb, A, pacc);
       asm volatile("" ::: "memory");
-      if constexpr (r == 0) RTSV(14);
     };
+    // Waves 0..3 run round 0 only and stage round 1's rows for wave + kGqa, which runs them after its
+    // own two rounds: the K waves reach barrier B and the walk a round earlier, while waves kGqa..
+    // would idle through the walk.
     if (kw0 < np) {                            // (uniform) the wave holds keys
-      round(std::integral_constant<int, 0>{});
-      if constexpr (NR > 1)
-        if (kw0 + kPv8Rows < np) round(std::integral_constant<int, 1>{});
+      stage_rows(std::integral_constant<int, 0>{});
+      comp(std::true_type{}, wave, kw0, lim, sga, stg);
+      RTSV(14);
+      if constexpr (NR > 1) {
+        if (kw0 + kPv8Rows < np) {
+          if (kwave) {
+            wave_lds_sync();                   // round 0's staging reads are done
+            stage_rows(std::integral_constant<int, 1>{});
+          } else {
+            stage_rows(std::integral_constant<int, 1>{});
+            comp(std::false_type{}, wave, kw0 + kPv8Rows, lim, sga, stg);
+          }
+        }
+      }
       const int nsig = -pick4(sig, lane >> 4);
 #pragma unroll
       for (int t = 0; t < 16; ++t) pvp[t] = pv8_value(pacc[t], nsig);
@@ -1049,6 +1070,24 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
     } else {
 #pragma unroll
       for (int t = 0; t < 16; ++t) pvp[t] = 0.0f;
+    }
+    if (kwave) {
+      lds_arrive(&s_stg1);                     // round 1's rows staged (or none to stage)
+    } else if constexpr (NR > 1) {
+      const int bw = wave - kSwKW, kwb = NKW * bw;
+      if (kwb + kPv8Rows < np) {               // (uniform) wave bw's round 1, with its own 2^sig
+        int sig2[kGqa];
+        const uint32_t dm = f16_row_max(vsc[bw * 64 + (lane & (NKW - 1))]);
+        const int ed2 = f16_exp_bound(__builtin_bit_cast(uint16_t, (_Float16)wave_max64(f16_to_f32(dm))));
+#pragma unroll
+        for (int h = 0; h < kGqa; ++h) sig2[h] = min(100, 27 - ep[h] - ed2);
+        lds_wait(&s_stg1, kSwKW);
+        const uint32_t stgb = __builtin_amdgcn_readfirstlane(lds_addr(xb + kStg + bw * kStgW));
+        comp(std::true_type{}, bw, kwb + kPv8Rows, min(np, kwb + NKW), __builtin_ldexpf(1.0f, pick4(sig2, ha)), stgb);
+        const int nsig2 = -pick4(sig2, lane >> 4);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) pvp[t] += pv8_value(pacc[t], nsig2);
+      }
     }
     lds_arrive(&s_pvctr);                      // (waits for this wave's staging reads)
   }
