@@ -622,7 +622,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
   };
-  request_v();
+  if (kwave || SHORT) request_v();            // (waves kGqa.. of full plans: once barrier A has passed)
 
   // ---------------------------------------------------------------- barrier A: global max
   // wave h polls head h's statistics of every workgroup of the group (the V stream has landed by
@@ -656,6 +656,9 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   }
   __syncthreads();
   RTS(2);
+  // waves kGqa.. of full plans request their first V group now: their PV starts only after the e
+  // pass, and in front of the barrier-A polls the loads would hold the polls up
+  if (!kwave && !SHORT) request_v();
 
   // ---------------------------------------------------------------- e, classification, records
   // Block w = keys 64 w .. 64 w + 63 (wave w); wave 0 also the tail (block 8, lane 16 h + t: key
