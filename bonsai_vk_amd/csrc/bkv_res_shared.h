@@ -141,7 +141,9 @@ __device__ __forceinline__ int wave_scan_i32(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
   return v;
 }
-template <typename WS>
+// REG: up to 64 specials resolved, segmented and chained in registers (one per lane); otherwise
+// through the LDS scratch w.
+template <typename WS, bool REG = true>
 __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t kpw, int64_t nfill, WS &w,
                          float &s_out, bool &good_out, unsigned *tsw = nullptr) {
   const int lane = threadIdx.x & 63;
@@ -171,8 +173,42 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
   const int T = ok ? T0 : 0;
   __builtin_amdgcn_wave_barrier();
   if (tsw && lane == 0) tsw[0] = (unsigned)wall_clock64();
-  // 2. the specials, resolved to global key index, increment prefix and starting binade
-  for (int o = lane; o < T; o += 64) {
+  // the chain: per special, the sum's bits advance by du ulps and e is added in fp32; pre (lane j)
+  // keeps the bits before step j. Blocks of 16 steps, then of 4 (entries past the live ones are
+  // du 0, e 0: no change; n <= 64 and j stays a multiple of 4, so no index passes lane 63).
+  auto chain = [&](float &s, int du_l, float e_l, int n, uint32_t &pre) {
+    auto step = [&](int j) {
+      const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l, j);
+      const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), j));
+      const uint32_t bits = __float_as_uint(s);
+      pre = lane == j ? bits : pre;
+      s = __fadd_rn(__uint_as_float(bits + du), ev);
+    };
+    int j0 = 0;
+    for (; j0 + 16 <= n; j0 += 16) {
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) step(j0 + jj);
+    }
+    for (; j0 < n; j0 += 4) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) step(j0 + jj);
+    }
+  };
+  // the ulps of the segment before a special in its binade B (the sum's exponent field ck = B + 127
+  // at both ends), from the gaps in key index and increment prefix to the previous special
+  auto segment = [](long long gap, long long di, int B, int &du, int &ck) -> bool {
+    du = 0;
+    ck = -1;
+    if (gap > 1) {
+      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24))
+        return true;
+      du = (int)(di >> (B + 17));
+      ck = B + 127;
+      return false;
+    }
+    return di != 0;
+  };
+  auto resolve = [&](int o, long long &si, int &sk, float &se, int &sb) {
     int l = 0, hi = gg - 1;
     while (l < hi) {
       const int mid = (l + hi + 1) >> 1;
@@ -180,63 +216,78 @@ __device__ void walk_one(const ChunkRec &x, const Special *spec, int gg, int64_t
     }
     const Special sx = ld_spec(&spec[(size_t)l * kMaxSpecial + (o - w.wg_off[l])]);
     const int bf = (sx.meta >> 16) & 0xFF;
-    w.si[o] = w.wg_ib[l] + sx.ipre;
-    w.sk[o] = (int)(l * kpw + (sx.meta & 0xFFFF));
-    w.se[o] = sx.e;
-    w.sck[o] = bf == 255 ? w.wg_bp[l] : (bf == 0 ? kNoBinade : bf - 128);
-  }
-  __builtin_amdgcn_wave_barrier();
-  if (tsw && lane == 0) tsw[1] = (unsigned)wall_clock64();   // (instrumented builds: the wave's clocks)
-  // 3. per special: the ulps of the segment before it in its binade
-  bool bad = false;
-  for (int o = lane; o < T; o += 64) {
-    const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
-    const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
-    int du = 0, ck = -1;
-    if (gap > 1) {
-      const int B = w.sck[o];
-      if (B < -17 || B > 22 || di < 0 || (di & ((1ll << (B + 17)) - 1)) != 0 || (di >> (B + 17)) >= (1ll << 24)) {
-        bad = true;
-      } else {
-        du = (int)(di >> (B + 17));
-        ck = B + 127;
-      }
-    } else if (di != 0) {
-      bad = true;
-    }
-    w.sdu[o] = du;
-    w.sck[o] = ck;
-  }
-  ok = ok && !__any(bad);
-  const int Tc = ok ? T : 0;
-  __builtin_amdgcn_wave_barrier();
-  if (tsw && lane == 0) tsw[2] = (unsigned)wall_clock64();
-  // 4. the chain, 16 steps per unrolled block; entries past Tc are du 0, e 0 (no change)
+    si = w.wg_ib[l] + sx.ipre;
+    sk = (int)(l * kpw + (sx.meta & 0xFFFF));
+    se = sx.e;
+    sb = bf == 255 ? w.wg_bp[l] : (bf == 0 ? kNoBinade : bf - 128);
+  };
   float s = 0.0f;
-  bool bad2 = false;
-  for (int base = 0; base < Tc; base += 64) {
-    const int o = base + lane;
-    const bool inn = o < Tc;
-    const int du_l = inn ? w.sdu[o] : 0, ck_l = inn ? w.sck[o] : -1;
-    const float e_l = inn ? w.se[o] : 0.0f;
-    uint32_t pre = 0u;
-    const int n = min(64, Tc - base);
-    for (int j0 = 0; j0 < n; j0 += 16) {
-#pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int j = j0 + jj;
-        const uint32_t du = (uint32_t)__builtin_amdgcn_readlane(du_l, j);
-        const float ev = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e_l), j));
-        const uint32_t bits = __float_as_uint(s);
-        pre = lane == j ? bits : pre;
-        s = __fadd_rn(__uint_as_float(bits + du), ev);
-      }
+  bool good;
+  long long k_last = -1, i_last = 0;
+  if (REG && T <= 64) {
+    // one special per lane: resolved, segmented and chained in registers
+    long long si = 0;
+    int sk = -1, sb = kNoBinade;
+    float se = 0.0f;
+    if (lane < T) resolve(lane, si, sk, se, sb);
+    if (tsw && lane == 0) tsw[1] = (unsigned)wall_clock64();   // (instrumented builds: the wave's clocks)
+    long long psi = ((long long)__shfl_up((int)(si >> 32), 1) << 32) | (long long)(unsigned)__shfl_up((int)si, 1);
+    int psk = __shfl_up(sk, 1);
+    if (lane == 0) {
+      psi = 0;
+      psk = -1;
     }
-    if (ck_l >= 0) bad2 |= (int)(pre >> 23) != ck_l || (int)((pre + (uint32_t)du_l) >> 23) != ck_l;
+    int du = 0, ck = -1;
+    const bool bad = lane < T && segment((long long)sk - psk, si - psi, sb, du, ck);
+    ok = ok && !__any(bad);
+    const int Tc = ok ? T : 0;
+    if (tsw && lane == 0) tsw[2] = (unsigned)wall_clock64();
+    const bool inn = lane < Tc;
+    uint32_t pre = 0u;
+    chain(s, inn ? du : 0, inn ? se : 0.0f, Tc, pre);
+    const bool bad2 = inn && ck >= 0 && ((int)(pre >> 23) != ck || (int)((pre + (uint32_t)du) >> 23) != ck);
+    good = ok && !__any(bad2);
+    if (Tc > 0) {
+      k_last = __builtin_amdgcn_readlane(sk, Tc - 1);
+      i_last = ((long long)__builtin_amdgcn_readlane((int)(si >> 32), Tc - 1) << 32) |
+               (long long)(unsigned)__builtin_amdgcn_readlane((int)si, Tc - 1);
+    }
+  } else {
+    // 2. the specials, resolved to global key index, increment prefix and starting binade
+    for (int o = lane; o < T; o += 64) resolve(o, w.si[o], w.sk[o], w.se[o], w.sck[o]);
+    __builtin_amdgcn_wave_barrier();
+    if (tsw && lane == 0) tsw[1] = (unsigned)wall_clock64();
+    // 3. per special: the ulps of the segment before it in its binade
+    bool bad = false;
+    for (int o = lane; o < T; o += 64) {
+      const long long gap = (long long)w.sk[o] - (o > 0 ? w.sk[o - 1] : -1);
+      const long long di = w.si[o] - (o > 0 ? w.si[o - 1] : 0);
+      int du, ck;
+      bad = segment(gap, di, w.sck[o], du, ck) || bad;
+      w.sdu[o] = du;
+      w.sck[o] = ck;
+    }
+    ok = ok && !__any(bad);
+    const int Tc = ok ? T : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (tsw && lane == 0) tsw[2] = (unsigned)wall_clock64();
+    // 4. the chain, 64 specials per block
+    bool bad2 = false;
+    for (int base = 0; base < Tc; base += 64) {
+      const int o = base + lane;
+      const bool inn = o < Tc;
+      const int du_l = inn ? w.sdu[o] : 0, ck_l = inn ? w.sck[o] : -1;
+      uint32_t pre = 0u;
+      chain(s, du_l, inn ? w.se[o] : 0.0f, min(64, Tc - base), pre);
+      if (ck_l >= 0) bad2 |= (int)(pre >> 23) != ck_l || (int)((pre + (uint32_t)du_l) >> 23) != ck_l;
+    }
+    good = ok && !__any(bad2);
+    if (Tc > 0) {
+      k_last = w.sk[Tc - 1];
+      i_last = w.si[Tc - 1];
+    }
   }
-  bool good = ok && !__any(bad2);
   if (tsw && lane == 0) { tsw[3] = (unsigned)wall_clock64(); tsw[4] = (unsigned)T; }
-  const long long k_last = Tc > 0 ? w.sk[Tc - 1] : -1, i_last = Tc > 0 ? w.si[Tc - 1] : 0;
   if (good && nfill - 1 - k_last > 0) good = advance(s, blast_last, itot - i_last);
   s_out = s;
   good_out = good;

@@ -705,7 +705,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
     const ChunkRec x = unpack_rec(v[0], v[1]);
     float sres;
     bool gres;
-    walk_one<WS>(x, a.spec + (size_t)hh * G * kMaxSpecial, G, (int64_t)a.kpw, (int64_t)a.nfill,
+    walk_one<WS, false>(x, a.spec + (size_t)hh * G * kMaxSpecial, G, (int64_t)a.kpw, (int64_t)a.nfill,
                  reinterpret_cast<WS *>(ldx)[wave], sres, gres);
     if (lane == 0) {
       s_S[wave] = sres;
