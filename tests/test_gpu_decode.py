@@ -513,3 +513,39 @@ def test_q8k_query_exponent_spread(n, path, monkeypatch):
     assert oracle.bit_diff(p_gpu, pr) == 0
     assert np.array_equal(oracle.f32_to_f16(p_gpu), p16)
     assert report("out", out.cpu().numpy(), want) <= TOL
+
+
+def test_many_specials_first_and_second_workgroup(path, monkeypatch):
+    """Keys shaped so that the exact-sum walk has more specials than the copies handed over with the
+    records cover: the first 40 keys point away from their group's queries (e ~ 1e-15: every step of
+    the running sum below 2^-17 is a special), the rest of the first workgroup's keys hold e ~ 2^-12,
+    and the second workgroup's normal keys carry the sum across several binades (one special per
+    crossing). e, the serial sum and p16 stay bit-exact, with no fallback to the serial loop on the
+    single-launch paths."""
+    monkeypatch.setenv("BKV_KEEP_INTERMEDIATES", "1")
+    n, kpw = 4097, 125                         # 33 workgroups of 125 keys per group at this context
+    dev, host = pair(1, n, BKV_Q8_0, BKV_Q8_0)
+    k, v = oracle.synth_kv(n, 4, 256, 23, 0, outliers=3)
+    q, _ = qg(23, 0)
+    qsum = q.reshape(4, 4, 256).sum(axis=1)    # [kv group][dim]: the group's four query rows
+    k[:40] = -2.0 * qsum[None]
+    k[40:kpw] = -0.3 * qsum[None] + 0.1 * k[40:kpw]
+    host.append(0, 0, k, v)
+    dev.append(0, 0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    want, _, sc, pr, p16 = host.decode(0, n, q, debug=True, nthreads=8)
+    out, _ = dev.decode(0, n, torch.from_numpy(q).cuda())
+    torch.cuda.synchronize()
+    _, e, ssum, status = dev.debug_intermediates(n)
+    x = sc * np.float32(0.0625)
+    e_want = np.exp((x - x.max(axis=1, keepdims=True)).astype(np.float64)).astype(np.float32)
+    run = np.cumsum(e_want.astype(np.float64), axis=1)
+    # what the shape promises: > 32 tiny-sum specials in workgroup 0, >= 2 binade crossings in workgroup 1
+    assert np.all(run[:, 33] < 2.0 ** -17)
+    assert np.all(np.floor(np.log2(run[:, 2 * kpw - 1])) - np.floor(np.log2(run[:, kpw - 1])) >= 2)
+    assert oracle.bit_diff(e.numpy(), e_want) == 0
+    if path != "split":                       # (the split path's larger chunks overflow their record
+        assert int(status.sum()) == 0, "the exact walk fell back to the serial loop"   # and take it)
+    p_gpu = (e.numpy() / ssum.numpy()[:, None]).astype(np.float32)
+    assert oracle.bit_diff(p_gpu, pr) == 0
+    assert np.array_equal(oracle.f32_to_f16(p_gpu), p16)
+    assert report("out", out.cpu().numpy(), want) <= TOL
