@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   __shared__ uint32_t s_tsw[kResTail * 4];  // the tail's V scale rows
   __shared__ int s_pg[kResPgMax];
   __shared__ double s_t2[32];               // 2^(j/32)
-  __shared__ float shf4[NW * kGqa];
+  __shared__ float2 s_ml[NW * kGqa];            // each wave's (max, sum of exps against it) per head
   __shared__ float s_M[kGqa], s_Sa[kGqa], s_S[kGqa];
   __shared__ double s_P0[kGqa];
   __shared__ int s_ok[kGqa];
@@ -563,29 +563,61 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   RTSC(7);
   RTS(1);
   RTSV(2);
-  // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head
-  block_max4(mloc, shf4);
-  RTSV(3);
-  float lsum[kGqa];
+  // the workgroup's (max of s*scale, sum of exp(s*scale - max)) per head, with one barrier: each
+  // wave's maximum and its sum of exps against it go to LDS; every lane takes the maximum over the
+  // waves (mloc, which the PV's scale bound reads), and the lanes that store the statistics rescale
+  // the waves' sums to it. (The sum feeds S_a and the workgroups' positions, estimates whose
+  // margins are far above the few fp32 roundings this adds; the exact sum is the walk's.)
+  {
+    float wm[kGqa];
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    float l;
-    if constexpr (SHORT) {
-      l = (16 * wave + (lane & 15) < np && h == (lane >> 4)) ? __expf(sv_short * a.scale - mloc[h]) : 0.0f;
-    } else {
-      l = (t0 && kl < np) ? __expf(sc[h] * a.scale - mloc[h]) : 0.0f;
+    for (int h = 0; h < kGqa; ++h)
+      wm[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_max_l63(mloc[h])), 63));
+    float lw[kGqa];
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      float l;
+      if constexpr (SHORT) {
+        l = (16 * wave + (lane & 15) < np && h == (lane >> 4)) ? __expf(sv_short * a.scale - wm[h]) : 0.0f;
+      } else {
+        l = (t0 && kl < np) ? __expf(sc[h] * a.scale - wm[h]) : 0.0f;
+      }
+      lw[h] = wave_sum_l63(l);
     }
-    if (wave == 0 && tt < tn && th == h) l += __expf(s_tsc[tt * kGqa + h] * a.scale - mloc[h]);
-    lsum[h] = l;
+    if (lane == 63)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) s_ml[wave * kGqa + h] = make_float2(wm[h], lw[h]);
+    __syncthreads();
+    RTSV(3);
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      float r = s_ml[h].x;
+#pragma unroll
+      for (int i = 1; i < NW; ++i) r = fmaxf(r, s_ml[i * kGqa + h].x);
+      mloc[h] = r;
+    }
+    // wave 0: the waves' sums rescaled to the maximum (lane 4 i + h: wave i < NW, head h) and the
+    // tail keys (several waves scored them: read after the barrier; lane 16 h + t), summed per head
+    if (wave == 0) {
+      const int hh = lane & 3;
+      const float M = pick4(mloc, hh);
+      const float2 x = lane < NW * kGqa ? s_ml[lane] : make_float2(-INFINITY, 0.0f);
+      float r = x.x != -INFINITY ? x.y * __expf(x.x - M) : 0.0f;
+      r += __shfl_xor(r, 4);
+      r += __shfl_xor(r, 8);
+      r += __shfl_xor(r, 16);
+      const float tx = row16_sum(tt < tn ? __expf(s_tsc[tt * kGqa + th] * a.scale - pick4(mloc, th)) : 0.0f);
+      const float L = r + __shfl(tx, 16 * hh);
+      if (lane < kGqa) st_agent(tstats + lane * GM + wi, pack_stats(M, L, tag));
+    }
+    __syncthreads();                           // the statistics go out ahead of every wave's V requests
   }
-  block_sum4(lsum, shf4);
-  if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
   RTS(9);
   // V after the statistics: the K stream (which the scores wait for) is not shared with the V
   // stream (which only the PV needs), and the statistics do not wait behind the V requests, whose
   // issue stalls a wave while its CU's memory queue is full. (Polling waves that request theirs
   // only after barrier A hold up the e pass: 288 against 280 us per token.) The digits in vsc were
-  // read before the barriers of the statistics.
+  // read before the statistics' barrier.
   // (vector types: copies of HIP's uint4 struct into LDS are memcpys, which keep the array in
   // scratch memory)
   u32x4 vd[NS];                                // slot s: row kw0 + 4 s + vkk
@@ -622,7 +654,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
       vd[s] = *reinterpret_cast<const u32x4 *>(L.vd + (sl * nkv + g) * kHd + vsub * 16);
     }
   };
-  if (kwave || SHORT) request_v();            // (waves kGqa.. of full plans: once barrier A has passed)
+  if (kwave) request_v();
 
   // ---------------------------------------------------------------- barrier A: global max
   // wave h polls head h's statistics of every workgroup of the group (the V stream has landed by
@@ -658,7 +690,7 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   RTS(2);
   // waves kGqa.. of full plans request their first V group now: their PV starts only after the e
   // pass, and in front of the barrier-A polls the loads would hold the polls up
-  if (!kwave && !SHORT) request_v();
+  if (!kwave) request_v();
 
   // ---------------------------------------------------------------- e, classification, records
   // Block w = keys 64 w .. 64 w + 63 (wave w); wave 0 also the tail (block 8, lane 16 h + t: key
