@@ -509,41 +509,6 @@ __device__ __forceinline__ float wave_sum_l63(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
   return v;
 }
-__device__ __forceinline__ void block_max4(float (&v)[kGqa], float *sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) v[h] = wave_max_l63(v[h]);
-  if (lane == 63)
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    float r = sh[h];
-#pragma unroll
-    for (int i = 1; i < kResNW; ++i) r = fmaxf(r, sh[i * kGqa + h]);
-    v[h] = r;
-  }
-  __syncthreads();
-}
-__device__ __forceinline__ void block_sum4(float (&v)[kGqa], float *sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) v[h] = wave_sum_l63(v[h]);
-  if (lane == 63)
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) sh[wave * kGqa + h] = v[h];
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    float r = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kResNW; ++i) r += sh[i * kGqa + h];
-    v[h] = r;
-  }
-  __syncthreads();
-}
-
 // qv[h][j] for a per-lane h, as masked bits (a select chain would be folded into an indexed
 // access, which moves qv to private memory)
 __device__ __forceinline__ float pick4h(const float (&qv)[kGqa][kHd / 16], int h, int j) {

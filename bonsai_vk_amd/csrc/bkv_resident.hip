@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   static_assert(kGqa * sizeof(WS) <= sizeof(ldx), "walk scratch must fit");
   static_assert(SB * sizeof(uint2) <= sizeof(ldx), "p16 buffer must fit");
   static_assert(NW * kGqa * kHd * sizeof(float) <= sizeof(lds), "PV reduction must fit");
-  __shared__ float shf4[NW * kGqa];
+  __shared__ float2 s_ml[NW * kGqa];            // each wave's (max, sum of exps against it) per head
   __shared__ float4 s_wf[NW];
   __shared__ double s_wd[NW * kGqa];
   __shared__ int s_wc[NW * kGqa];
@@ -387,20 +387,49 @@ __global__ __launch_bounds__(kResNT, 1) void resident_kernel(ResArgs a) {
   unsigned *cnt = gs + (1 + (gen & 1u) * 4) * kCounterStride;
   if (wi == 0 && tid < 4) st_agent(gs + (1 + ((gen + 1u) & 1u) * 4 + tid) * kCounterStride, 0u);
   const unsigned tag = 1u + (gen & 1u);
-  block_max4(mloc, shf4);                  // also: every wave is done with its K tile
-
-  float lsum[kGqa];
+  // Two barriers: each wave's maximum per head and its sum of exps against that maximum go to LDS;
+  // after the first barrier (also: every wave is done with its K tile) every lane takes the maximum
+  // over the waves, and wave 0 rescales the waves' sums to it (lane 4 i + h: wave i, head h); the
+  // second keeps the later loads behind the statistics' store. (The sum feeds S_a and the
+  // workgroups' positions, estimates whose margins are far above the roundings this adds; the
+  // exact sum is the walk's.)
+  {
+    float wm[kGqa], lw[kGqa];
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    float l = 0.0f;
+    for (int h = 0; h < kGqa; ++h)
+      wm[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_max_l63(mloc[h])), 63));
 #pragma unroll
-    for (int r = 0; r < MP; ++r)
-      if (r * NT + tid < tpk) l += __expf(sc[r][h] * a.scale - mloc[h]);
-    if (TAIL && wave == 0 && th == h && tt < tn) l += __expf(sct * a.scale - mloc[h]);
-    lsum[h] = l;
+    for (int h = 0; h < kGqa; ++h) {
+      float l = 0.0f;
+#pragma unroll
+      for (int r = 0; r < MP; ++r)
+        if (r * NT + tid < tpk) l += __expf(sc[r][h] * a.scale - wm[h]);
+      if (TAIL && wave == 0 && th == h && tt < tn) l += __expf(sct * a.scale - wm[h]);
+      lw[h] = wave_sum_l63(l);
+    }
+    if (lane == 63)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) s_ml[wave * kGqa + h] = make_float2(wm[h], lw[h]);
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      float r = s_ml[h].x;
+#pragma unroll
+      for (int i = 1; i < NW; ++i) r = fmaxf(r, s_ml[i * kGqa + h].x);
+      mloc[h] = r;
+    }
+    if (wave == 0) {
+      const int hh = lane & 3;
+      const float M = pick4(mloc, hh);
+      const float2 x = lane < NW * kGqa ? s_ml[lane] : make_float2(-INFINITY, 0.0f);
+      float r = x.x != -INFINITY ? x.y * __expf(x.x - M) : 0.0f;
+      r += __shfl_xor(r, 4);
+      r += __shfl_xor(r, 8);
+      r += __shfl_xor(r, 16);
+      if (lane < kGqa) st_agent(tstats + lane * GM + wi, pack_stats(M, r, tag));
+    }
+    __syncthreads();
   }
-  block_sum4(lsum, shf4);
-  if (tid < kGqa) st_agent(tstats + tid * GM + wi, pack_stats(pick4(mloc, tid), pick4(lsum, tid), tag));
   // VPF: the first pass's V rows once the statistics are out (every wave is done with its K tile:
   // the reductions above synchronise the workgroup), so that the K stream of the later passes and
   // the statistics do not wait behind them. (Issued by waves kGqa.. once barrier A has passed, with
