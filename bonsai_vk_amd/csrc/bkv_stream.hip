@@ -688,8 +688,8 @@ __global__ __launch_bounds__(kResNT, 1) void stream_kernel(ResArgs a) {
   }
   __syncthreads();
   RTS(2);
-  // waves kGqa.. of full plans request their first V group now: their PV starts only after the e
-  // pass, and in front of the barrier-A polls the loads would hold the polls up
+  // waves kGqa.. request their first V group now: their PV starts only after the e pass, and in
+  // front of the barrier-A polls the loads would hold the polls up
   if (!kwave) request_v();
 
   // ---------------------------------------------------------------- e, classification, records
